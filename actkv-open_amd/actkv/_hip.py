@@ -1,0 +1,131 @@
+"""ctypes binding of libactkv_hip.so, the gfx950 C-ABI library (include/actkv.h).
+
+torch is imported first on purpose: torch ships libamdhip64.so.7 and the library's
+dependency on that SONAME then resolves to torch's copy, so the process holds one HIP
+runtime and device pointers from torch tensors are valid in the library's kernels.
+
+There is no CPU path.  Every wrapper requires ROCm GPU tensors and raises when the
+library is missing or a tensor lives on the CPU.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libactkv_hip.so")
+
+F32, F16, BF16 = 0, 1, 2
+REDUCE_MEAN, REDUCE_MAX = 0, 1
+WS_KEEP_MASK = 0
+
+_DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+_c_i32, _c_i64, _c_p, _c_f, _c_sz = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
+
+_SIGNATURES = {
+    "actkv_error_string": (ctypes.c_char_p, [_c_i32]),
+    "actkv_version": (ctypes.c_char_p, []),
+    "actkv_action_scores": (_c_i32, [
+        _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64,            # q
+        _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64,            # kv
+        _c_i64,                                                  # num_blocks
+        _c_p, _c_i64, _c_i32,                                    # block_table, bt_sr, max_blocks
+        _c_p,                                                    # seq_used
+        _c_p, _c_i64, _c_i64, _c_i64,                            # lse
+        _c_p, _c_i64, _c_i64, _c_i64, _c_i64,                    # out, strides, width
+        _c_p, _c_p, _c_p,                                        # n_seen, n_valid, kv_len
+        _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,  # L R N Hq Hkv D bs
+        _c_f, _c_p]),
+    "actkv_copy_slots": (_c_i32, [_c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_p]),
+    "actkv_keep_mask": (_c_i32, [
+        _c_p, _c_i32, _c_i64, _c_i64, _c_i64,                    # scores
+        _c_i32, _c_i32, _c_i32,                                  # L H R
+        _c_p, _c_p, _c_p, _c_p, _c_i64,                          # seq_used budget prot_count prot_mask pm_sr
+        _c_i32,                                                  # head_reduce
+        _c_p, _c_i64, _c_p, _c_i64,                              # keep, keep_sr, bits, bits_sr
+        _c_i32, _c_i32, _c_p, _c_sz, _c_p]),                     # bs, max_seq, ws, ws_bytes, stream
+    "actkv_pack_keep": (_c_i32, [_c_p, _c_i64, _c_i32, _c_p, _c_i32, _c_p, _c_i64, _c_p, _c_i32, _c_p]),
+    "actkv_compact": (_c_i32, [
+        _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,            # kv planes sp ss row_bytes num_blocks
+        _c_p, _c_i64, _c_i32, _c_p,                              # bits bits_sr R seq_used
+        _c_p, _c_i64, _c_i32,                                    # block_table bt_sr bs
+        _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64,                # perm pin_in pin_out
+        _c_p, _c_i64, _c_p, _c_i64,                              # table_out freed
+        _c_p, _c_p, _c_i64, _c_p,                                # src_out dst_out pairs_sr counts
+        _c_i32, _c_i32, _c_i32, _c_p]),                          # do_copy max_seq max_kept stream
+    "actkv_workspace_size": (_c_sz, [_c_i32, _c_i32, _c_i32]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load the library once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python actkv-open_amd/build_lib.py` "
+                               "(the ActKV kernels have no CPU or Triton fallback)")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype, fn.argtypes = res, args
+        _lib = handle
+    return _lib
+
+
+def available() -> bool:
+    """True when the library is built and a ROCm GPU is visible."""
+    return os.path.exists(LIB_PATH) and torch.cuda.is_available()
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed: {lib().actkv_error_string(rc).decode()}")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype not in _DTYPES:
+        raise TypeError(f"unsupported dtype {dtype}: the kernels take float32, float16 or bfloat16")
+    return _DTYPES[dtype]
+
+
+def require_gpu(what: str, *tensors) -> torch.device:
+    """All tensors must live on one ROCm GPU: the kernels have no CPU path."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(f"{what} runs HIP kernels and needs tensors on a ROCm GPU, got {t.device}; "
+                               "the *_ref functions are the CPU formulations")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"{what}: tensors on different devices ({dev}, {t.device})")
+    return dev
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+_workspaces: dict = {}
+
+
+def workspace(device: torch.device, kind: int, r: int, max_seq: int) -> torch.Tensor:
+    """Cached per (device, kind) and grown on demand; the kernels need no initialised
+    contents.  Calls sharing it are ordered on the current stream."""
+    need = int(lib().actkv_workspace_size(kind, r, max_seq))
+    key = (device, kind)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(max(need, 1 << 16), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws

@@ -1,0 +1,177 @@
+"""Recovery-based attention scoring on a paged KV cache (ActKV Algorithm 3), on gfx950.
+
+Drop-in for the reference module actkv/kernels/lse_attn.py: same names, arguments, in-place
+semantics and errors.  `action_scores` runs the HIP kernels of libactkv_hip.so (bf16/fp16
+MFMA tile kernel for head_dim 128 and GQA groups of 1, 2 or 4; a VALU kernel for every other
+shape and for float32 caches).  It has no CPU path: CPU tensors raise.
+
+Layout (vLLM-style), one layer:
+    kv          [2, num_blocks, block_size, n_kv_heads, head_dim]
+    block_table [R, max_blocks] int32, logical block -> physical block
+    seq_used    [R] int32, valid tokens per request
+Output, updated in place:
+    out         [R, n_kv_heads, max_blocks * block_size] float32, running mean over action tokens
+    n_seen      [R] int32, action tokens already folded into `out` for each request
+
+Additive extensions (they reduce to the reference for one query and one layer):
+    q [R, N, Hq, D] with lse [R, N, Hq] folds N action tokens in one launch, and
+    q [L, R, N, Hq, D], kv [L, 2, NB, BS, Hkv, D], lse [L, R, N, Hq], out [L, R, Hkv, W]
+    score every layer in that same launch (n_seen counts action tokens, not layers).
+    n_valid [R] int32: request r folds only its first n_valid[r] of the N queries.
+    kv_len [R, N] int32: query n of request r sees only tokens t < kv_len[r, n] (causal
+    action region); tokens it cannot see contribute probability 0.
+
+`gather_kv`, `paged_decode_attention_ref` and `action_scores_ref` are the reference's torch
+formulations (lse_attn.py:32-78), kept so callers of the reference module find them; the
+HIP path never calls them.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _hip
+
+HAS_KERNELS = _hip.available()
+# The reference's flag for "compiled kernels are active" (tests and the bench read it).
+HAS_TRITON = HAS_KERNELS
+
+
+# ----------------------------------------------------------------------------- reference (torch)
+
+def gather_kv(kv: torch.Tensor, block_table: torch.Tensor, seq_used: int, row: int):
+    """Contiguous K, V [S, H, D] for one request (what a gather-based approach materializes).
+
+    Reference: actkv/kernels/lse_attn.py:32-39.
+    """
+    bs = kv.shape[2]
+    n_blocks = math.ceil(seq_used / bs)
+    blocks = block_table[row, :n_blocks].long()
+    k = kv[0, blocks].reshape(-1, kv.shape[3], kv.shape[4])[:seq_used]
+    v = kv[1, blocks].reshape(-1, kv.shape[3], kv.shape[4])[:seq_used]
+    return k, v
+
+
+def paged_decode_attention_ref(q, kv, block_table, seq_used, scale=None):
+    """Plain decode attention over a paged cache. Returns (out [R,Hq,D], lse [R,Hq]).
+
+    Reference: actkv/kernels/lse_attn.py:42-60 (stands in for the paged FlashAttention
+    backend whose LSE by-product Algorithm 3 consumes).
+    """
+    r_n, hq, d = q.shape
+    hkv = kv.shape[3]
+    g = hq // hkv
+    scale = scale if scale is not None else d ** -0.5
+    out = torch.empty_like(q, dtype=torch.float32)
+    lse = torch.empty(r_n, hq, dtype=torch.float32, device=q.device)
+    for r in range(r_n):
+        k, v = gather_kv(kv, block_table, int(seq_used[r]), r)
+        k = k.float().repeat_interleave(g, dim=1)
+        v = v.float().repeat_interleave(g, dim=1)
+        logits = torch.einsum("hd,shd->hs", q[r].float(), k) * scale
+        lse[r] = torch.logsumexp(logits, -1)
+        out[r] = torch.einsum("hs,shd->hd", torch.softmax(logits, -1), v)
+    return out, lse
+
+
+def action_scores_ref(q, kv, block_table, seq_used, lse, out, n_seen, scale=None):
+    """One action-query fold per request in torch. Reference: lse_attn.py:63-78."""
+    r_n, hq, d = q.shape
+    hkv = kv.shape[3]
+    g = hq // hkv
+    scale = scale if scale is not None else d ** -0.5
+    for r in range(r_n):
+        s = int(seq_used[r])
+        k, _ = gather_kv(kv, block_table, s, r)
+        k = k.float().repeat_interleave(g, dim=1)
+        logits = torch.einsum("hd,shd->hs", q[r].float(), k) * scale
+        p = torch.exp(logits - lse[r].unsqueeze(-1))
+        p = p.view(hkv, g, s).amax(1)
+        n = float(n_seen[r])
+        out[r, :, :s] += (p - out[r, :, :s]) / (n + 1.0)
+    n_seen += 1
+    return out
+
+
+# ----------------------------------------------------------------------------- HIP path
+
+def _as_i32(t: torch.Tensor, device) -> torch.Tensor:
+    if t.dtype != torch.int32 or t.device != device:
+        t = t.to(device=device, dtype=torch.int32)
+    return t
+
+
+def action_scores(q, kv, block_table, seq_used, lse, out, n_seen, scale=None, *,
+                  n_valid=None, kv_len=None):
+    """Fold the action query tokens of every request into `out` (Algorithm 3). In-place;
+    returns `out`.
+
+    q [R, Hq, D] (or [R, N, Hq, D], or [L, R, N, Hq, D]), kv [2, NB, BS, Hkv, D] (or
+    [L, 2, NB, BS, Hkv, D]), block_table [R, MB] int32, seq_used [R] int32, lse [R, Hq]
+    (or [R, N, Hq], [L, R, N, Hq]) fp32, out [R, Hkv, MB*BS] (or [L, R, Hkv, W]) fp32,
+    n_seen [R] int32 (incremented by the number of folded queries).
+
+    Reference: actkv/kernels/lse_attn.py:133-163.
+    """
+    span = block_table.shape[1] * kv.shape[-3]
+    if out.shape[-1] < span:   # the kernel would write past each row
+        raise ValueError(f"out is {out.shape[-1]} wide but the block table spans {span} slots; "
+                         "allocate it as [R, Hkv, max_blocks * block_size]")
+    dev = _hip.require_gpu("action_scores", q, kv, block_table, seq_used, lse, out, n_seen,
+                           n_valid, kv_len)
+    multi_layer = kv.dim() == 6
+    if multi_layer:
+        L, _, nb, bs, hkv, d = kv.shape
+        if q.dim() != 5 or lse.dim() != 4 or out.dim() != 4:
+            raise ValueError("a [L, 2, NB, BS, Hkv, D] cache takes q [L, R, N, Hq, D], "
+                             "lse [L, R, N, Hq] and out [L, R, Hkv, W]")
+        q5, lse4, out4 = q, lse, out
+        kv_sl = kv.stride(0)
+        kv_k = kv[:, 0]
+    else:
+        _, nb, bs, hkv, d = kv.shape
+        L = 1
+        if q.dim() == 3:        # one action token per request: the reference signature
+            q5, lse4 = q.unsqueeze(1).unsqueeze(0), lse.unsqueeze(1).unsqueeze(0)
+        elif q.dim() == 4:      # N action tokens per request
+            q5, lse4 = q.unsqueeze(0), lse.unsqueeze(0)
+        else:
+            raise ValueError(f"q must be [R, Hq, D] or [R, N, Hq, D] for a one-layer cache, got {tuple(q.shape)}")
+        out4 = out.unsqueeze(0)
+        kv_sl = 0
+        kv_k = kv[0]
+    _, r_n, n_q, hq, dq = q5.shape
+    assert hq % hkv == 0
+    assert dq == d
+    assert kv.stride(-1) == 1 and q.stride(-1) == 1
+    if lse4.dtype != torch.float32 or out4.dtype != torch.float32:
+        raise TypeError("lse and out must be float32")
+    if lse4.stride(-1) != 1 or out4.stride(-1) != 1:
+        raise ValueError("lse and out need a unit stride in their last dimension")
+    if n_seen.dtype != torch.int32:
+        raise TypeError("n_seen must be int32 (it is updated in place)")
+    if tuple(lse4.shape) != (L, r_n, n_q, hq) or tuple(out4.shape[:3]) != (L, r_n, hkv):
+        raise ValueError(f"shape mismatch: q {tuple(q.shape)}, lse {tuple(lse.shape)}, out {tuple(out.shape)}")
+    scale = scale if scale is not None else d ** -0.5
+    bt = _as_i32(block_table, dev)
+    if bt.stride(-1) != 1:
+        bt = bt.contiguous()
+    seq = _as_i32(seq_used, dev).contiguous()
+    nv = None if n_valid is None else _as_i32(n_valid, dev).contiguous()
+    kl = None if kv_len is None else _as_i32(kv_len, dev).contiguous()
+    if kl is not None and tuple(kl.shape) != (r_n, n_q):
+        raise ValueError(f"kv_len must be [R, N] = {(r_n, n_q)}")
+    lib = _hip.lib()
+    rc = lib.actkv_action_scores(
+        q5.data_ptr(), _hip.dtype_code(q5.dtype), q5.stride(0), q5.stride(1), q5.stride(2), q5.stride(3),
+        kv_k.data_ptr(), _hip.dtype_code(kv.dtype), kv_sl, kv_k.stride(-4), kv_k.stride(-3), kv_k.stride(-2),
+        nb,
+        bt.data_ptr(), bt.stride(0), bt.shape[1],
+        seq.data_ptr(),
+        lse4.data_ptr(), lse4.stride(0), lse4.stride(1), lse4.stride(2),
+        out4.data_ptr(), out4.stride(0), out4.stride(1), out4.stride(2), out4.shape[-1],
+        n_seen.data_ptr(), _hip.ptr(nv), _hip.ptr(kl),
+        L, r_n, n_q, hq, hkv, d, bs, float(scale), _hip.stream(dev))
+    _hip.check(rc, "actkv_action_scores")
+    return out

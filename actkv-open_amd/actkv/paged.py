@@ -1,0 +1,373 @@
+"""A vLLM-style paged KV cache whose eviction primitives run on gfx950 HIP kernels.
+
+    kv[layer] : [2, num_blocks, block_size, n_kv_heads, head_dim]
+
+Drop-in for the reference module actkv/paged.py (same class, attributes, methods and
+errors).  The allocator state (`free`, `tables`, `seq_used`, `pinned`) stays in host Python
+lists and dicts exactly as in the reference, so callers may read and assign it; the device
+work of `cal_attn`, `keep_mask_from_scores`, `compact` and `evict` runs in libactkv_hip.so:
+
+  cal_attn   -> actkv_action_scores  (Algorithm 3, N action tokens and L layers per launch)
+  evict      -> actkv_keep_mask      (head/layer reduction, radix top-k, keep bits)
+             -> actkv_compact        (plan + conflict-free moves + reclaim, one launch)
+
+`evict` does not synchronise the device: the kept count B is known on the host (protected
+count + budget), so the host lists are updated from host values while the kernels run.
+`compact` with a caller-supplied mask synchronises once to learn B, as the reference does.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _hip
+from .kernels.compaction import keep_words, upload_i32
+from .kernels.lse_attn import action_scores, paged_decode_attention_ref
+
+
+class OutOfBlocks(RuntimeError):
+    pass
+
+
+_REDUCE = {"mean": _hip.REDUCE_MEAN, "max": _hip.REDUCE_MAX}
+
+
+def _scores_layout(scores: torch.Tensor, seq_used: int):
+    """[..., H, W] / [H, W] / [W] -> (tensor, L, H, s_sl, s_sh) with a unit last stride."""
+    if scores.shape[-1] < seq_used:
+        raise ValueError(f"scores cover {scores.shape[-1]} tokens, seq_used is {seq_used}")
+    s = scores[..., :seq_used]
+    if s.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        s = s.float()
+    if s.stride(-1) != 1:
+        s = s.contiguous()
+    if s.dim() == 1:
+        return s, 1, 1, 0, 0
+    if s.dim() == 2:
+        return s, 1, s.shape[0], 0, s.stride(0)
+    h = s.shape[-2]
+    try:
+        s3 = s.view(-1, h, seq_used)
+    except RuntimeError:
+        s3 = s.reshape(-1, h, seq_used).contiguous()
+    return s3, s3.shape[0], h, s3.stride(0), s3.stride(1)
+
+
+def _keep_mask_launch(s, L, H, s_sl, s_sr, s_sh, R, seq_dev, budget_dev, prot_count_dev,
+                      prot_mask, pm_sr, head_reduce, block_size, max_seq, device):
+    """Run actkv_keep_mask; returns (keep [R, max_seq] bool, bits [R, words] int32)."""
+    keep = torch.empty(R, max(max_seq, 1), dtype=torch.bool, device=device)
+    nw = keep_words(max_seq, block_size)
+    bits = torch.empty(R, max(nw, 1), dtype=torch.int32, device=device)
+    ws = _hip.workspace(device, _hip.WS_KEEP_MASK, R, max_seq)
+    rc = _hip.lib().actkv_keep_mask(
+        s.data_ptr(), _hip.dtype_code(s.dtype), s_sl, s_sr, s_sh, L, H, R,
+        seq_dev.data_ptr(), budget_dev.data_ptr(), _hip.ptr(prot_count_dev), _hip.ptr(prot_mask), pm_sr,
+        _REDUCE[head_reduce], keep.data_ptr(), keep.shape[1], bits.data_ptr(), bits.shape[1],
+        block_size, max_seq, ws.data_ptr(), ws.numel(), _hip.stream(device))
+    _hip.check(rc, "actkv_keep_mask")
+    return keep, bits
+
+
+def _keep_mask_bits(scores, seq_used: int, budget: int, protected, head_reduce: str, block_size: int):
+    if head_reduce not in _REDUCE:
+        raise ValueError(head_reduce)
+    dev = _hip.require_gpu("keep_mask_from_scores", scores,
+                           protected if isinstance(protected, torch.Tensor) else None)
+    s, L, H, s_sl, s_sh = _scores_layout(scores, seq_used)
+    prot_mask = None
+    if isinstance(protected, torch.Tensor):
+        prot_mask = protected.to(device=dev, dtype=torch.bool)
+        if prot_mask.numel() < seq_used:
+            raise ValueError(f"protected mask has {prot_mask.numel()} entries, seq_used is {seq_used}")
+        prot_mask = prot_mask.reshape(-1).contiguous()
+        params = upload_i32([seq_used, budget], dev)
+        prot_count = None
+    else:
+        params = upload_i32([seq_used, budget, int(protected)], dev)
+        prot_count = params[2:3]
+    return _keep_mask_launch(s, L, H, s_sl, 0, s_sh, 1, params[0:1], params[1:2], prot_count,
+                             prot_mask, 0, head_reduce, block_size, seq_used, dev)
+
+
+def keep_mask_from_scores(scores: torch.Tensor, seq_used: int, budget: int,
+                          protected: int | torch.Tensor = 0, head_reduce: str = "mean") -> torch.Tensor:
+    """Per-token scores -> keep mask [seq_used]: the protected tokens plus the top-`budget` others.
+
+    scores: [S], [Hkv, S] or [n_layers, Hkv, S].  KV heads are reduced with `head_reduce`, then
+    layers are averaged (float32, in torch's CPU summation order, so the per-token score is
+    bit-identical to the reference's).  protected: a count of leading tokens, or a bool mask
+    [seq_used] of tokens that are always kept.  Equal scores at the top-k boundary keep the
+    lower index.
+
+    Reference: actkv/paged.py:23-46.
+    """
+    keep, _ = _keep_mask_bits(scores, seq_used, budget, protected, head_reduce, 16)
+    return keep[0, :seq_used]
+
+
+class PagedKVCache:
+    def __init__(self, num_blocks: int, block_size: int, n_kv_heads: int, head_dim: int,
+                 n_layers: int = 1, dtype=torch.float16, device="cpu"):
+        self.block_size, self.n_kv_heads, self.head_dim = block_size, n_kv_heads, head_dim
+        self.n_layers, self.num_blocks = n_layers, num_blocks
+        self.kv = torch.zeros(n_layers, 2, num_blocks, block_size, n_kv_heads, head_dim,
+                              dtype=dtype, device=device)
+        self.free: list[int] = list(range(num_blocks - 1, -1, -1))
+        self.tables: dict[int, list[int]] = {}
+        self.seq_used: dict[int, int] = {}
+        self.pinned: dict[int, torch.Tensor] = {}   # per request: which logical positions evict() protects
+        self.device = device
+        self._pin_count: dict[int, tuple] = {}      # req -> (tensor, version, count): avoids a sync
+
+    # ---------------------------------------------------------------- allocation
+    @property
+    def used_blocks(self) -> int:
+        return self.num_blocks - len(self.free)
+
+    def _ensure(self, req: int, n_tokens: int) -> None:
+        table = self.tables.setdefault(req, [])
+        self.seq_used.setdefault(req, 0)
+        need = math.ceil(n_tokens / self.block_size) - len(table)
+        if need > len(self.free):
+            raise OutOfBlocks(f"need {need} blocks, {len(self.free)} free")
+        for _ in range(need):
+            table.append(self.free.pop())
+
+    def append(self, req: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """k, v: [n_layers, n, Hkv, D] new tokens for request `req`."""
+        n = k.shape[1]
+        start = self.seq_used.get(req, 0)
+        self._ensure(req, start + n)
+        slots = self.slot_map(req, start + n)[start:]
+        flat = self.kv.view(self.n_layers, 2, -1, self.n_kv_heads, self.head_dim)
+        flat[:, 0, slots] = k.to(device=self.kv.device, dtype=self.kv.dtype)
+        flat[:, 1, slots] = v.to(device=self.kv.device, dtype=self.kv.dtype)
+        self.seq_used[req] = start + n
+
+    def release(self, req: int) -> None:
+        self.free.extend(reversed(self.tables.pop(req, [])))
+        self.seq_used.pop(req, None)
+        self.pinned.pop(req, None)
+        self._pin_count.pop(req, None)
+
+    # ---------------------------------------------------------------- views
+    def slot_map(self, req: int, n: int | None = None) -> torch.Tensor:
+        n = self.seq_used[req] if n is None else n
+        table = torch.tensor(self.tables[req], dtype=torch.long, device=self.device)
+        pos = torch.arange(n, device=self.device)
+        return table[pos // self.block_size] * self.block_size + pos % self.block_size
+
+    def block_table(self, reqs: list[int]) -> torch.Tensor:
+        mb = max(max(len(self.tables[r]) for r in reqs), 1)
+        host = torch.zeros(len(reqs), mb, dtype=torch.int32)
+        for i, r in enumerate(reqs):
+            if self.tables[r]:
+                host[i, : len(self.tables[r])] = torch.tensor(self.tables[r], dtype=torch.int32)
+        if torch.device(self.device).type == "cuda":
+            return host.pin_memory().to(self.device, non_blocking=True)
+        return host.to(self.device)
+
+    def seq_tensor(self, reqs: list[int]) -> torch.Tensor:
+        vals = [self.seq_used[r] for r in reqs]
+        if torch.device(self.device).type == "cuda":
+            return upload_i32(vals, self.device)
+        return torch.tensor(vals, dtype=torch.int32, device=self.device)
+
+    def gather(self, req: int, layer: int = 0):
+        slots = self.slot_map(req)
+        flat = self.kv[layer].view(2, -1, self.n_kv_heads, self.head_dim)
+        return flat[0, slots], flat[1, slots]
+
+    # ---------------------------------------------------------------- primitives
+    def decode_attention(self, reqs, q, layer=0, scale=None):
+        """Reference paged decode attention -> (out, lse); stands in for the paged FA backend."""
+        return paged_decode_attention_ref(q, self.kv[layer], self.block_table(reqs),
+                                          self.seq_tensor(reqs), scale)
+
+    def cal_attn(self, reqs, q, lse, out, n_seen, layer=0, scale=None, *, n_valid=None, kv_len=None):
+        """Primitive 1: AttnScore <- CalAttn(target_q, KCache) via LSE recovery (Algorithm 3).
+
+        layer=None scores every layer in one launch: q [L, R, N, Hq, D], lse [L, R, N, Hq],
+        out [L, R, Hkv, W].  Reference: actkv/paged.py:120-123.
+        """
+        kv = self.kv if layer is None else self.kv[layer]
+        return action_scores(q, kv, self.block_table(reqs), self.seq_tensor(reqs),
+                             lse, out, n_seen, scale, n_valid=n_valid, kv_len=kv_len)
+
+    def _pinned_count(self, req: int, pinned: torch.Tensor) -> int:
+        rec = self._pin_count.get(req)
+        if rec is not None and rec[0] is pinned and rec[1] == pinned._version:
+            return rec[2]
+        cnt = int(pinned.sum())
+        self._pin_count[req] = (pinned, pinned._version, cnt)
+        return cnt
+
+    def _compact_launch(self, reqs, bits, kept, pinned_in=None):
+        """One actkv_compact launch over `reqs` with packed keep bits [R, words] and host-known
+        kept counts; then the host allocator updates in request order (sequential semantics).
+        Returns perm [R, max(kept)] int64 and pinned_out [R, max(kept)] bool (or None)."""
+        dev = self.kv.device
+        bs = self.block_size
+        r_n = len(reqs)
+        seqs = [self.seq_used[r] for r in reqs]
+        ys = [math.ceil(s / bs) for s in seqs]
+        mb = max(max(ys), 1)
+        host = torch.zeros(r_n * (mb + 1), dtype=torch.int32)
+        host[:r_n] = torch.tensor(seqs, dtype=torch.int32)
+        for i, r in enumerate(reqs):
+            if ys[i]:
+                host[r_n + i * mb: r_n + i * mb + ys[i]] = torch.tensor(self.tables[r][: ys[i]], dtype=torch.int32)
+        params = host.pin_memory().to(dev, non_blocking=True)
+        seq_dev, bt_dev = params[:r_n], params[r_n:].view(r_n, mb)
+        bmax = max(max(kept), 1)
+        perm = torch.empty(r_n, bmax, dtype=torch.int64, device=dev)
+        pin_out = None if pinned_in is None else torch.empty(r_n, bmax, dtype=torch.bool, device=dev)
+        es = self.kv.element_size()
+        row = self.n_kv_heads * self.head_dim
+        flat = self.kv.view(self.n_layers * 2, -1, row)
+        rc = _hip.lib().actkv_compact(
+            flat.data_ptr(), flat.shape[0], flat.stride(0) * es, flat.stride(1) * es, row * es, self.num_blocks,
+            bits.data_ptr(), bits.stride(0), r_n, seq_dev.data_ptr(),
+            bt_dev.data_ptr(), mb, bs,
+            perm.data_ptr(), bmax, _hip.ptr(pinned_in), 0 if pinned_in is None else pinned_in.stride(0),
+            _hip.ptr(pin_out), bmax,
+            None, 0, None, 0, None, None, 0, None,
+            1, max(seqs), max(kept), _hip.stream(dev))
+        _hip.check(rc, "actkv_compact")
+        for i, r in enumerate(reqs):
+            drop = ys[i] - math.ceil(kept[i] / bs)
+            freed = self.tables[r][:drop]
+            self.tables[r] = self.tables[r][drop:]
+            self.free.extend(reversed(freed))
+            self.seq_used[r] = kept[i]
+        return perm, pin_out
+
+    def compact(self, req: int, keep_mask: torch.Tensor) -> torch.Tensor:
+        """Primitive 3: KVCache <- Compaction(KVCache, KeepMask) (Algorithm 4), all layers at once.
+
+        Returns `perm` (new logical position -> old logical position) so callers can permute
+        per-token metadata.  Freed blocks go straight back to the allocator.
+        Reference: actkv/paged.py:125-139.
+        """
+        dev = _hip.require_gpu("PagedKVCache.compact", self.kv, keep_mask)
+        n = self.seq_used[req]
+        keep = keep_mask[:n]
+        if keep.dtype != torch.bool:
+            keep = keep.bool()
+        keep = keep.contiguous()
+        seq = upload_i32([n], dev)
+        bits = torch.empty(1, max(keep_words(n, self.block_size), 1), dtype=torch.int32, device=dev)
+        kept = torch.empty(1, dtype=torch.int32, device=dev)
+        _hip.check(_hip.lib().actkv_pack_keep(keep.data_ptr(), keep.numel(), 1, seq.data_ptr(), self.block_size,
+                                              bits.data_ptr(), bits.shape[1], kept.data_ptr(), n,
+                                              _hip.stream(dev)), "actkv_pack_keep")
+        b = int(kept.item())    # the one synchronisation: B sizes perm and the host lists
+        perm, _ = self._compact_launch([req], bits, [b])
+        return perm[0, :b]
+
+    def evict(self, req: int, scores: torch.Tensor, budget: int, protected: int = 0,
+              head_reduce: str = "mean") -> torch.Tensor:
+        """Scores -> KeepMask -> Compaction: keep the protected prefix plus the top-`budget` tokens.
+
+        `protected` counts the request's first tokens (e.g. the prompt) the first time it is evicted.
+        Compaction moves them, so the cache remembers where they went and keeps protecting them.
+        Returns `perm` like compact(); a request already within budget is left untouched.
+        Reference: actkv/paged.py:141-157.
+        """
+        return self.evict_batch([req], [scores], budget, protected, head_reduce)[0]
+
+    def evict_batch(self, reqs: list[int], scores, budget, protected=0,
+                    head_reduce: str = "mean") -> list[torch.Tensor]:
+        """`evict` for several requests with one keep-mask launch and one compaction launch.
+
+        Equal to calling evict(reqs[i], scores[i], budget[i], protected[i]) in order (the free
+        list ends in the same order).  scores: a list with one [S]/[Hkv, S]/[L, Hkv, S] tensor
+        per request, or one tensor [..., R, Hkv, W] (leading dims are layers), e.g. the
+        [L, R, Hkv, W] output of a multi-layer cal_attn.  budget / protected: an int for every
+        request or one per request.
+        """
+        if head_reduce not in _REDUCE:
+            raise ValueError(head_reduce)
+        r_n = len(reqs)
+        budgets = list(budget) if isinstance(budget, (list, tuple)) else [budget] * r_n
+        prots = list(protected) if isinstance(protected, (list, tuple)) else [protected] * r_n
+        dev = self.kv.device
+        out = [None] * r_n
+        active, pinneds, kept = [], [], []
+        for i, req in enumerate(reqs):
+            n = self.seq_used[req]
+            pinned = self.pinned.get(req)
+            if pinned is None:
+                pinned = torch.arange(n, device=dev) < prots[i]
+                self._pin_count[req] = (pinned, pinned._version, min(max(int(prots[i]), 0), n))
+            cnt = self._pinned_count(req, pinned)
+            if pinned.numel() < n:                      # tokens appended since
+                pinned = torch.cat([pinned, pinned.new_zeros(n - pinned.numel())])
+                self._pin_count[req] = (pinned, pinned._version, cnt)
+            self.pinned[req] = pinned
+            if n - cnt <= budgets[i]:
+                out[i] = torch.arange(n, device=dev)
+                continue
+            active.append(i)
+            pinneds.append(pinned)
+            kept.append(cnt + max(budgets[i], 0))
+        if not active:
+            return out
+        _hip.require_gpu("PagedKVCache.evict", self.kv)
+        a_reqs = [reqs[i] for i in active]
+        seqs = [self.seq_used[r] for r in a_reqs]
+        smax = max(seqs)
+        ra = len(active)
+        # scores -> one [L, R, H, W] view
+        if isinstance(scores, torch.Tensor):
+            _hip.require_gpu("PagedKVCache.evict", scores)
+            if scores.dim() < 3:
+                raise ValueError("a scores tensor for several requests is [..., R, Hkv, W]")
+            sc = scores
+            if sc.shape[-3] != r_n:
+                raise ValueError(f"scores {tuple(scores.shape)} do not have {r_n} requests at dim -3")
+            sc = sc.reshape(-1, *sc.shape[-3:]) if sc.dim() != 4 else sc
+            sc = sc[:, active] if ra != r_n else sc
+        else:
+            per = []
+            for i in active:
+                s_i = scores[i]
+                _hip.require_gpu("PagedKVCache.evict", s_i)
+                s3, L_i, H_i, _, _ = _scores_layout(s_i, self.seq_used[reqs[i]])
+                per.append(s3.reshape(L_i, H_i, -1))
+            L0, H0 = per[0].shape[0], per[0].shape[1]
+            if any(p.shape[0] != L0 or p.shape[1] != H0 for p in per):
+                raise ValueError("every request's scores need the same layer and head counts")
+            if ra == 1:                                   # no copy: a strided view
+                sc = per[0].unsqueeze(1)
+            else:
+                sc = torch.zeros(L0, ra, H0, smax, dtype=per[0].dtype, device=dev)
+                for j, p in enumerate(per):
+                    sc[:, j, :, : p.shape[-1]] = p
+        if sc.shape[-1] < smax:
+            raise ValueError(f"scores cover {sc.shape[-1]} tokens, a request holds {smax}")
+        if sc.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            sc = sc.float()
+        if sc.stride(-1) != 1:
+            sc = sc.contiguous()
+        L, _, H, _ = sc.shape
+        if ra == 1:
+            pin_mat = pinneds[0].view(1, -1)
+        else:
+            pin_mat = torch.zeros(ra, smax, dtype=torch.bool, device=dev)
+            for j, p in enumerate(pinneds):
+                pin_mat[j, : p.numel()] = p
+        params = upload_i32(seqs + [max(budgets[i], 0) for i in active], dev)
+        _, bits = _keep_mask_launch(sc, L, H, sc.stride(0), sc.stride(1), sc.stride(2), ra,
+                                    params[:ra], params[ra:], None, pin_mat, pin_mat.stride(0),
+                                    head_reduce, self.block_size, smax, dev)
+        perm, pin_out = self._compact_launch(a_reqs, bits, kept, pin_mat)
+        for j, i in enumerate(active):
+            b = kept[j]
+            out[i] = perm[j, :b]
+            newpin = pin_out[j, :b]
+            self.pinned[reqs[i]] = newpin
+            self._pin_count[reqs[i]] = (newpin, newpin._version, self._pin_count[reqs[i]][2])
+        return out

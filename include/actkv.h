@@ -1,0 +1,194 @@
+/*
+ * actkv.h -- C ABI of the MI355X (gfx950) ActKV eviction hot path.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes,
+ * launches asynchronously on the caller's HIP stream, allocates no memory and
+ * returns an int status (ACTKV_OK or an ACTKV_ERR_* code).  Caller-owned
+ * workspaces are sized with actkv_workspace_size().  No entry point
+ * synchronises the device.
+ *
+ * Layout vocabulary (the reference's paged cache, actkv/paged.py:3, :54-55):
+ *   kv          [layers, 2, num_blocks, block_size, n_kv_heads, head_dim]
+ *   block_table [R, max_blocks] int32   logical block -> physical block
+ *   seq_used    [R] int32               valid tokens per request
+ *   scores/out  [layers, R, n_kv_heads, W] float32, W >= max_blocks*block_size
+ *
+ * Citations are path:line in the reference repository (Maurya30/actkv-open).
+ */
+#ifndef ACTKV_H_
+#define ACTKV_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------- status */
+#define ACTKV_OK 0
+#define ACTKV_ERR_INVALID_ARG 1   /* a size, stride, pointer or dtype is invalid   */
+#define ACTKV_ERR_UNSUPPORTED 2   /* valid, but outside what the kernels handle    */
+#define ACTKV_ERR_WORKSPACE 3     /* workspace missing or smaller than required    */
+#define ACTKV_ERR_LAUNCH 4        /* hipLaunchKernel / hipGetLastError failed      */
+
+/* element types */
+#define ACTKV_F32 0
+#define ACTKV_F16 1
+#define ACTKV_BF16 2
+
+/* head_reduce (actkv/paged.py:32-36) */
+#define ACTKV_REDUCE_MEAN 0
+#define ACTKV_REDUCE_MAX 1
+
+/* workspace kinds for actkv_workspace_size */
+#define ACTKV_WS_KEEP_MASK 0
+
+/* Human-readable name of a status code (static storage). */
+const char *actkv_error_string(int status);
+
+/* Library version string, e.g. "actkv-hip 0.1 gfx950". */
+const char *actkv_version(void);
+
+/*
+ * actkv_action_scores -- LSE-recovery scoring (ActKV Algorithm 3).
+ *
+ * Replaces actkv/kernels/lse_attn.py:133-163 (`action_scores`) and its
+ * Triton kernel lse_attn.py:85-130.  The reference folds ONE action query per
+ * request per call; this entry point folds N queries (and L layers) in one
+ * launch.  For every layer l, request r, KV head h and token t < seq_used[r]:
+ *
+ *   p_n[t] = max_{g<G} exp(scale * q[l,r,n,h*G+g,:] . k[l,t,h,:] - lse[l,r,n,h*G+g])
+ *   out[l,r,h,t] <- running mean of p_0..p_{nq-1} continuing from n_seen[r]
+ *                   (== the reference's nq successive folds, lse_attn.py:127-130)
+ *
+ * then n_seen[r] += nq (lse_attn.py:162).  nq = n_valid ? n_valid[r] : N.
+ * Query n of request r only sees tokens t < kv_len[r*N + n] when kv_len is
+ * non-NULL (causal action region); unseen tokens contribute 0 to the mean.
+ * Slots t >= seq_used[r] are not touched (lse_attn.py:111, :130).
+ *
+ * q     : dtype q_dtype, [L, R, N, Hq, D], strides q_sl q_sr q_sn q_sh, unit last
+ * kv    : dtype kv_dtype, K plane of layer l at kv + l*kv_sl; V plane ignored;
+ *         block stride kv_sb, slot stride kv_ss, head stride kv_sh, unit last.
+ *         num_blocks bounds every physical id read from block_table.
+ * lse   : float32 [L, R, N, Hq], strides lse_sl lse_sr lse_sn, unit last
+ * out   : float32 [L, R, Hkv, W], strides out_sl out_sr out_sh, unit last,
+ *         W >= max_blocks*block_size (checked)
+ * scale : softmax scale (the reference default is head_dim^-0.5, lse_attn.py:148)
+ */
+int actkv_action_scores(
+    const void *q, int q_dtype, int64_t q_sl, int64_t q_sr, int64_t q_sn, int64_t q_sh,
+    const void *kv, int kv_dtype, int64_t kv_sl, int64_t kv_sb, int64_t kv_ss, int64_t kv_sh,
+    int64_t num_blocks,
+    const int32_t *block_table, int64_t bt_sr, int max_blocks,
+    const int32_t *seq_used,
+    const float *lse, int64_t lse_sl, int64_t lse_sr, int64_t lse_sn,
+    float *out, int64_t out_sl, int64_t out_sr, int64_t out_sh, int64_t out_width,
+    int32_t *n_seen, const int32_t *n_valid, const int32_t *kv_len,
+    int L, int R, int N, int Hq, int Hkv, int D, int block_size,
+    float scale, void *stream);
+
+/*
+ * actkv_copy_slots -- row copies kv_flat[p, dst[i], :] = kv_flat[p, src[i], :]
+ * for every plane p < planes and pair i < n_pairs.
+ *
+ * Replaces actkv/kernels/compaction.py:96-106 (`apply_copies`) and its Triton
+ * kernel compaction.py:79-93.  src and dst are int64 slot indices; the caller
+ * guarantees src and dst are disjoint (compaction.py:13, :72-74), which makes
+ * every copy order-independent.  Strides are in BYTES (64-bit), row_bytes is
+ * the contiguous row length.  Slots must lie in [0, num_slots).
+ */
+int actkv_copy_slots(void *kv_flat, int64_t planes, int64_t stride_plane_bytes,
+                     int64_t stride_slot_bytes, int64_t row_bytes, int64_t num_slots,
+                     const int64_t *src, const int64_t *dst, int64_t n_pairs,
+                     void *stream);
+
+/*
+ * actkv_keep_mask -- scores -> keep mask (protected tokens + top-`budget` others).
+ *
+ * Replaces actkv/paged.py:23-46 (`keep_mask_from_scores`), batched over R
+ * requests.  scores is [L, R, H, W] of dtype scores_dtype with element strides
+ * s_sl s_sr s_sh and unit last stride; the reference's 1-D case is L=H=1 and
+ * the 2-D [Hkv, S] case is L=1.  Per request r with S = seq_used[r]:
+ *
+ *   s[t] = mean_l( reduce_h scores[l,r,h,t] )      reduce = mean | max
+ *
+ * with the float32 summation order of torch's CPU `mean` (a cascade of
+ * 16-row blocks; the last S%32 columns use its 4-way interleaved order) and a
+ * correctly rounded division, so s is bit-identical to the reference on the
+ * same scores.  keep = protected  OR  the k = clamp(budget[r], 0, #unprotected)
+ * largest s among unprotected tokens; among equal scores at the boundary the
+ * lower index wins.  protected is a per-request count of leading tokens
+ * (protected_count) or a bool mask (protected_mask, row stride pm_sr); exactly
+ * one of the two may be non-NULL (both NULL: nothing protected).
+ *
+ * keep (bool bytes, row stride keep_sr) receives S entries per request.
+ * keep_bits (optional, row stride bits_sr in uint32 words) receives the same
+ * mask packed LSB-first, zero-padded to a whole number of blocks of
+ * block_size tokens: the input of actkv_compact.
+ * workspace must hold actkv_workspace_size(ACTKV_WS_KEEP_MASK, R, max_seq)
+ * bytes; it needs no initialisation (the call clears what it accumulates
+ * into).  Calls that share a workspace must be stream-ordered.
+ */
+int actkv_keep_mask(const void *scores, int scores_dtype, int64_t s_sl, int64_t s_sr,
+                    int64_t s_sh, int L, int H, int R, const int32_t *seq_used,
+                    const int32_t *budget, const int32_t *protected_count,
+                    const uint8_t *protected_mask, int64_t pm_sr, int head_reduce,
+                    uint8_t *keep, int64_t keep_sr, uint32_t *keep_bits, int64_t bits_sr,
+                    int block_size, int max_seq, void *workspace, size_t workspace_bytes,
+                    void *stream);
+
+/*
+ * actkv_pack_keep -- bool keep mask [R, >=S] -> packed bits (LSB-first),
+ * zero beyond seq_used[r] up to a whole number of blocks, plus the popcount
+ * of each request's mask in kept_out[r] (optional).  Support for
+ * actkv_compact when the caller holds a bool mask (actkv/paged.py:125-132).
+ */
+int actkv_pack_keep(const uint8_t *keep, int64_t keep_sr, int R, const int32_t *seq_used,
+                    int block_size, uint32_t *keep_bits, int64_t bits_sr,
+                    int32_t *kept_out, int max_seq, void *stream);
+
+/*
+ * actkv_compact -- fused conflict-free in-place compaction (ActKV Algorithm 4)
+ * of R requests in ONE launch: plan + row moves + block reclaim.
+ *
+ * Replaces actkv/paged.py:125-139 (`PagedKVCache.compact`) together with
+ * actkv/kernels/compaction.py:44-69 (`plan_compaction`) and :96-106
+ * (`apply_copies`).  Per request r with S = seq_used[r], B = popcount of its
+ * keep bits, Y = ceil(S/bs), X = ceil(B/bs), start = (Y-X)*bs, end = start+B:
+ *   dst = non-kept logical positions in [start, end), ascending
+ *   src = kept logical positions outside [start, end), ascending
+ *   the i-th src row moves onto the i-th dst row in every one of the `planes`
+ *   planes of kv (all layers' K and V), physical slot = table[l/bs]*bs + l%bs.
+ * src and dst are disjoint, so no copy reads a row another copy writes; rows
+ * in reclaimed blocks are read within this launch and only handed out by
+ * allocations that are stream-ordered after it.
+ * Outputs (each optional, NULL to skip; row strides in elements):
+ *   perm_out   int64 [R, >=B]: new logical -> old logical (compaction.py:67-68)
+ *   pinned_in/pinned_out bool: pinned_out[r, j] = pinned_in[r, perm[j]] (paged.py:156)
+ *   table_out  int32 [R, >=X]: block_table[r, drop:drop+X] (paged.py:136)
+ *   freed_out  int32 [R, >=drop]: freed blocks in free-list push order,
+ *              i.e. block_table[r, drop-1-j] (paged.py:135-137)
+ *   src_out/dst_out int64 [R, >=M]: physical slots of the plan (compaction.py:69)
+ *   counts_out int32 [R, 4]: {B, M, drop, X}
+ * do_copy = 0 computes the plan outputs without moving rows (plan_compaction).
+ * kv strides are in BYTES; row_bytes is the contiguous row (n_kv_heads*head_dim*esize).
+ * max_kept bounds B over all requests (sizes the grid; checked in-kernel).
+ */
+int actkv_compact(void *kv, int64_t planes, int64_t stride_plane_bytes,
+                  int64_t stride_slot_bytes, int64_t row_bytes, int64_t num_blocks,
+                  const uint32_t *keep_bits, int64_t bits_sr, int R, const int32_t *seq_used,
+                  const int32_t *block_table, int64_t bt_sr, int block_size,
+                  int64_t *perm_out, int64_t perm_sr, const uint8_t *pinned_in, int64_t pin_sr,
+                  uint8_t *pinned_out, int64_t pout_sr, int32_t *table_out, int64_t tout_sr,
+                  int32_t *freed_out, int64_t freed_sr, int64_t *src_out, int64_t *dst_out,
+                  int64_t pairs_sr, int32_t *counts_out, int do_copy, int max_seq, int max_kept,
+                  void *stream);
+
+/* Bytes of caller workspace an entry point needs (kind = ACTKV_WS_*). */
+size_t actkv_workspace_size(int kind, int R, int max_seq);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ACTKV_H_ */

@@ -1,0 +1,275 @@
+"""HIP kernels vs the CPU oracle on the reference's kernel-test cases (tests/test_kernels.py of
+the reference repository), plus the bf16/fp16 MFMA shapes.  Every call goes through the C ABI
+(libactkv_hip.so) via the drop-in modules."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from actkv.kernels.compaction import apply_copies, plan_compaction
+from actkv.kernels.lse_attn import action_scores
+from actkv.paged import PagedKVCache, keep_mask_from_scores
+from oracle import reference as ref
+
+pytestmark = pytest.mark.gpu
+
+BITS = {torch.float32: np.uint32, torch.float16: np.uint16, torch.bfloat16: np.uint16}
+
+
+def _filled_cache(lens, bs=16, hkv=2, d=32, layers=1, seed=0, shuffle=True, dtype=torch.float32):
+    """Same construction as the reference fixture (tests/test_kernels.py:19-30), on the GPU."""
+    g = torch.Generator().manual_seed(seed)
+    nb = sum(math.ceil(n / bs) for n in lens) + 8
+    cache = PagedKVCache(nb, bs, hkv, d, n_layers=layers, dtype=dtype, device="cuda")
+    if shuffle:
+        cache.free = torch.randperm(nb, generator=g).tolist()
+    for r, n in enumerate(lens):
+        k = torch.randn(layers, n, hkv, d, generator=g).to(dtype)
+        v = torch.randn(layers, n, hkv, d, generator=g).to(dtype)
+        cache.append(r, k.cuda(), v.cuda())
+    return cache
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    """Raw element bits of a tensor on the host (byte-exact comparisons)."""
+    t = t.detach().cpu().contiguous()
+    return t.view({4: torch.int32, 2: torch.int16, 1: torch.uint8}[t.element_size()]).numpy()
+
+
+def _model_of(cache: PagedKVCache) -> ref.PagedCacheModel:
+    """CPU oracle model holding the same bytes and allocator state as a GPU cache."""
+    m = ref.PagedCacheModel(cache.num_blocks, cache.block_size, cache.n_kv_heads, cache.head_dim,
+                            cache.n_layers, np_dtype=_bits(cache.kv[:1, :1, :1]).dtype)
+    m.kv = _bits(cache.kv).copy()
+    m.free = list(cache.free)
+    m.tables = {r: list(t) for r, t in cache.tables.items()}
+    m.seq_used = dict(cache.seq_used)
+    return m
+
+
+def _assert_same_state(cache, model):
+    assert np.array_equal(_bits(cache.kv), model.kv), "KV bytes differ"
+    assert cache.free == model.free
+    assert cache.tables == model.tables
+    assert cache.seq_used == model.seq_used
+
+
+@pytest.mark.parametrize("lens,hq,hkv,d,bs,dtype", [
+    ([37], 4, 2, 32, 16, torch.float32),
+    ([5, 64, 100], 8, 2, 64, 16, torch.float32),
+    ([33, 17], 6, 3, 24, 8, torch.float32),        # non-power-of-two head_dim and group size
+    ([37, 300], 32, 8, 128, 16, torch.bfloat16),   # MFMA tile kernel, G = 4
+    ([130, 19], 16, 8, 128, 16, torch.float16),    # MFMA, G = 2
+    ([77], 8, 8, 128, 32, torch.bfloat16),         # MFMA, G = 1, block_size 32
+])
+def test_action_scores_matches_oracle(lens, hq, hkv, d, bs, dtype):
+    cache = _filled_cache(lens, bs=bs, hkv=hkv, d=d, dtype=dtype)
+    reqs = list(range(len(lens)))
+    bt, seq = cache.block_table(reqs), cache.seq_tensor(reqs)
+    width = bt.shape[1] * bs
+    out_k = torch.zeros(len(reqs), hkv, width, device="cuda")
+    n_k = torch.zeros(len(reqs), dtype=torch.int32, device="cuda")
+    out_o = torch.zeros(len(reqs), hkv, width)
+    n_o = torch.zeros(len(reqs), dtype=torch.int32)
+    kv0 = cache.kv[0].cpu()
+    tables = [cache.tables[r] for r in reqs]
+    g = torch.Generator().manual_seed(1)
+    for _ in range(3):  # three action tokens -> exercises the running mean
+        q = torch.randn(len(reqs), hq, d, generator=g).to(dtype)
+        lse = ref.decode_lse(q, kv0, tables, lens)
+        action_scores(q.cuda(), cache.kv[0], bt, seq, lse.cuda(), out_k, n_k)
+        ref.action_scores_fold(q, kv0, tables, lens, lse, out_o, n_o)
+    rtol = 1e-4 if dtype == torch.float32 else 1e-3
+    torch.testing.assert_close(out_k.cpu(), out_o, rtol=rtol, atol=1e-6)
+    assert torch.equal(n_k.cpu(), n_o)
+
+
+@pytest.mark.parametrize("n_q,hq,hkv,dtype", [(37, 32, 8, torch.bfloat16), (129, 32, 8, torch.bfloat16),
+                                              (40, 16, 8, torch.float16), (9, 6, 3, torch.float32)])
+def test_action_scores_n_queries_in_one_launch(n_q, hq, hkv, dtype):
+    """N action tokens folded by one call == N reference folds (additive extension)."""
+    lens = [200, 1000, 17]
+    d = 128 if dtype != torch.float32 else 24
+    cache = _filled_cache(lens, hkv=hkv, d=d, dtype=dtype, seed=3)
+    reqs = list(range(len(lens)))
+    bt, seq = cache.block_table(reqs), cache.seq_tensor(reqs)
+    width = bt.shape[1] * 16
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(len(reqs), n_q, hq, d, generator=g).to(dtype)
+    kv0 = cache.kv[0].cpu()
+    tables = [cache.tables[r] for r in reqs]
+    lse = torch.stack([ref.decode_lse(q[:, n], kv0, tables, lens) for n in range(n_q)], 1)
+    out0 = torch.rand(len(reqs), hkv, width, generator=g)
+    n0 = torch.tensor([0, 3, 1], dtype=torch.int32)
+    out_k, n_k = out0.cuda(), n0.cuda()
+    action_scores(q.cuda(), cache.kv[0], bt, seq, lse.cuda(), out_k, n_k)
+    out_o, n_o = out0.clone(), n0.clone()
+    ref.action_scores_nfold(q, kv0, tables, lens, lse, out_o, n_o)
+    rtol = 1e-4 if dtype == torch.float32 else 1e-3
+    torch.testing.assert_close(out_k.cpu(), out_o, rtol=rtol, atol=1e-6)
+    assert torch.equal(n_k.cpu(), n_o)
+
+
+def test_recovered_scores_are_probabilities():
+    cache = _filled_cache([50], hkv=1, d=16)
+    bt, seq = cache.block_table([0]), cache.seq_tensor([0])
+    q = torch.randn(1, 1, 16)
+    lse = ref.decode_lse(q, cache.kv[0].cpu(), [cache.tables[0]], [50])
+    out = torch.zeros(1, 1, bt.shape[1] * 16, device="cuda")
+    action_scores(q.cuda(), cache.kv[0], bt, seq, lse.cuda(), out, torch.zeros(1, dtype=torch.int32, device="cuda"))
+    assert abs(float(out[0, 0, :50].sum()) - 1.0) < 1e-4
+    assert float(out[0, 0, 50:].abs().sum()) == 0.0
+
+
+def test_mfma_scores_are_probabilities():
+    """Hq == Hkv (G = 1) on the bf16 MFMA path: each query's probabilities sum to 1."""
+    cache = _filled_cache([1000], hkv=8, d=128, dtype=torch.bfloat16, seed=9)
+    bt, seq = cache.block_table([0]), cache.seq_tensor([0])
+    q = torch.randn(1, 8, 128).to(torch.bfloat16)
+    lse = ref.decode_lse(q, cache.kv[0].cpu(), [cache.tables[0]], [1000])
+    out = torch.zeros(1, 8, bt.shape[1] * 16, device="cuda")
+    action_scores(q.cuda(), cache.kv[0], bt, seq, lse.cuda(), out, torch.zeros(1, dtype=torch.int32, device="cuda"))
+    sums = out[0, :, :1000].sum(-1).cpu()
+    torch.testing.assert_close(sums, torch.ones(8), rtol=0, atol=1e-4)
+    assert float(out[0, :, 1000:].abs().sum()) == 0.0
+
+
+@pytest.mark.parametrize("seq_used,budget,bs", [(100, 40, 16), (17, 10, 16), (64, 64, 16), (200, 3, 8),
+                                                (5000, 1234, 16), (33, 0, 16)])
+def test_plan_matches_oracle_and_is_conflict_free(seq_used, budget, bs):
+    g = torch.Generator().manual_seed(seq_used)
+    keep = torch.zeros(seq_used, dtype=torch.bool)
+    keep[torch.randperm(seq_used, generator=g)[:budget]] = True
+    table = torch.randperm(math.ceil(seq_used / bs) + 4, generator=g)
+    plan = plan_compaction(keep.cuda(), seq_used, table.cuda(), bs)
+    src_o, dst_o, perm_o, drop_o = ref.plan_compaction(keep.numpy(), seq_used, table.numpy(), bs)
+    assert np.array_equal(plan.src_slots.cpu().numpy(), src_o)
+    assert np.array_equal(plan.dst_slots.cpu().numpy(), dst_o)
+    assert np.array_equal(plan.perm.cpu().numpy(), perm_o)
+    assert plan.drop_blocks == drop_o
+    src, dst = set(plan.src_slots.tolist()), set(plan.dst_slots.tolist())
+    assert not (src & dst)
+    assert sorted(plan.perm.tolist()) == sorted(torch.nonzero(keep).flatten().tolist())
+    assert plan.drop_blocks == math.ceil(seq_used / bs) - math.ceil(budget / bs)
+
+
+@pytest.mark.parametrize("dtype,planes,slots,row", [(torch.float32, 4, 300, 96), (torch.bfloat16, 6, 1000, 1024),
+                                                    (torch.float16, 3, 77, 7), (torch.float32, 2, 50, 3)])
+def test_copy_kernel_matches_oracle(dtype, planes, slots, row):
+    g = torch.Generator().manual_seed(7)
+    flat = torch.randn(planes, slots, row, generator=g).to(dtype)
+    perm = torch.randperm(slots, generator=g)
+    m = slots // 3
+    src, dst = perm[:m], perm[m:2 * m]
+    a = flat.cuda()
+    apply_copies(a, src.cuda(), dst.cuda())
+    b = _bits(flat).copy()
+    ref.apply_copies(b, src.numpy(), dst.numpy())
+    assert np.array_equal(_bits(a), b)
+
+
+def test_copy_kernel_handles_offsets_past_2_to_the_31():
+    """Multi-layer caches put later planes past 2^31 elements; int32 offsets would wrap there."""
+    row = 1024
+    slots = 2**31 // row // 2 + 64                      # each plane holds just over 2^30 elements
+    flat = torch.zeros(3, slots, row, dtype=torch.float16, device="cuda")
+    src = torch.tensor([5, slots - 1], device="cuda")
+    dst = torch.tensor([7, 9], device="cuda")
+    flat[:, src] = torch.arange(1, 4, dtype=torch.float16, device="cuda").view(3, 1, 1)
+    apply_copies(flat, src, dst)
+    torch.cuda.synchronize()
+    assert torch.equal(flat[:, dst], flat[:, src])
+    del flat
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("n,budget,dtype", [(150, 60, torch.float32), (40, 39, torch.float32), (33, 16, torch.float32),
+                                            (1000, 101, torch.bfloat16), (2048, 2047, torch.float16)])
+def test_compaction_is_bit_exact_and_frees_blocks(n, budget, dtype):
+    cache = _filled_cache([n], layers=2, dtype=dtype)
+    model = _model_of(cache)
+    k_before = [cache.gather(0, layer)[0].clone() for layer in range(2)]
+    used_before = cache.used_blocks
+    keep = torch.zeros(n, dtype=torch.bool)
+    keep[torch.randperm(n, generator=torch.Generator().manual_seed(n))[:budget]] = True
+    perm = cache.compact(0, keep.cuda())
+    perm_o = model.compact(0, keep.numpy())
+    assert np.array_equal(perm.cpu().numpy(), perm_o)
+    _assert_same_state(cache, model)
+    assert cache.seq_used[0] == budget
+    for layer in range(2):
+        assert torch.equal(cache.gather(0, layer)[0], k_before[layer][perm])
+    assert used_before - cache.used_blocks == math.ceil(n / 16) - math.ceil(budget / 16)
+
+
+def test_attention_is_invariant_to_compaction_permutation():
+    cache = _filled_cache([90], hkv=2, d=32)
+    keep = torch.zeros(90, dtype=torch.bool, device="cuda")
+    keep[torch.randperm(90)[:41].cuda()] = True
+    k, v = cache.gather(0)
+    k_kept, v_kept = k[keep], v[keep]
+    q = torch.randn(1, 4, 32, device="cuda")
+    other = _filled_cache([1], hkv=2, d=32)
+    other.release(0)
+    other.append(0, k_kept.unsqueeze(0), v_kept.unsqueeze(0))
+    want, _ = other.decode_attention([0], q)
+    cache.compact(0, keep)
+    got, _ = cache.decode_attention([0], q)
+    torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-5)
+
+
+def test_evict_keeps_the_protected_prefix_and_the_top_scored_tokens():
+    cache = _filled_cache([70], hkv=2, d=16, layers=2)
+    model = _model_of(cache)
+    k_before, v_before = cache.gather(0, layer=1)
+    scores = 0.1 * torch.rand(2, 2, 70, generator=torch.Generator().manual_seed(3))
+    hot = [5, 17, 40, 69]
+    scores[..., hot] += 1.0
+    perm = cache.evict(0, scores.cuda(), budget=4, protected=3)
+    assert sorted(perm.tolist()) == [0, 1, 2, *hot]
+    k_after, v_after = cache.gather(0, layer=1)
+    assert torch.equal(k_after, k_before[perm])
+    assert torch.equal(v_after, v_before[perm])
+    assert cache.seq_used[0] == 7 and len(cache.tables[0]) == 1
+    perm_o = model.evict(0, scores, budget=4, protected=3)
+    assert np.array_equal(perm.cpu().numpy(), perm_o)
+    _assert_same_state(cache, model)
+    assert np.array_equal(cache.pinned[0].cpu().numpy(), model.pinned[0])
+
+
+def test_evict_within_budget_is_a_no_op():
+    cache = _filled_cache([20])
+    table = list(cache.tables[0])
+    assert cache.evict(0, torch.rand(2, 20, device="cuda"), budget=20).tolist() == list(range(20))
+    assert cache.tables[0] == table and cache.seq_used[0] == 20
+
+
+def test_keep_mask_reduces_heads_then_averages_layers():
+    scores = torch.zeros(2, 2, 4)
+    scores[0, 0, 1] = 1.0
+    scores[:, :, 2] = 0.3
+    assert keep_mask_from_scores(scores.cuda(), 4, budget=1).tolist() == [False, False, True, False]
+    assert keep_mask_from_scores(scores.cuda(), 4, budget=1, head_reduce="max").tolist() == [False, True, False, False]
+
+
+def test_evict_keeps_the_protected_tokens_across_repeated_evictions():
+    cache = _filled_cache([64], hkv=2, d=16)
+    model = _model_of(cache)
+    prompt = cache.gather(0)[0][:8].clone()
+    scores = torch.zeros(2, 64)
+    scores[:, 8:56] = torch.rand(2, 48, generator=torch.Generator().manual_seed(4)) + 1
+    cache.evict(0, scores.cuda(), budget=24, protected=8)
+    model.evict(0, scores, budget=24, protected=8)
+    new = torch.randn(1, 16, 2, 16, generator=torch.Generator().manual_seed(5))
+    cache.append(0, new.cuda(), new.cuda())
+    model.append(0, _bits(new), _bits(new))
+    scores = torch.zeros(2, cache.seq_used[0])
+    scores[:, -16:] = 1.0
+    perm = cache.evict(0, scores.cuda(), budget=16, protected=8)
+    perm_o = model.evict(0, scores, budget=16, protected=8)
+    k = cache.gather(0)[0]
+    assert cache.seq_used[0] == 8 + 16
+    assert all(any(torch.equal(p, row) for row in k) for p in prompt)
+    assert np.array_equal(np.sort(perm.cpu().numpy()), np.sort(perm_o))
+    _assert_same_state(cache, model)

@@ -19,6 +19,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 
 from . import _hip
@@ -28,6 +29,59 @@ from .kernels.lse_attn import action_scores, paged_decode_attention_ref
 
 class OutOfBlocks(RuntimeError):
     pass
+
+
+class _Table(list):
+    """A request's block table: a plain list of physical block ids (callers may read, copy and
+    mutate it like the reference's) that counts its own mutations and keeps an int32 mirror,
+    so the device copy of an unchanged table is reused instead of re-converted and re-sent."""
+
+    __slots__ = ("version", "_np", "_np_version")
+
+    def __init__(self, it=(), mirror=None):
+        super().__init__(it)
+        self.version = 0
+        self._np, self._np_version = mirror, 0
+
+    def as_array(self) -> np.ndarray:
+        if self._np is None or self._np_version != self.version or self._np.size != len(self):
+            self._np = np.array(self, dtype=np.int32)
+            self._np_version = self.version
+        return self._np
+
+    def extend_ids(self, ids) -> None:
+        """Append newly allocated blocks and grow the mirror instead of rebuilding it."""
+        fresh = self._np is not None and self._np_version == self.version and self._np.size == len(self)
+        super().extend(ids)
+        self.version += 1
+        if fresh:
+            self._np = np.concatenate([self._np, np.asarray(ids, dtype=np.int32)])
+            self._np_version = self.version
+
+    def tail(self, drop: int) -> "_Table":
+        """A new table holding self[drop:] (the survivors of a compaction), mirror sliced."""
+        arr = self.as_array()
+        return _Table(self[drop:], arr[drop:])
+
+
+def _mutator(name):
+    base = getattr(list, name)
+
+    def method(self, *args, **kw):
+        self.version += 1
+        return base(self, *args, **kw)
+
+    method.__name__ = name
+    return method
+
+
+for _name in ("__setitem__", "__delitem__", "__iadd__", "__imul__", "append", "extend", "insert", "pop",
+              "remove", "clear", "sort", "reverse"):
+    setattr(_Table, _name, _mutator(_name))
+
+
+def _as_i32(table) -> np.ndarray:
+    return table.as_array() if isinstance(table, _Table) else np.array(table, dtype=np.int32)
 
 
 _REDUCE = {"mean": _hip.REDUCE_MEAN, "max": _hip.REDUCE_MAX}
@@ -120,6 +174,7 @@ class PagedKVCache:
         self.pinned: dict[int, torch.Tensor] = {}   # per request: which logical positions evict() protects
         self.device = device
         self._pin_count: dict[int, tuple] = {}      # req -> (tensor, version, count): avoids a sync
+        self._dev_cache: dict = {}                  # device copies of unchanged block tables
 
     # ---------------------------------------------------------------- allocation
     @property
@@ -127,13 +182,17 @@ class PagedKVCache:
         return self.num_blocks - len(self.free)
 
     def _ensure(self, req: int, n_tokens: int) -> None:
-        table = self.tables.setdefault(req, [])
+        table = self.tables.setdefault(req, _Table())
         self.seq_used.setdefault(req, 0)
         need = math.ceil(n_tokens / self.block_size) - len(table)
         if need > len(self.free):
             raise OutOfBlocks(f"need {need} blocks, {len(self.free)} free")
-        for _ in range(need):
-            table.append(self.free.pop())
+        if need > 0:
+            ids = [self.free.pop() for _ in range(need)]
+            if isinstance(table, _Table):
+                table.extend_ids(ids)
+            else:
+                table.extend(ids)
 
     def append(self, req: int, k: torch.Tensor, v: torch.Tensor) -> None:
         """k, v: [n_layers, n, Hkv, D] new tokens for request `req`."""
@@ -159,21 +218,54 @@ class PagedKVCache:
         pos = torch.arange(n, device=self.device)
         return table[pos // self.block_size] * self.block_size + pos % self.block_size
 
+    def _host_tables(self, reqs, ys=None):
+        """[len(reqs) + R*MB] int32 host array: seq_used values, then the block tables (first
+        ys[i] entries of each, zero padded to MB columns)."""
+        tabs = [_as_i32(self.tables[r]) for r in reqs]
+        if ys is None:
+            ys = [t.size for t in tabs]
+        mb = max(max(ys), 1)
+        r_n = len(reqs)
+        host = np.zeros(r_n + r_n * mb, dtype=np.int32)
+        host[:r_n] = [self.seq_used[r] for r in reqs]
+        grid = host[r_n:].reshape(r_n, mb)
+        for i, t in enumerate(tabs):
+            grid[i, : ys[i]] = t[: ys[i]]
+        return host, mb
+
+    def _upload(self, host: np.ndarray) -> torch.Tensor:
+        if torch.device(self.device).type != "cuda":
+            return torch.from_numpy(host.copy()).to(self.device)
+        pinned = torch.empty(host.size, dtype=torch.int32, pin_memory=True)
+        pinned.numpy()[:] = host
+        return pinned.to(self.device, non_blocking=True)
+
+    def _device_tables(self, reqs, ys=None):
+        """(seq_used [R], block_table [R, MB]) int32 on the device, reused while the requests'
+        tables and lengths are unchanged (the device copy is never handed to callers)."""
+        key = tuple(reqs), tuple(ys) if ys is not None else None
+        tabs = tuple(self.tables[r] for r in reqs)
+        stamp = tuple((getattr(t, "version", None), len(t), self.seq_used[r]) for t, r in zip(tabs, reqs))
+        hit = self._dev_cache.get(key)
+        # the entry holds the table objects themselves: identity, not id(), decides a hit
+        if (hit is not None and hit[1] == stamp and all(isinstance(t, _Table) for t in tabs)
+                and all(a is b for a, b in zip(hit[0], tabs))):
+            return hit[2], hit[3]
+        host, mb = self._host_tables(reqs, ys)
+        dev = self._upload(host)
+        r_n = len(reqs)
+        seq, bt = dev[:r_n], dev[r_n:].view(r_n, mb)
+        if len(self._dev_cache) > 64:
+            self._dev_cache.clear()
+        self._dev_cache[key] = (tabs, stamp, seq, bt)
+        return seq, bt
+
     def block_table(self, reqs: list[int]) -> torch.Tensor:
-        mb = max(max(len(self.tables[r]) for r in reqs), 1)
-        host = torch.zeros(len(reqs), mb, dtype=torch.int32)
-        for i, r in enumerate(reqs):
-            if self.tables[r]:
-                host[i, : len(self.tables[r])] = torch.tensor(self.tables[r], dtype=torch.int32)
-        if torch.device(self.device).type == "cuda":
-            return host.pin_memory().to(self.device, non_blocking=True)
-        return host.to(self.device)
+        host, mb = self._host_tables(reqs)
+        return self._upload(host[len(reqs):]).view(len(reqs), mb)
 
     def seq_tensor(self, reqs: list[int]) -> torch.Tensor:
-        vals = [self.seq_used[r] for r in reqs]
-        if torch.device(self.device).type == "cuda":
-            return upload_i32(vals, self.device)
-        return torch.tensor(vals, dtype=torch.int32, device=self.device)
+        return self._upload(np.array([self.seq_used[r] for r in reqs], dtype=np.int32))
 
     def gather(self, req: int, layer: int = 0):
         slots = self.slot_map(req)
@@ -193,8 +285,8 @@ class PagedKVCache:
         out [L, R, Hkv, W].  Reference: actkv/paged.py:120-123.
         """
         kv = self.kv if layer is None else self.kv[layer]
-        return action_scores(q, kv, self.block_table(reqs), self.seq_tensor(reqs),
-                             lse, out, n_seen, scale, n_valid=n_valid, kv_len=kv_len)
+        seq, bt = self._device_tables(reqs)
+        return action_scores(q, kv, bt, seq, lse, out, n_seen, scale, n_valid=n_valid, kv_len=kv_len)
 
     def _pinned_count(self, req: int, pinned: torch.Tensor) -> int:
         rec = self._pin_count.get(req)
@@ -213,14 +305,8 @@ class PagedKVCache:
         r_n = len(reqs)
         seqs = [self.seq_used[r] for r in reqs]
         ys = [math.ceil(s / bs) for s in seqs]
-        mb = max(max(ys), 1)
-        host = torch.zeros(r_n * (mb + 1), dtype=torch.int32)
-        host[:r_n] = torch.tensor(seqs, dtype=torch.int32)
-        for i, r in enumerate(reqs):
-            if ys[i]:
-                host[r_n + i * mb: r_n + i * mb + ys[i]] = torch.tensor(self.tables[r][: ys[i]], dtype=torch.int32)
-        params = host.pin_memory().to(dev, non_blocking=True)
-        seq_dev, bt_dev = params[:r_n], params[r_n:].view(r_n, mb)
+        seq_dev, bt_dev = self._device_tables(reqs)
+        mb = bt_dev.shape[1]
         bmax = max(max(kept), 1)
         perm = torch.empty(r_n, bmax, dtype=torch.int64, device=dev)
         pin_out = None if pinned_in is None else torch.empty(r_n, bmax, dtype=torch.bool, device=dev)
@@ -238,8 +324,9 @@ class PagedKVCache:
         _hip.check(rc, "actkv_compact")
         for i, r in enumerate(reqs):
             drop = ys[i] - math.ceil(kept[i] / bs)
-            freed = self.tables[r][:drop]
-            self.tables[r] = self.tables[r][drop:]
+            table = self.tables[r]
+            freed = table[:drop]
+            self.tables[r] = table.tail(drop) if isinstance(table, _Table) else table[drop:]
             self.free.extend(reversed(freed))
             self.seq_used[r] = kept[i]
         return perm, pin_out

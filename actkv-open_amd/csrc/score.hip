@@ -44,6 +44,10 @@ struct ScoreArgs {
   int qc0, qcn;  // query chunk [qc0, qc0+qcn) handled by this launch (MFMA path)
 };
 
+// IEEE maximum (NaN-propagating, as torch's amax): lowers to v_maximum3_f32 on
+// gfx950 without the operand canonicalisation fmaxf needs.
+__device__ __forceinline__ float vmax(float x, float y) { return __builtin_elementwise_maximum(x, y); }
+
 __device__ __forceinline__ int seq_len_of(const ScoreArgs &a, int r) {
   int s = a.seq_used[r];
   int span = a.max_blocks * a.BS;
@@ -108,30 +112,42 @@ __global__ void __launch_bounds__(256) score_generic_kernel(ScoreArgs a) {
 }
 
 // ------------------------------------------------------------------ MFMA tile
-// One workgroup = WAVES waves; wave w holds rows [(w*RT)*16, (w*RT+RT)*16) of the
-// [nq*G, 128] query tile as v_mfma_f32_16x16x32 A-operands (RT row tiles of 16
-// rows = 16/G queries each).  K rows of the head stream through a
-// double-buffered LDS stage of CH = 64 tokens (16 KiB), XOR-swizzled in 16-byte
-// pieces so the B-operand reads (16 tokens x one piece) hit distinct banks.
+// One workgroup (NW waves) owns a (layer, request, KV head) pair and a
+// token range.  The pair's whole action-query tile -- rows (query n, group head g),
+// nq*G <= ROWS of them, head_dim 128, bf16/fp16 -- is staged ONCE into LDS
+// (rows padded to 272 bytes: conflict-free A-operand reads), with the
+// accumulator seeds -lse/scale (-inf for padding rows, which then add
+// exp2(-inf) = 0) and the pair's slice of the block table.  After that single
+// barrier each wave works alone on 32*TT-token slices of the range: it loads the
+// slice's K rows straight from HBM into MFMA B-operand registers (double
+// buffered: the next slice is in flight while this one is multiplied), sweeps all
+// 32-row tiles of the query tile from LDS with v_mfma_f32_32x32x16 (the shape
+// that reaches the bf16 peak on gfx950), and writes the slice's running means.
 //
-// MFMA lane layout (16x16x32): lane L supplies A[L%16][8*(L/16)+j] and
-// B[8*(L/16)+j][L%16] (j<8) and receives D[4*(L/16)+i][L%16] (i<4).  Rows are
-// ordered (query, group head), so with G=4 a lane's four outputs are the four
-// group heads of one query at one token: the GQA max is in-register.
-template <typename T, typename V8, int G, int WAVES, int RT>
-__global__ void __launch_bounds__(WAVES * 64) score_mfma_kernel(ScoreArgs a, int tpw, int cpp,
-                                                                 int pairs) {
-  constexpr int KS = 4, CH = 64, NT = WAVES * 64;  // head_dim 128 = KS x 32
-  constexpr int QS = 4 / G;                    // queries per lane per row tile
-  constexpr int PIECES = CH * 16;              // 16-byte pieces per stage
-  constexpr int PPT = PIECES / NT;             // pieces per thread per stage
-  static_assert(PIECES % NT == 0, "stage must divide evenly");
-  __shared__ __attribute__((aligned(16))) unsigned char kbuf[2][CH * 256];
-  __shared__ float red[2][WAVES][CH];
+// v_mfma_f32_32x32x16 lane layout: lane L supplies A[L%32][8*(L/32)+j] and
+// B[8*(L/32)+j][L%32] (j < 8) and receives D[8*(r/4) + 4*(L/32) + r%4][L%32] in
+// register r < 16.  Rows are ordered (n, g); with G = 4 each aligned group of
+// four rows is one query's four group heads, so a lane holds four queries x
+// four heads at one token: the GQA max is in-register and
+// max_g exp(x_g) = exp(max_g x_g) costs one exp per (query, token).
+template <typename T, typename V8, int G, int ROWS, bool CAUSAL, int NW, int TT>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
+score_mfma_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
+  // NW waves (NW/4 per SIMD), TT 32-token tiles per wave slice
+  constexpr int SLICE = TT * 32, KS = 8, MAXBT = 8192 / 16 + 2;
+  constexpr int QG = 4 / G;  // queries in an aligned group of four rows
+  // query rows are padded to 272 bytes: 16 consecutive rows then start in 16
+  // distinct 16-byte bank groups (conflict-free A reads) and every A-operand
+  // read of a tile is a constant offset from one per-lane base address
+  constexpr int QROW = 272;
+  __shared__ __attribute__((aligned(16))) unsigned char qs[ROWS * QROW];
+  __shared__ __attribute__((aligned(16))) float cs[ROWS];
+  __shared__ __attribute__((aligned(16))) int ls[CAUSAL ? ROWS : 4];
+  __shared__ int bts[MAXBT];
 
-  // XCD-aware work mapping: all token chunks of one (layer, request, head)
+  // XCD-aware work mapping: all token ranges of one (layer, request, head)
   // pair land on the same XCD (blockIdx % 8), so its query tile is fetched
-  // into that XCD's L2 once.
+  // from HBM into that XCD's L2 once.
   const int bid = blockIdx.x;
   const int xcd = bid & 7, jj = bid >> 3;
   const int p = (jj / cpp) * 8 + xcd;
@@ -148,149 +164,211 @@ __global__ void __launch_bounds__(WAVES * 64) score_mfma_kernel(ScoreArgs a, int
   const int nq = min(max(nq_all - a.qc0, 0), a.qcn);
   if (nq <= 0) return;
   const int n0 = a.n_seen[r] + min(nq_all, a.qc0);
+  const int BS = a.BS;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int lrow = lane & 15, lgrp = lane >> 4;
-  const float c2 = a.scale * 1.4426950408889634f;
-  const float inv_scale = 1.0f / a.scale;
+  const int lcol = lane & 31, lh = lane >> 5;
+  const int rows = nq * G;
+  // an even number of 32-row tiles keeps the two-tile software pipeline
+  // branch-free; padding rows have zero queries and -inf seeds
+  const int rtiles = (((rows + 31) >> 5) + 1) & ~1;
 
-  // ---- query tile -> A operands, -lse/scale -> accumulator seeds
-  V8 qa[RT][KS];
-  f32x4 cinit[RT];
-  int lim[RT][QS];
-  const T *qbase = (const T *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr;
-  const float *lbase = a.lse + (int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr;
-#pragma unroll
-  for (int jt = 0; jt < RT; ++jt) {
-    const int row = (wave * RT + jt) * 16 + lrow;
-    const int n = row / G, g = row % G;
-    if (n < nq) {
-      const T *qp = qbase + (int64_t)(a.qc0 + n) * a.q_sn + (int64_t)(h * G + g) * a.q_sh + lgrp * 8;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qa[jt][ks] = *(const V8 *)(qp + ks * 32);
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qa[jt][ks] = V8{};
+  // ---- stage the query tile, the accumulator seeds and the block-table slice
+  {
+    const T *qbase = (const T *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr;
+    for (int e = tid; e < rtiles * 32 * 16; e += NW * 64) {
+      const int row = e >> 4, pc = e & 15;
+      const int n = row / G, g = row % G;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (n < nq)
+        v = *(const uint4 *)(qbase + (int64_t)(a.qc0 + n) * a.q_sn + (int64_t)(h * G + g) * a.q_sh + pc * 8);
+      *(uint4 *)(&qs[row * QROW + pc * 16]) = v;
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int orow = (wave * RT + jt) * 16 + 4 * lgrp + i;
-      const int on = orow / G, og = orow % G;
-      cinit[jt][i] = on < nq ? -lbase[(int64_t)(a.qc0 + on) * a.lse_sn + h * G + og] * inv_scale : 0.f;
+    const float *lbase = a.lse + (int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr;
+    const float inv_scale = 1.0f / a.scale;
+    for (int row = tid; row < rtiles * 32; row += NW * 64) {
+      const int n = row / G, g = row % G;
+      cs[row] = n < nq ? -lbase[(int64_t)(a.qc0 + n) * a.lse_sn + h * G + g] * inv_scale : -INFINITY;
+      if constexpr (CAUSAL) ls[row] = n < nq ? a.kv_len[(int64_t)r * a.N + a.qc0 + n] : 0;
     }
-#pragma unroll
-    for (int qsl = 0; qsl < QS; ++qsl) {
-      const int on = ((wave * RT + jt) * 16 + 4 * lgrp) / G + qsl;
-      int lm = 0;
-      if (on < nq) lm = a.kv_len ? a.kv_len[(int64_t)r * a.N + a.qc0 + on] : 0x7fffffff;
-      lim[jt][qsl] = lm;
+    const int b0 = t_begin >> bs_shift;
+    const int nbt = ((t_end - 1) >> bs_shift) - b0 + 1;
+    const int32_t *btr = a.bt + (int64_t)r * a.bt_sr;
+    for (int i = tid; i < nbt; i += NW * 64) {
+      const int64_t phys = btr[b0 + i];
+      bts[i] = (phys >= 0 && phys < a.num_blocks) ? (int)phys : -1;
     }
   }
-
-  // ---- K stage loader: piece e = tid + i*NT -> token e/16, piece e%16
-  const T *kbase = (const T *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh;
-  const int32_t *btr = a.bt + (int64_t)r * a.bt_sr;
-  uint4 pre[PPT];
-  auto load_stage = [&](int cb) {
-#pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      const int e = tid + i * NT;
-      const int tk = e >> 4, pc = e & 15;
-      const int t = cb + tk;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (t < t_end) {
-        const int64_t phys = btr[t / a.BS];
-        if (phys >= 0 && phys < a.num_blocks)
-          v = *(const uint4 *)(kbase + phys * a.kv_sb + (int64_t)(t % a.BS) * a.kv_ss + pc * 8);
-      }
-      pre[i] = v;
-    }
-  };
-  auto store_stage = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < PPT; ++i) {
-      const int e = tid + i * NT;
-      const int tk = e >> 4, pc = e & 15;
-      *(uint4 *)(&kbuf[buf][tk * 256 + ((pc ^ (tk & 15)) << 4)]) = pre[i];
-    }
-  };
-
-  const int nchunks = (t_end - t_begin + CH - 1) / CH;
-  load_stage(t_begin);
-  store_stage(0);
   __syncthreads();
 
+  const T *kbase = (const T *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh + lh * 8;
+  const int b0 = t_begin >> bs_shift;
+  const int nbt = ((t_end - 1) >> bs_shift) - b0 + 1;
+  const float c2 = a.scale * 1.4426950408889634f;
   float *obase = a.out + (int64_t)l * a.out_sl + (int64_t)r * a.out_sr + (int64_t)h * a.out_sh;
   const float fn0 = (float)n0, fden = (float)(n0 + nq);
 
-  for (int c = 0; c < nchunks; ++c) {
-    const int buf = c & 1;
-    const int cb = t_begin + c * CH;
-    if (c + 1 < nchunks) load_stage(cb + CH);
+  // B operands of one slice: kf[tt][ks] = K[token s+32tt+lcol][16ks + 8lh .. +8].
+  // Unconditional loads (no branch) keep the compiler's wait counts exact, so the
+  // next slice stays in flight: a token past t_end, or in a block the table marks
+  // invalid, reads row 0 of block 0 instead and its output column is never written.
+  auto load_slice = [&](V8 (&kf)[TT][KS], int s) {
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      const int tb = s + tt * 32;           // 32-token tile: whole blocks when bs >= 32,
+      const int t = tb + lcol;              // else two blocks (per-lane block index)
+      const int bi = min((t >> bs_shift) - b0, nbt - 1);
+      int phys = bts[bi];
+      const bool ok = t < t_end && phys >= 0;
+      phys = ok ? phys : 0;
+      const int slot = ok ? (t & (BS - 1)) : 0;
+      const T *kp = kbase + (int64_t)phys * a.kv_sb + (int64_t)slot * a.kv_ss;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[tt][ks] = *(const V8 *)(kp + ks * 16);
+    }
+  };
 
-    float psum[4];
+  // A operands and seeds of one 32-row tile
+  auto load_a = [&](int jt, V8 (&af)[KS], f32x16 &c, int (&lim)[4][QG]) {
+    const unsigned char *qrow = qs + (jt * 32 + lcol) * QROW + lh * 16;
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const int tk = tt * 16 + lrow;
-      V8 kb[KS];
+    for (int ks = 0; ks < KS; ++ks) af[ks] = *(const V8 *)(qrow + ks * 32);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        kb[ks] = *(const V8 *)(&kbuf[buf][tk * 256 + (((ks * 4 + lgrp) ^ (tk & 15)) << 4)]);
-      f32x4 acc[RT];
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 v = *(const f32x4 *)(&cs[jt * 32 + 8 * i + 4 * lh]);
+      c[4 * i + 0] = v[0]; c[4 * i + 1] = v[1]; c[4 * i + 2] = v[2]; c[4 * i + 3] = v[3];
+      if constexpr (CAUSAL) {
 #pragma unroll
-      for (int jt = 0; jt < RT; ++jt) acc[jt] = cinit[jt];
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-        for (int jt = 0; jt < RT; ++jt) {
-          if constexpr (sizeof(T) == 2 && __is_same(T, __bf16))
-            acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[jt][ks], kb[ks], acc[jt], 0, 0, 0);
-          else
-            acc[jt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[jt][ks], kb[ks], acc[jt], 0, 0, 0);
-        }
+        for (int qg = 0; qg < QG; ++qg) lim[i][qg] = ls[jt * 32 + 8 * i + 4 * lh + qg * G];
       }
-      const int t = cb + tk;
-      float s = 0.f;
+    }
+  };
+  auto mfma_tile = [&](const V8 (&kf)[TT][KS], const V8 (&af)[KS], const f32x16 &c, f32x16 (&acc)[TT]) {
 #pragma unroll
-      for (int jt = 0; jt < RT; ++jt) {
+    for (int tt = 0; tt < TT; ++tt) acc[tt] = c;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        if constexpr (__is_same(T, __bf16))
+          acc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks], kf[tt][ks], acc[tt], 0, 0, 0);
+        else
+          acc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[ks], kf[tt][ks], acc[tt], 0, 0, 0);
+      }
+    }
+  };
+  auto post = [&](const f32x16 (&acc)[TT], const int (&lim)[4][QG], int s, float (&psum)[TT]) {
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      const int t = s + tt * 32 + lcol;
+      float sum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a0 = acc[tt][4 * i], a1 = acc[tt][4 * i + 1], a2 = acc[tt][4 * i + 2], a3 = acc[tt][4 * i + 3];
         if constexpr (G == 4) {
-          const float m = fmaxf(fmaxf(acc[jt][0], acc[jt][1]), fmaxf(acc[jt][2], acc[jt][3]));
-          const float e = __builtin_amdgcn_exp2f(m * c2);
-          s += t < lim[jt][0] ? e : 0.f;
+          const float e = __builtin_amdgcn_exp2f(vmax(vmax(a0, a1), vmax(a2, a3)) * c2);
+          if constexpr (CAUSAL) sum += t < lim[i][0] ? e : 0.f;
+          else sum += e;
         } else if constexpr (G == 2) {
-          const float e0 = __builtin_amdgcn_exp2f(fmaxf(acc[jt][0], acc[jt][1]) * c2);
-          const float e1 = __builtin_amdgcn_exp2f(fmaxf(acc[jt][2], acc[jt][3]) * c2);
-          s += (t < lim[jt][0] ? e0 : 0.f) + (t < lim[jt][1] ? e1 : 0.f);
+          const float e0 = __builtin_amdgcn_exp2f(vmax(a0, a1) * c2);
+          const float e1 = __builtin_amdgcn_exp2f(vmax(a2, a3) * c2);
+          if constexpr (CAUSAL) sum += (t < lim[i][0] ? e0 : 0.f) + (t < lim[i][1] ? e1 : 0.f);
+          else sum += e0 + e1;
         } else {
+          const float v[4] = {a0, a1, a2, a3};
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float e = __builtin_amdgcn_exp2f(acc[jt][i] * c2);
-            s += t < lim[jt][i] ? e : 0.f;
+          for (int j = 0; j < 4; ++j) {
+            const float e = __builtin_amdgcn_exp2f(v[j] * c2);
+            if constexpr (CAUSAL) sum += t < lim[i][j] ? e : 0.f;
+            else sum += e;
           }
         }
       }
-      psum[tt] = s;
+      psum[tt] += sum;
     }
+  };
+  // One pipeline block: the 8*TT MFMAs of row tile j, the exp/max/sum of tile
+  // j-1 and the 12 LDS reads of tile j+1, interleaved so the VALU work and the
+  // LDS traffic co-issue with the matrix core.
+  auto schedule_block = [&]() {
+    if constexpr (TT == 1) {  // 8 MFMAs, 12 DS reads, ~30 VALU
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      float v = psum[tt];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      if (lgrp == 0) red[buf][wave][tt * 16 + lrow] = v;
-    }
-    if (c + 1 < nchunks) store_stage(buf ^ 1);
-    __syncthreads();
-    if (tid < CH) {
-      const int t = cb + tid;
-      if (t < t_end) {
-        float tot = 0.f;
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    } else {                  // 16 MFMAs, 12 DS reads, ~60 VALU
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) tot += red[buf][w][tid];
-        const float old = obase[t];
-        obase[t] = (old * fn0 + tot) / fden;
+      for (int i = 0; i < 12; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
       }
     }
+  };
+
+  auto process_slice = [&](const V8 (&kf)[TT][KS], int s) {
+    // the running-mean update reads the slice's old scores: fetch them now (clamped
+    // in-bounds address, unconditional) so the read is long done when they are used
+    const int t_own = s + (TT == 2 ? lh * 32 : 0) + lcol;
+    const float old = obase[min(t_own, t_end - 1)];
+    float psum[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) psum[tt] = 0.f;
+    V8 afA[KS], afB[KS];
+    f32x16 cA, cB, accA[TT], accB[TT];
+    int limA[4][QG], limB[4][QG];
+    // rtiles is even: tile 0 (prologue), pairs (1,2) .. (rt-3, rt-2), tile rt-1
+    // (epilogue); even tiles use the A buffers, odd tiles the B buffers
+    load_a(0, afA, cA, limA);
+    load_a(1, afB, cB, limB);
+    mfma_tile(kf, afA, cA, accA);
+    for (int jt = 1; jt + 1 < rtiles; jt += 2) {
+      mfma_tile(kf, afB, cB, accB);
+      post(accA, limA, s, psum);
+      load_a(jt + 1, afA, cA, limA);
+      schedule_block();
+      mfma_tile(kf, afA, cA, accA);
+      post(accB, limB, s, psum);
+      load_a(jt + 2, afB, cB, limB);
+      schedule_block();
+    }
+    mfma_tile(kf, afB, cB, accB);
+    post(accA, limA, s, psum);
+    post(accB, limB, s, psum);
+    // sum the two lane halves (the queries) of each token; with TT = 2 half lh owns
+    // token tile lh of the slice, with TT = 1 the first half writes
+    float mine = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      const float v = psum[tt] + __shfl_xor(psum[tt], 32, 64);
+      mine = (TT == 1 || lh == tt) ? v : mine;
+    }
+    if (t_own < t_end && (TT == 2 || lh == 0)) obase[t_own] = (old * fn0 + mine) / fden;
+  };
+
+  const int step = NW * SLICE;
+  int s = t_begin + wave * SLICE;
+  if (s >= t_end) return;
+  V8 ka[TT][KS], kb[TT][KS];
+  load_slice(ka, s);
+  for (;;) {
+    load_slice(kb, s + step);   // past the end it reads harmless in-bounds rows
+    process_slice(ka, s);
+    s += step;
+    if (s >= t_end) break;
+    load_slice(ka, s + step);
+    process_slice(kb, s);
+    s += step;
+    if (s >= t_end) break;
   }
 }
 
@@ -300,31 +378,39 @@ __global__ void bump_n_seen_kernel(int32_t *n_seen, const int32_t *n_valid, int 
 }
 
 template <typename T, typename V8, int G>
-static int launch_mfma(const ScoreArgs &a0, hipStream_t st) {
+static int launch_mfma(const ScoreArgs &a0, int bs_shift, hipStream_t st) {
   const int pairs = a0.L * a0.R * a0.Hkv;
   const int span = a0.max_blocks * a0.BS;
-  const int rows_max = 512;  // 8 waves x 4 row tiles x 16 rows; more rows spill VGPRs
-  const int q_per_launch = rows_max / G;
+  const int q_per_launch = 512 / G;  // LDS holds at most 512 query rows (128 KiB)
+  const bool causal = a0.kv_len != nullptr;
   for (int qc0 = 0; qc0 < a0.N; qc0 += q_per_launch) {
     ScoreArgs a = a0;
     a.qc0 = qc0;
     a.qcn = std::min(q_per_launch, a0.N - qc0);
     const int rows = a.qcn * G;
-    // token range per workgroup: enough workgroups to fill 256 CUs several
-    // times over, at least 256 tokens so the query tile load is amortised.
-    const int64_t total_tiles = (int64_t)pairs * ((span + 63) / 64);
-    int tiles_per_wg = (int)std::max<int64_t>(4, (total_tiles + 2047) / 2048);
-    int tpw = tiles_per_wg * 64;
-    if (tpw > span) tpw = ((span + 63) / 64) * 64;
+    // NW waves (NW/4 per SIMD: 3 keeps the VALU post-processing overlapped with
+    // the matrix core), 32-token slices.  Token range per workgroup: a multiple of
+    // NW*32, at least 4 slices per wave so the staged query tile is reused, about
+    // 2048 workgroups in total, at most 8192 tokens (the block-table slice).
+    constexpr int NW = 12, TT = 1;
+    constexpr int round = NW * 32 * TT;
+    const int64_t rounds = (int64_t)pairs * ((span + round - 1) / round);
+    int per_wg = (int)std::min<int64_t>(8192 / round, std::max<int64_t>(4, (rounds + 2047) / 2048));
+    int tpw = per_wg * round;
     const int cpp = (span + tpw - 1) / tpw;
     const int grid = ((pairs + 7) / 8) * 8 * cpp;
-#define ACTKV_LAUNCH(WV, RTV)                                                               \
-  hipLaunchKernelGGL((score_mfma_kernel<T, V8, G, WV, RTV>), dim3(grid), dim3(WV * 64), 0, st, \
-                     a, tpw, cpp, pairs)
-    if (rows <= 64) ACTKV_LAUNCH(4, 1);
-    else if (rows <= 128) ACTKV_LAUNCH(4, 2);
-    else if (rows <= 256) ACTKV_LAUNCH(4, 4);
-    else ACTKV_LAUNCH(8, 4);
+#define ACTKV_LAUNCH(ROWSV)                                                                        \
+  do {                                                                                             \
+    if (causal)                                                                                    \
+      hipLaunchKernelGGL((score_mfma_kernel<T, V8, G, ROWSV, true, NW, TT>), dim3(grid),           \
+                         dim3(NW * 64), 0, st, a, tpw, cpp, pairs, bs_shift);                      \
+    else                                                                                           \
+      hipLaunchKernelGGL((score_mfma_kernel<T, V8, G, ROWSV, false, NW, TT>), dim3(grid),          \
+                         dim3(NW * 64), 0, st, a, tpw, cpp, pairs, bs_shift);                      \
+  } while (0)
+    if (rows <= 128) ACTKV_LAUNCH(128);
+    else if (rows <= 256) ACTKV_LAUNCH(256);
+    else ACTKV_LAUNCH(512);
 #undef ACTKV_LAUNCH
     int rc = actkv_check_launch();
     if (rc) return rc;
@@ -392,18 +478,23 @@ extern "C" int actkv_action_scores(
   const bool vec_ok = aligned16(q) && aligned16(kv) && q_sl % 8 == 0 && q_sr % 8 == 0 &&
                       q_sn % 8 == 0 && q_sh % 8 == 0 && kv_sl % 8 == 0 && kv_sb % 8 == 0 &&
                       kv_ss % 8 == 0 && kv_sh % 8 == 0;
+  // the MFMA path takes whole 16-token tiles from one block: power-of-two block sizes >= 16
+  int bs_shift = -1;
+  for (int sh = 4; sh < 31; ++sh)
+    if (block_size == (1 << sh)) bs_shift = sh;
   const bool mfma_ok = q_dtype == kv_dtype && (kv_dtype == ACTKV_BF16 || kv_dtype == ACTKV_F16) &&
-                       D == 128 && (G == 1 || G == 2 || G == 4) && scale > 0.f && vec_ok;
+                       D == 128 && (G == 1 || G == 2 || G == 4) && scale > 0.f && vec_ok &&
+                       bs_shift >= 0;
   int rc;
   if (mfma_ok) {
     if (kv_dtype == ACTKV_BF16) {
-      rc = G == 4 ? launch_mfma<__bf16, bf16x8, 4>(a, st)
-         : G == 2 ? launch_mfma<__bf16, bf16x8, 2>(a, st)
-                  : launch_mfma<__bf16, bf16x8, 1>(a, st);
+      rc = G == 4 ? launch_mfma<__bf16, bf16x8, 4>(a, bs_shift, st)
+         : G == 2 ? launch_mfma<__bf16, bf16x8, 2>(a, bs_shift, st)
+                  : launch_mfma<__bf16, bf16x8, 1>(a, bs_shift, st);
     } else {
-      rc = G == 4 ? launch_mfma<_Float16, f16x8, 4>(a, st)
-         : G == 2 ? launch_mfma<_Float16, f16x8, 2>(a, st)
-                  : launch_mfma<_Float16, f16x8, 1>(a, st);
+      rc = G == 4 ? launch_mfma<_Float16, f16x8, 4>(a, bs_shift, st)
+         : G == 2 ? launch_mfma<_Float16, f16x8, 2>(a, bs_shift, st)
+                  : launch_mfma<_Float16, f16x8, 1>(a, bs_shift, st);
     }
   } else {
     switch (q_dtype) {

@@ -1,0 +1,338 @@
+"""Score + compact throughput of the ActKV eviction step on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--layers 36] [--seq 32768] [--queries 128]
+
+Workload (defaults): a Qwen3-8B-shaped paged cache -- 36 layers, 32 query / 8 KV heads,
+head_dim 128, block_size 16, bf16 K/V ~ N(0,1) from a seed, physical blocks randomly permuted
+-- holding one 32768-token sequence.  One step is the whole eviction pass:
+
+  cal_attn : 128 action queries (bf16) with exact per-query lse, every layer, one launch
+  evict    : keep mask = 4 sinks + top 10% by the layer-averaged head-mean score, then the
+             conflict-free in-place compaction of all 72 K/V planes and block reclaim
+
+Inputs are resident in HBM when a step starts.  Compaction mutates the cache, so every step
+starts from a restored copy (device copy of kv + the host lists), outside the timed region;
+the restore also overwrites the 256 MB MALL.  Each step is timed with HIP events on the
+current stream; per-phase events give the scoring kernel's duration for the roofline.
+
+The single JSON line also carries the same numbers for one layer (BASELINE config 2 shape),
+the CPU baseline (the oracle's reference-style torch path timed on a bounded sample of the
+same workload on this host) and checks of the step's results.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "actkv-open_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg):
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def parse(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--seq", type=int, default=32768)
+    ap.add_argument("--queries", type=int, default=128)
+    ap.add_argument("--q-heads", type=int, default=32)
+    ap.add_argument("--kv-heads", type=int, default=8)
+    ap.add_argument("--head-dim", type=int, default=128)
+    ap.add_argument("--block-size", type=int, default=16)
+    ap.add_argument("--keep", type=float, default=0.10)
+    ap.add_argument("--sinks", type=int, default=4)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--cpu-folds", type=int, default=32, help="action-query folds in the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-single-layer", action="store_true", help="skip the one-layer measurement")
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "score_kernel_traffic.json"),
+                    help="rocprofv3 FETCH_SIZE/WRITE_SIZE summary of the scoring kernel (JSON)")
+    ap.add_argument("--out", help="also write the JSON line here")
+    return ap.parse_args(argv)
+
+
+class Workload:
+    """Seeded synthetic cache + action queries with exact lse, and a restorable snapshot."""
+
+    def __init__(self, args, layers, device):
+        import torch
+        from actkv.paged import PagedKVCache
+
+        self.args, self.L, self.dev = args, layers, device
+        S, bs, hkv, hq, d = args.seq, args.block_size, args.kv_heads, args.q_heads, args.head_dim
+        self.S, self.bs, self.hkv, self.hq, self.d, self.N = S, bs, hkv, hq, d, args.queries
+        self.nb = math.ceil(S / bs) + 64
+        gcpu = torch.Generator().manual_seed(args.seed)
+        self.cache = PagedKVCache(self.nb, bs, hkv, d, n_layers=layers, dtype=torch.bfloat16, device=device)
+        self.cache.free = torch.randperm(self.nb, generator=gcpu).tolist()
+        gdev = torch.Generator(device=device).manual_seed(args.seed + 1)
+        k = torch.randn(layers, S, hkv, d, generator=gdev, device=device, dtype=torch.bfloat16)
+        v = torch.randn(layers, S, hkv, d, generator=gdev, device=device, dtype=torch.bfloat16)
+        self.cache.append(0, k, v)
+        del k, v
+        self.q = torch.randn(layers, 1, self.N, hq, d, generator=gdev, device=device, dtype=torch.bfloat16)
+        self.lse = self._exact_lse()
+        self.kv0 = self.cache.kv.clone()
+        self.host0 = (list(self.cache.free), {0: list(self.cache.tables[0])}, dict(self.cache.seq_used))
+        self.table0_i32 = np.array(self.host0[1][0], dtype=np.int32)
+        self.width = math.ceil(S / bs) * bs
+        self.out = torch.zeros(layers, 1, hkv, self.width, device=device)
+        self.n_seen = torch.zeros(1, dtype=torch.int32, device=device)
+        self.budget = int(args.keep * S)
+
+    def _exact_lse(self):
+        """lse[l, 0, n, h] = logsumexp_t scale * q . k_t over the whole prefix, float32 on the GPU."""
+        import torch
+        g = self.hq // self.hkv
+        scale = self.d ** -0.5
+        lse = torch.empty(self.L, 1, self.N, self.hq, device=self.dev)
+        slots = self.cache.slot_map(0)
+        for l in range(self.L):
+            kflat = self.cache.kv[l, 0].reshape(-1, self.hkv, self.d)[slots].float()   # [S, Hkv, D]
+            for h in range(self.hkv):
+                kt = kflat[:, h].t().contiguous()                                      # [D, S]
+                qh = self.q[l, 0, :, h * g:(h + 1) * g].float().reshape(-1, self.d)   # [N*G, D]
+                lse[l, 0, :, h * g:(h + 1) * g] = torch.logsumexp((qh @ kt) * scale, -1).view(self.N, g)
+        return lse
+
+    def restore(self):
+        """Back to the pre-eviction state: KV bytes, free list, block table (with the int32 mirror
+        the cache keeps for its own tables), lengths, pins."""
+        from actkv.paged import _Table
+        self.cache.kv.copy_(self.kv0)
+        free, tables, seq = self.host0
+        self.cache.free = list(free)
+        self.cache.tables = {0: _Table(tables[0], self.table0_i32.copy())}
+        self.cache.seq_used = dict(seq)
+        self.cache.pinned.clear()
+        self.n_seen.zero_()
+
+    def step(self, ev=None):
+        """One eviction pass; ev = (start, scored, end) events recorded on the current stream."""
+        if ev:
+            ev[0].record()
+        self.cache.cal_attn([0], self.q, self.lse, self.out, self.n_seen, layer=None)
+        if ev:
+            ev[1].record()
+        perm = self.cache.evict(0, self.out[:, 0], self.budget, protected=self.args.sinks)
+        if ev:
+            ev[2].record()
+        return perm
+
+    # ---------------------------------------------------------------- algorithmic work
+    def algorithmic(self, moved_pairs, drop):
+        L, S, hkv, hq, d, N, bs, e = self.L, self.S, self.hkv, self.hq, self.d, self.N, self.bs, 2
+        nblk = math.ceil(S / bs)
+        per_layer_score = S * hkv * d * e + N * hq * d * e + N * hq * 4 + 2 * hkv * S * 4 + nblk * 4
+        score = L * per_layer_score
+        keep = L * hkv * S * 4 + S
+        compact = moved_pairs * 2 * L * hkv * d * e * 2 + S + 2 * nblk * 4 + drop * 4
+        flops = 2 * N * hq * S * d * L
+        return {"bytes_score": score, "bytes_keep": keep, "bytes_compact": compact, "flops_score": flops,
+                "bytes_score_per_layer": per_layer_score}
+
+
+def measure(w, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        w.restore()
+        w.step()
+    torch.cuda.synchronize()
+    t_step, t_score, t_evict = [], [], []
+    wall0 = time.perf_counter()
+    for _ in range(steps):
+        w.restore()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        w.step(ev)
+        torch.cuda.synchronize()
+        t_step.append(ev[0].elapsed_time(ev[2]) * 1e3)
+        t_score.append(ev[0].elapsed_time(ev[1]) * 1e3)
+        t_evict.append(ev[1].elapsed_time(ev[2]) * 1e3)
+    wall = time.perf_counter() - wall0
+    return {"step_us": statistics.mean(t_step), "step_us_median": statistics.median(t_step),
+            "score_us": statistics.mean(t_score), "evict_us": statistics.mean(t_evict),
+            "wall_s_incl_restore": wall}
+
+
+def check_step(w):
+    """Run one step from a fresh copy and check it: keep mask == the oracle's keep mask on the
+    GPU's own scores; survivors of layer 0 == the pre-compaction rows at perm; host lists."""
+    import numpy as np
+    import torch
+    from oracle import reference as ref
+
+    w.restore()
+    slots_before = w.cache.slot_map(0)
+    perm = w.step()
+    torch.cuda.synchronize()
+    scores = w.out[:, 0].cpu()
+    keep_o = ref.keep_mask_from_scores(scores, w.S, w.budget, protected=w.args.sinks)
+    kept_o = torch.nonzero(keep_o).flatten()
+    ok_mask = bool(torch.equal(torch.sort(perm.cpu()).values, kept_o))
+    src, dst, perm_o, drop = ref.plan_compaction(keep_o.numpy(), w.S, w.host0[1][0], w.bs)
+    ok_perm = bool(np.array_equal(perm.cpu().numpy(), perm_o))
+    flat0 = w.kv0[0].view(2, -1, w.hkv, w.d)
+    before = flat0[:, slots_before[perm]]
+    after_slots = w.cache.slot_map(0)
+    after = w.cache.kv[0].view(2, -1, w.hkv, w.d)[:, after_slots]
+    ok_rows = bool(torch.equal(before.view(torch.int16), after.view(torch.int16)))
+    nblk = math.ceil(w.S / w.bs)
+    ok_host = (w.cache.seq_used[0] == int(keep_o.sum()) and len(w.cache.tables[0]) == nblk - drop
+               and len(w.cache.free) == w.nb - (nblk - drop))
+    return {"keep_mask_matches_oracle": ok_mask, "perm_matches_oracle": ok_perm,
+            "layer0_rows_match": ok_rows, "allocator_state_ok": ok_host}, int(src.size), int(drop)
+
+
+def cpu_baseline(w, folds):
+    """The oracle's reference-style torch CPU path on a bounded sample: `folds` action-query folds
+    of one layer (one query per fold, as the reference), then keep mask + compaction of that layer;
+    extrapolated linearly to the whole step (L layers x N folds)."""
+    import numpy as np
+    import torch
+    from oracle import reference as ref
+
+    kv_l = w.kv0[0].cpu()
+    table = [w.host0[1][0]]
+    q = w.q[0, 0].cpu()            # [N, Hq, D]
+    lse = w.lse[0, 0].cpu()        # [N, Hq]
+    out = torch.zeros(1, w.hkv, w.width)
+    ns = torch.zeros(1, dtype=torch.int32)
+    folds = min(folds, w.N)
+    t0 = time.perf_counter()
+    for n in range(folds):
+        ref.action_scores_fold(q[n:n + 1], kv_l, table, [w.S], lse[n:n + 1], out, ns)
+    t_fold = (time.perf_counter() - t0) / folds
+    model = ref.PagedCacheModel(w.nb, w.bs, w.hkv, w.d, 1)
+    model.kv = kv_l.unsqueeze(0).view(torch.int16).numpy().copy()
+    model.free, model.tables, model.seq_used = list(w.host0[0]), {0: list(table[0])}, {0: w.S}
+    t1 = time.perf_counter()
+    model.evict(0, out[0], w.budget, protected=w.args.sinks)
+    t_evict_layer = time.perf_counter() - t1
+    total_s = w.L * (w.N * t_fold + t_evict_layer)
+    return {"t_fold_s": t_fold, "t_evict_one_layer_s": t_evict_layer, "extrapolated_step_s": total_s,
+            "threads": torch.get_num_threads(), "sample_s": folds * t_fold + t_evict_layer}
+
+
+def load_traffic(path):
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
+def main(argv=None):
+    args = parse(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (the eviction path "
+              "shards by request or KV head, see DESIGN.md), run with --gpus 1", file=sys.stderr)
+        return 2
+    import torch
+    from actkv import _hip
+
+    if not _hip.available():
+        print("bench.py needs a ROCm GPU and the built libactkv_hip.so", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    log(f"building the {args.layers}-layer workload")
+    w = Workload(args, args.layers, dev)
+    log("checking one step against the oracle")
+    checks, moved, drop = check_step(w)
+    log(f"checks {checks}; timing {args.warmup} + {args.steps} steps")
+    work = w.algorithmic(moved, drop)
+    m = measure(w, args.steps, args.warmup)
+    total_bytes = work["bytes_score"] + work["bytes_keep"] + work["bytes_compact"]
+    gbs = total_bytes / (m["step_us"] * 1e-6) / 1e9
+    score_tflops = work["flops_score"] / (m["score_us"] * 1e-6) / 1e12
+    traffic = load_traffic(args.traffic)
+    traffic_bytes = None
+    if traffic and traffic.get("layers") == args.layers and traffic.get("seq") == args.seq \
+            and traffic.get("queries") == args.queries:
+        traffic_bytes = traffic.get("hbm_bytes_per_launch")
+
+    log(f"step {m['step_us']:.1f} us, score {m['score_us']:.1f} us")
+    single = None
+    if not args.no_single_layer and args.layers != 1:
+        log("one-layer workload")
+        w1 = Workload(args, 1, dev)
+        c1, mv1, dr1 = check_step(w1)
+        wk1 = w1.algorithmic(mv1, dr1)
+        m1 = measure(w1, args.steps, args.warmup)
+        b1 = wk1["bytes_score"] + wk1["bytes_keep"] + wk1["bytes_compact"]
+        single = {"step_us": round(m1["step_us"], 2), "score_us": round(m1["score_us"], 2),
+                  "evict_us": round(m1["evict_us"], 2),
+                  "score_compact_GBps": round(b1 / (m1["step_us"] * 1e-6) / 1e9, 1),
+                  "pct_of_hbm_peak": round(100 * b1 / (m1["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
+                  "score_TFLOPs": round(wk1["flops_score"] / (m1["score_us"] * 1e-6) / 1e12, 1),
+                  "checks": c1}
+        del w1
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"CPU baseline sample ({args.cpu_folds} folds of one layer)")
+        c = cpu_baseline(w, args.cpu_folds)
+        cpu = {"value": round(total_bytes / c["extrapolated_step_s"] / 1e9, 4), "unit": "GB/s",
+               "cores": c["threads"], "kind": "port",
+               "sample": (f"1 of {args.layers} layers x {min(args.cpu_folds, args.queries)} of {args.queries} "
+                          f"one-query folds (reference torch fold per action token) + keep mask + compaction "
+                          f"of that layer, {c['sample_s']:.1f} s; extrapolated linearly to the whole step "
+                          f"({c['extrapolated_step_s']:.0f} s)"),
+               "step_s_extrapolated": round(c["extrapolated_step_s"], 1)}
+
+    result = {
+        "metric": "score+compact HBM GB/s (% of 8 TB/s) and evict us/layer, Qwen3-8B shape 32k",
+        "value": round(gbs, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(m["step_us"] / 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"qwen3-8b-shaped paged cache: {args.layers} layers x 1 sequence x {args.seq} "
+                               f"tokens, Hq {args.q_heads} / Hkv {args.kv_heads}, head_dim {args.head_dim}, "
+                               f"block {args.block_size}, bf16, {args.queries} action queries, keep "
+                               f"{args.keep:.0%} + {args.sinks} sinks, shuffled blocks",
+                   "layers": args.layers, "seq_len": args.seq, "action_queries": args.queries,
+                   "parallelism": "single-gpu"},
+        "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "evict_us_per_layer": round(m["step_us"] / args.layers, 3),
+        "phases_us": {"score": round(m["score_us"], 2), "keep_mask+compact": round(m["evict_us"], 2),
+                      "step_median": round(m["step_us_median"], 2)},
+        "algorithmic": work,
+        "roofline": {"kernel": "score_mfma_kernel (actkv_action_scores)", "bound": "mfma",
+                     "achieved": round(score_tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(score_tflops / BF16_PEAK_TFLOPS, 4), "traffic": traffic_bytes,
+                     "hbm_GBps_algorithmic": round(work["bytes_score"] / (m["score_us"] * 1e-6) / 1e9, 1)},
+        "cpu_baseline": cpu,
+        "single_layer": single,
+        "checks": checks,
+        "wall_s_incl_restore": round(m["wall_s_incl_restore"], 3),
+        "gpu": torch.cuda.get_device_name(dev),
+    }
+    line = json.dumps(result)
+    print(line)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(line + "\n")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -273,3 +273,56 @@ def test_evict_keeps_the_protected_tokens_across_repeated_evictions():
     assert all(any(torch.equal(p, row) for row in k) for p in prompt)
     assert np.array_equal(np.sort(perm.cpu().numpy()), np.sort(perm_o))
     _assert_same_state(cache, model)
+
+
+@pytest.mark.parametrize("dtype,hq,hkv,d,bs", [(torch.bfloat16, 32, 8, 128, 16), (torch.float16, 16, 8, 128, 32),
+                                               (torch.bfloat16, 8, 8, 128, 16), (torch.float32, 6, 3, 24, 8)])
+def test_action_scores_causal_region_and_ragged_query_counts(dtype, hq, hkv, d, bs):
+    """kv_len (query n sees tokens t < kv_len[r, n]) and n_valid (request r folds its first
+    n_valid[r] queries): the causal action region of an agent round (additive extension)."""
+    lens = [700, 90, 1500]
+    n_q = 23
+    cache = _filled_cache(lens, bs=bs, hkv=hkv, d=d, dtype=dtype, seed=11)
+    reqs = list(range(len(lens)))
+    bt, seq = cache.block_table(reqs), cache.seq_tensor(reqs)
+    width = bt.shape[1] * bs
+    g = torch.Generator().manual_seed(12)
+    q = torch.randn(len(reqs), n_q, hq, d, generator=g).to(dtype)
+    kv0 = cache.kv[0].cpu()
+    tables = [cache.tables[r] for r in reqs]
+    lse = torch.stack([ref.decode_lse(q[:, n], kv0, tables, lens) for n in range(n_q)], 1)
+    n_valid = torch.tensor([23, 5, 17], dtype=torch.int32)
+    kv_len = torch.stack([torch.randint(1, s + 1, (n_q,), generator=g) for s in lens]).to(torch.int32)
+    kv_len[0, 3] = lens[0]
+    out0 = torch.rand(len(reqs), hkv, width, generator=g)
+    n0 = torch.tensor([2, 0, 7], dtype=torch.int32)
+    out_k, n_k = out0.cuda(), n0.cuda()
+    action_scores(q.cuda(), cache.kv[0], bt, seq, lse.cuda(), out_k, n_k, n_valid=n_valid.cuda(), kv_len=kv_len.cuda())
+    out_o, n_o = out0.clone(), n0.clone()
+    ref.action_scores_nfold(q, kv0, tables, lens, lse, out_o, n_o, n_valid=n_valid, kv_len=kv_len)
+    rtol = 1e-4 if dtype == torch.float32 else 1e-3
+    torch.testing.assert_close(out_k.cpu(), out_o, rtol=rtol, atol=1e-6)
+    assert torch.equal(n_k.cpu(), n_o)
+
+
+def test_action_scores_every_layer_in_one_launch():
+    """kv [L, 2, ...] with q [L, R, N, Hq, D]: each layer scored against its own K (extension)."""
+    lens = [300, 77]
+    L, hq, hkv, d, n_q = 3, 32, 8, 128, 6
+    cache = _filled_cache(lens, hkv=hkv, d=d, layers=L, dtype=torch.bfloat16, seed=13)
+    reqs = [0, 1]
+    width = cache.block_table(reqs).shape[1] * 16
+    g = torch.Generator().manual_seed(14)
+    q = torch.randn(L, 2, n_q, hq, d, generator=g).to(torch.bfloat16)
+    tables = [cache.tables[r] for r in reqs]
+    kvs = [cache.kv[l].cpu() for l in range(L)]
+    lse = torch.stack([torch.stack([ref.decode_lse(q[l, :, n], kvs[l], tables, lens) for n in range(n_q)], 1)
+                       for l in range(L)])
+    out = torch.zeros(L, 2, hkv, width, device="cuda")
+    n_seen = torch.zeros(2, dtype=torch.int32, device="cuda")
+    cache.cal_attn(reqs, q.cuda(), lse.cuda(), out, n_seen, layer=None)
+    for l in range(L):
+        want = torch.zeros(2, hkv, width)
+        ref.action_scores_nfold(q[l], kvs[l], tables, lens, lse[l], want, torch.zeros(2, dtype=torch.int32))
+        torch.testing.assert_close(out[l].cpu(), want, rtol=1e-3, atol=1e-6)
+    assert n_seen.tolist() == [n_q, n_q]

@@ -50,27 +50,29 @@ struct CompactArgs {
 };
 
 // Exclusive scan of popcounts of words[0..nw) into pre[0..nw]; pre[nw] = total.
+// Each thread sums a contiguous run of words; runs are scanned with wave
+// shuffles and one LDS pass over the CT/64 wave totals.
 __device__ void scan_words(const uint32_t *words, uint32_t *pre, int nw) {
-  __shared__ uint32_t part[CT];
+  __shared__ uint32_t wsum[CT / 64];
   const int per = (nw + CT - 1) / CT;
   const int lo = threadIdx.x * per, hi = min(lo + per, nw);
   uint32_t s = 0;
   for (int w = lo; w < hi; ++w) s += __popc(words[w]);
-  part[threadIdx.x] = s;
-  __syncthreads();
-  // Hillis-Steele inclusive scan over CT partials
-  for (int o = 1; o < CT; o <<= 1) {
-    const uint32_t v = threadIdx.x >= o ? part[threadIdx.x - o] : 0u;
-    __syncthreads();
-    part[threadIdx.x] += v;
-    __syncthreads();
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  uint32_t inc = s;
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t v = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += v;
   }
-  uint32_t run = threadIdx.x > 0 ? part[threadIdx.x - 1] : 0u;
+  if (lane == 63) wsum[wv] = inc;
+  __syncthreads();
+  uint32_t run = inc - s;
+  for (int i = 0; i < wv; ++i) run += wsum[i];
   for (int w = lo; w < hi; ++w) {
     pre[w] = run;
     run += __popc(words[w]);
   }
-  if (threadIdx.x == CT - 1) pre[nw] = part[CT - 1];
+  if (threadIdx.x == CT - 1) pre[nw] = run;
   __syncthreads();
 }
 
@@ -104,6 +106,12 @@ __device__ __forceinline__ int select0(const uint32_t *words, const uint32_t *pr
   return lo * 32 + select_bit(~words[lo], (int)(k - ((uint32_t)(lo * 32) - pre[lo])));
 }
 
+// Streaming copies: every moved row is read once and written once, so both
+// sides use non-temporal accesses (no L2 allocation for the destination lines,
+// which a write-allocate would otherwise fetch from HBM first).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
 template <typename U>
 __device__ __forceinline__ void copy_rows(unsigned char *kv, int64_t sp, int64_t ss,
                                           int64_t row_bytes, const int64_t *src_slot,
@@ -129,14 +137,14 @@ __device__ __forceinline__ void copy_rows(unsigned char *kv, int64_t sp, int64_t
         const int64_t s = src_slot[pr], d = dst_slot[pr];
         if (s >= 0 && d >= 0) {
           const int64_t poff = (p0 + pl) * sp + (int64_t)unit * sizeof(U);
-          v[u] = *(const U *)(kv + poff + s * ss);
+          v[u] = __builtin_nontemporal_load((const U *)(kv + poff + s * ss));
           dptr[u] = kv + poff + d * ss;
         }
       }
     }
 #pragma unroll
     for (int u = 0; u < UNR; ++u)
-      if (dptr[u]) *(U *)dptr[u] = v[u];
+      if (dptr[u]) __builtin_nontemporal_store(v[u], (U *)dptr[u]);
   }
 }
 
@@ -261,12 +269,12 @@ static int unit_bytes(const void *base, int64_t sp, int64_t ss, int64_t row_byte
   return 1;
 }
 
-// Pairs per tile and planes per group: aim for ~2048 workgroups, each moving
-// 32 KiB .. 1 MiB, so the per-workgroup plan scan stays a small fraction of
-// the moves.
+// Pairs per tile and planes per group: about 1024 workgroups, each moving 32 KiB
+// .. 2 MiB, so the per-workgroup plan (scan + selects) stays a small fraction of
+// its row moves.
 static void copy_shape(int64_t max_pairs, int64_t planes, int64_t row_bytes, int *P, int *PG) {
   const int64_t bytes = std::max<int64_t>(1, max_pairs) * planes * row_bytes;
-  int64_t per_wg = std::max<int64_t>(32 * 1024, std::min<int64_t>(1024 * 1024, bytes / 2048));
+  int64_t per_wg = std::max<int64_t>(32 * 1024, std::min<int64_t>(2048 * 1024, bytes / 1024));
   int64_t pairs_cap = std::max<int64_t>(1, per_wg / std::max<int64_t>(1, row_bytes));
   int p = (int)std::min<int64_t>(MAX_PAIRS, std::max<int64_t>(4, std::min<int64_t>(pairs_cap, max_pairs)));
   int64_t pg = std::max<int64_t>(1, per_wg / ((int64_t)p * row_bytes));
@@ -298,8 +306,8 @@ extern "C" int actkv_copy_slots(void *kv_flat, int64_t planes, int64_t stride_pl
                      stride_plane_bytes, stride_slot_bytes, row_bytes, num_slots, src, dst, \
                      n_pairs, P, PG);                                                       \
   break
-    case 16: ACTKV_COPY(uint4);
-    case 8: ACTKV_COPY(uint2);
+    case 16: ACTKV_COPY(u32x4);
+    case 8: ACTKV_COPY(u32x2);
     case 4: ACTKV_COPY(uint32_t);
     case 2: ACTKV_COPY(uint16_t);
     default: ACTKV_COPY(uint8_t);
@@ -351,8 +359,8 @@ extern "C" int actkv_compact(void *kv, int64_t planes, int64_t stride_plane_byte
   switch (do_copy ? unit_bytes(kv, stride_plane_bytes, stride_slot_bytes, row_bytes) : 16) {
 #define ACTKV_COMPACT(UT) \
   hipLaunchKernelGGL(compact_kernel<UT>, grid, dim3(CT), shm, st, a); break
-    case 16: ACTKV_COMPACT(uint4);
-    case 8: ACTKV_COMPACT(uint2);
+    case 16: ACTKV_COMPACT(u32x4);
+    case 8: ACTKV_COMPACT(u32x2);
     case 4: ACTKV_COMPACT(uint32_t);
     case 2: ACTKV_COMPACT(uint16_t);
     default: ACTKV_COMPACT(uint8_t);

@@ -91,7 +91,8 @@ struct KeepArgs {
   uint32_t *bits;
   int64_t bits_sr;
   int BS, max_seq;
-  uint32_t *keys;   // [R, max_seq]
+  uint32_t *keys;   // [R, keys_sr], keys_sr = max_seq rounded up to a multiple of 4
+  int64_t keys_sr;
   uint32_t *hist;   // [R, HIST_BINS]
   int32_t *sel;     // [R, 4]
 };
@@ -102,9 +103,11 @@ __device__ __forceinline__ bool is_protected(const KeepArgs &a, int r, int t) {
   return false;
 }
 
-// grid (ceil(max_seq/64), R), 256 threads: token = tid%64, layer group = tid/64.
+constexpr int REDUCE_THREADS = 1024;  // 64 tokens x 16 layer groups
+
+// grid (ceil(max_seq/64), R), REDUCE_THREADS threads: token = tid%64, layer group = tid/64.
 template <typename ST>
-__global__ void __launch_bounds__(256) keep_reduce_kernel(KeepArgs a) {
+__global__ void __launch_bounds__(REDUCE_THREADS) keep_reduce_kernel(KeepArgs a) {
   extern __shared__ float lvals[];  // [L][64]
   const int r = blockIdx.y;
   const int S = min(a.seq_used[r], a.max_seq);
@@ -115,7 +118,7 @@ __global__ void __launch_bounds__(256) keep_reduce_kernel(KeepArgs a) {
   const bool body = t < (S & ~31);
   const ST *sbase = (const ST *)a.scores + (int64_t)r * a.s_sr;
   if (t < S) {
-    for (int l = lg; l < a.L; l += 4) {
+    for (int l = lg; l < a.L; l += REDUCE_THREADS / 64) {
       const ST *col = sbase + (int64_t)l * a.s_sl + t;
       float v;
       if (a.head_reduce == ACTKV_REDUCE_MAX) {
@@ -137,7 +140,7 @@ __global__ void __launch_bounds__(256) keep_reduce_kernel(KeepArgs a) {
     const float s = __fdiv_rn(torch_sum(ld, a.L, body), (float)a.L);
     key = float_key(s);
   }
-  if (in) a.keys[(int64_t)r * a.max_seq + t] = key;
+  if (in) a.keys[(int64_t)r * a.keys_sr + t] = key;
   // wave-aggregated histogram of candidate keys (key != 0)
   uint32_t *hist = a.hist + (int64_t)r * HIST_BINS;
   bool pending = key != 0;
@@ -166,32 +169,36 @@ __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t *scratch)
   return tot;
 }
 
-// Find the bin holding the k-th largest element: hist[nbins] in LDS.
-// Returns bin; *need = k - (#elements in bins above it).
+// Find the bin holding the k-th largest element of hist[nbins] (LDS), 1 <= k <=
+// total.  Returns the bin; *need = k - (#elements in the bins above it).  Thread
+// i owns the nbins/blockDim bins counted from the top; a block-wide exclusive
+// scan of those counts (wave shuffles + one LDS pass) lets the one thread whose
+// range crosses k resolve the bin.
 __device__ int find_bin_desc(const uint32_t *hist, int nbins, uint32_t k, uint32_t *need,
                              uint32_t *scratch) {
-  // suffix sums computed serially by wave 0 in strided chunks: nbins <= 2048.
-  __shared__ uint32_t chunk_sum[64];
   __shared__ int found_bin;
   __shared__ uint32_t found_need;
-  const int per = nbins / 64;
-  if (threadIdx.x < 64) {
-    uint32_t s = 0;
-    const int hi = nbins - threadIdx.x * per;  // chunk covers bins [hi-per, hi)
-    for (int b = hi - 1; b >= hi - per; --b) s += hist[b];
-    chunk_sum[threadIdx.x] = s;
+  const int per = nbins / (int)blockDim.x;          // 2 (2048 bins) or 1 (1024 bins)
+  const int top = nbins - 1 - (int)threadIdx.x * per;
+  uint32_t c = 0;
+  for (int j = 0; j < per; ++j) c += hist[top - j];
+  // inclusive wave scan
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  uint32_t inc = c;
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t v = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += v;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t above = 0;
-    int c = 0;
-    for (; c < 64; ++c) {
-      if (above + chunk_sum[c] >= k) break;
-      above += chunk_sum[c];
-    }
-    const int hi = nbins - c * per;
-    int b = hi - 1;
-    for (; b >= hi - per; --b) {
+  if (lane == 63) scratch[w] = inc;
+  __syncthreads();
+  uint32_t before = 0;
+  for (int i = 0; i < w; ++i) before += scratch[i];
+  const uint32_t excl = before + inc - c;          // elements in bins above my range
+  if (excl < k && excl + c >= k) {
+    uint32_t above = excl;
+    int b = top;
+    for (int j = 0; j < per; ++j, --b) {
       if (above + hist[b] >= k) break;
       above += hist[b];
     }
@@ -201,6 +208,26 @@ __device__ int find_bin_desc(const uint32_t *hist, int nbins, uint32_t k, uint32
   __syncthreads();
   *need = found_need;
   return found_bin;
+}
+
+// Visit keys[0..S) with the whole block: 16-byte loads, four per thread in
+// flight before any is used, so a pass costs a few memory latencies, not S/1024.
+template <typename F>
+__device__ __forceinline__ void scan_keys(const uint32_t *keys, int S, F f) {
+  const int S4 = S & ~3;
+  const uint4 *k4 = (const uint4 *)keys;  // keys rows are 16-byte aligned (max_seq % 4 == 0)
+  constexpr int UNR = 4;
+  for (int base = threadIdx.x; base * 4 < S4; base += blockDim.x * UNR) {
+    uint4 v[UNR];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int i = base + u * blockDim.x;
+      v[u] = i * 4 < S4 ? k4[i] : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) { f(v[u].x); f(v[u].y); f(v[u].z); f(v[u].w); }
+  }
+  for (int t = S4 + threadIdx.x; t < S; t += blockDim.x) f(keys[t]);
 }
 
 // grid R, 1024 threads.
@@ -230,16 +257,15 @@ __global__ void __launch_bounds__(1024) keep_select_kernel(KeepArgs a) {
     }
     return;
   }
-  const uint32_t *keys = a.keys + (int64_t)r * a.max_seq;
+  const uint32_t *keys = a.keys + (int64_t)r * a.keys_sr;
   uint32_t need;
   const int b1 = find_bin_desc(hist, HIST_BINS, k, &need, scratch);
   // pass 2: bits [20:10] among keys whose top 11 bits == b1
   for (int b = threadIdx.x; b < HIST_BINS; b += blockDim.x) hist[b] = 0;
   __syncthreads();
-  for (int t = threadIdx.x; t < S; t += blockDim.x) {
-    const uint32_t key = keys[t];
+  scan_keys(keys, S, [&](uint32_t key) {
     if (key != 0 && (int)(key >> 21) == b1) atomicAdd(&hist[(key >> 10) & 2047u], 1u);
-  }
+  });
   __syncthreads();
   uint32_t need2;
   const int b2 = find_bin_desc(hist, HIST_BINS, need, &need2, scratch);
@@ -247,10 +273,9 @@ __global__ void __launch_bounds__(1024) keep_select_kernel(KeepArgs a) {
   const uint32_t pre22 = ((uint32_t)b1 << 11) | (uint32_t)b2;
   for (int b = threadIdx.x; b < HIST_BINS; b += blockDim.x) hist[b] = 0;
   __syncthreads();
-  for (int t = threadIdx.x; t < S; t += blockDim.x) {
-    const uint32_t key = keys[t];
+  scan_keys(keys, S, [&](uint32_t key) {
     if (key != 0 && (key >> 10) == pre22) atomicAdd(&hist[key & 1023u], 1u);
-  }
+  });
   __syncthreads();
   uint32_t need3;
   const int b3 = find_bin_desc(hist, 1024, need2, &need3, scratch);
@@ -302,7 +327,7 @@ __global__ void __launch_bounds__(256) keep_write_kernel(KeepArgs a) {
   const int cut = sel[1];
   bool kp = false;
   if (t < S) {
-    const uint32_t key = a.keys[(int64_t)r * a.max_seq + t];
+    const uint32_t key = a.keys[(int64_t)r * a.keys_sr + t];
     kp = key == 0 || key > thr || (key == thr && t < cut);
     a.keep[(int64_t)r * a.keep_sr + t] = kp ? 1 : 0;
   }
@@ -358,7 +383,8 @@ using namespace actkv;
 
 extern "C" size_t actkv_workspace_size(int kind, int R, int max_seq) {
   if (kind != ACTKV_WS_KEEP_MASK || R < 1 || max_seq < 0) return 0;
-  return align256((size_t)R * max_seq * 4) + align256((size_t)R * HIST_BINS * 4) +
+  const size_t keys_sr = ((size_t)max_seq + 3) & ~(size_t)3;
+  return align256((size_t)R * keys_sr * 4) + align256((size_t)R * HIST_BINS * 4) +
          align256((size_t)R * 16);
 }
 
@@ -389,18 +415,20 @@ extern "C" int actkv_keep_mask(const void *scores, int scores_dtype, int64_t s_s
   a.keep = keep; a.keep_sr = keep_sr; a.bits = keep_bits; a.bits_sr = bits_sr;
   a.BS = block_size; a.max_seq = max_seq;
   unsigned char *ws = (unsigned char *)workspace;
+  a.keys_sr = ((int64_t)max_seq + 3) & ~(int64_t)3;
+  const size_t keys_bytes = align256((size_t)R * a.keys_sr * 4);
   a.keys = (uint32_t *)ws;
-  a.hist = (uint32_t *)(ws + align256((size_t)R * max_seq * 4));
-  a.sel = (int32_t *)(ws + align256((size_t)R * max_seq * 4) + align256((size_t)R * HIST_BINS * 4));
+  a.hist = (uint32_t *)(ws + keys_bytes);
+  a.sel = (int32_t *)(ws + keys_bytes + align256((size_t)R * HIST_BINS * 4));
 
   const int64_t nh = (int64_t)R * HIST_BINS;
   hipLaunchKernelGGL(zero_u32_kernel, dim3((unsigned)((nh + 255) / 256)), dim3(256), 0, st, a.hist, nh);
   dim3 g1((max_seq + 63) / 64, R);
   const size_t shm = (size_t)L * 64 * sizeof(float);
   switch (scores_dtype) {
-    case ACTKV_F32: hipLaunchKernelGGL(keep_reduce_kernel<float>, g1, dim3(256), shm, st, a); break;
-    case ACTKV_F16: hipLaunchKernelGGL(keep_reduce_kernel<_Float16>, g1, dim3(256), shm, st, a); break;
-    default: hipLaunchKernelGGL(keep_reduce_kernel<__bf16>, g1, dim3(256), shm, st, a); break;
+    case ACTKV_F32: hipLaunchKernelGGL(keep_reduce_kernel<float>, g1, dim3(REDUCE_THREADS), shm, st, a); break;
+    case ACTKV_F16: hipLaunchKernelGGL(keep_reduce_kernel<_Float16>, g1, dim3(REDUCE_THREADS), shm, st, a); break;
+    default: hipLaunchKernelGGL(keep_reduce_kernel<__bf16>, g1, dim3(REDUCE_THREADS), shm, st, a); break;
   }
   int rc = actkv_check_launch();
   if (rc) return rc;

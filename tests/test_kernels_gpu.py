@@ -326,3 +326,34 @@ def test_action_scores_every_layer_in_one_launch():
         ref.action_scores_nfold(q[l], kvs[l], tables, lens, lse[l], want, torch.zeros(2, dtype=torch.int32))
         torch.testing.assert_close(out[l].cpu(), want, rtol=1e-3, atol=1e-6)
     assert n_seen.tolist() == [n_q, n_q]
+
+
+@pytest.mark.parametrize("L,H,S,W,budget,prot,reduce", [
+    (36, 8, 4096, 4096, 409, 4, "mean"),     # Qwen3-8B layer/head counts
+    (36, 8, 3001, 3072, 300, 0, "mean"),     # S not a multiple of 32: torch's tail-column order
+    (20, 8, 1000, 1024, 100, 7, "max"),
+    (1, 8, 777, 800, 77, 4, "mean"),
+    (3, 3, 200, 200, 20, 0, "mean"),
+    (40, 16, 513, 520, 64, 2, "mean"),       # 16 heads: a full cascade block per layer
+])
+def test_keep_mask_bit_exact_with_the_oracle(L, H, S, W, budget, prot, reduce):
+    """The device reduction reproduces torch's CPU mean bit for bit, so the keep mask equals
+    the oracle's on the same scores (distinct scores: no top-k ties)."""
+    g = torch.Generator().manual_seed(L * 1000 + S)
+    scores = torch.rand(L, H, W, generator=g) * torch.exp(torch.randn(L, H, W, generator=g))
+    want = ref.keep_mask_from_scores(scores, S, budget, protected=prot, head_reduce=reduce)
+    got = keep_mask_from_scores(scores.cuda(), S, budget, protected=prot, head_reduce=reduce).cpu()
+    assert torch.equal(got, want)
+    assert int(got.sum()) == min(prot, S) + budget
+
+
+def test_keep_mask_ties_keep_the_lower_index():
+    """Equal scores straddling the top-k boundary: the lower index wins (documented rule)."""
+    S = 5000
+    scores = torch.zeros(2, 4, S)
+    scores[..., 100:1100] = 0.5                      # 1000 tied candidates, 300 of them kept
+    scores[..., 3000:3050] = 1.0                     # 50 strictly higher
+    keep = keep_mask_from_scores(scores.cuda(), S, 350, protected=3).cpu()
+    want = ref.keep_mask_lowest_index_ties(scores, S, 350, protected=3)
+    assert torch.equal(keep, want)
+    assert keep[:3].all() and keep[3000:3050].all() and keep[100:400].all() and not keep[400:1100].any()

@@ -1,0 +1,94 @@
+"""The C ABI library: it is built, loads, exports every entry point include/actkv.h declares, and
+rejects invalid arguments before any device work (these calls never reach a kernel launch)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from actkv import _hip
+
+ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
+HEADER = os.path.join(ROOT, "include", "actkv.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(actkv_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_is_built_and_loads():
+    assert os.path.exists(_hip.LIB_PATH), "run python actkv-open_amd/build_lib.py"
+    assert _hip.lib().actkv_version().decode().startswith("actkv-hip")
+
+
+def test_every_declared_entry_point_is_exported():
+    names = _declared()
+    assert {"actkv_action_scores", "actkv_copy_slots", "actkv_keep_mask", "actkv_pack_keep",
+            "actkv_compact", "actkv_workspace_size", "actkv_error_string"} <= set(names)
+    lib = ctypes.CDLL(_hip.LIB_PATH)
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/actkv.h but not exported"
+    out = subprocess.run(["nm", "-D", "--defined-only", _hip.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (actkv_[a-z_0-9]+)$", out, flags=re.M))
+    assert exported == set(names), f"exported but undeclared: {exported - set(names)}"
+
+
+def test_status_strings():
+    lib = _hip.lib()
+    assert lib.actkv_error_string(0) == b"ACTKV_OK"
+    assert lib.actkv_error_string(1) == b"ACTKV_ERR_INVALID_ARG"
+    assert lib.actkv_error_string(2) == b"ACTKV_ERR_UNSUPPORTED"
+    assert lib.actkv_error_string(3) == b"ACTKV_ERR_WORKSPACE"
+    assert lib.actkv_error_string(4) == b"ACTKV_ERR_LAUNCH"
+    assert lib.actkv_error_string(99) == b"ACTKV_ERR_UNKNOWN"
+
+
+def test_workspace_size():
+    ws = _hip.lib().actkv_workspace_size
+    assert ws(_hip.WS_KEEP_MASK, 1, 32768) >= 32768 * 4 + 2048 * 4
+    assert ws(_hip.WS_KEEP_MASK, 8, 65536) > ws(_hip.WS_KEEP_MASK, 1, 65536)
+    assert ws(_hip.WS_KEEP_MASK, 0, 10) == 0 and ws(7, 1, 10) == 0
+
+
+@pytest.mark.skipif(_hip.torch.cuda.is_available(),
+                    reason="passes unmapped pointers that validation must reject; kept off GPU machines")
+def test_invalid_arguments_are_rejected_before_any_launch():
+    lib = _hip.lib()
+    # action_scores: null pointers, GQA mismatch, narrow out
+    args = [None, 2, 0, 0, 0, 0, None, 2, 0, 0, 0, 0, 10, None, 0, 1, None, None, 0, 0, 0,
+            None, 0, 0, 0, 16, None, None, None, 1, 1, 1, 4, 2, 128, 16, 0.1, None]
+    assert lib.actkv_action_scores(*args) == 1
+    fake = 1 << 20  # never dereferenced: validation fails first
+    args = [fake, 2, 0, 0, 0, 0, fake, 2, 0, 0, 0, 0, 10, fake, 0, 1, fake, fake, 0, 0, 0,
+            fake, 0, 0, 0, 16, fake, None, None, 1, 1, 1, 6, 4, 128, 16, 0.1, None]
+    assert lib.actkv_action_scores(*args) == 1          # Hq % Hkv != 0
+    args[33], args[34] = 4, 2
+    args[25] = 8                                         # out narrower than max_blocks * block_size
+    assert lib.actkv_action_scores(*args) == 1
+    # copy_slots: nothing to copy is fine anywhere; bad sizes are rejected
+    assert lib.actkv_copy_slots(None, 1, 0, 0, 16, 1, None, None, 0, None) == 0
+    assert lib.actkv_copy_slots(fake, 0, 0, 0, 16, 1, fake, fake, 3, None) == 1
+    # keep_mask: both protected forms at once, unknown head_reduce, missing workspace
+    km = [fake, 0, 0, 0, 0, 1, 1, 1, fake, fake, fake, fake, 0, 0, fake, 0, None, 0, 16, 100, fake, 1 << 20, None]
+    assert lib.actkv_keep_mask(*km) == 1
+    km[10] = None
+    km[13] = 5
+    assert lib.actkv_keep_mask(*km) == 1
+    km[13] = 0
+    km[20] = None
+    assert lib.actkv_keep_mask(*km) == 3
+    # compact: pinned_in without pinned_out
+    cp = [fake, 2, 0, 0, 16, 10, fake, 1, 1, fake, fake, 1, 16, None, 0, fake, 0, None, 0,
+          None, 0, None, 0, None, None, 0, None, 1, 16, 16, None]
+    assert lib.actkv_compact(*cp) == 1
+
+
+@pytest.mark.parametrize("bad", ["missing"])
+def test_python_layer_fails_loudly_without_the_library(monkeypatch, bad):
+    monkeypatch.setattr(_hip, "LIB_PATH", "/nonexistent/libactkv_hip.so")
+    monkeypatch.setattr(_hip, "_lib", None)
+    with pytest.raises(RuntimeError, match="no CPU or Triton fallback"):
+        _hip.lib()

@@ -13,11 +13,14 @@ head_dim 128, block_size 16, bf16 K/V ~ N(0,1) from a seed, physical blocks rand
 Inputs are resident in HBM when a step starts.  Compaction mutates the cache, so every step
 starts from a restored copy (device copy of kv + the host lists), outside the timed region;
 the restore also overwrites the 256 MB MALL.  Each step is timed with HIP events on the
-current stream; per-phase events give the scoring kernel's duration for the roofline.
+current stream (the library's launch stream), its launches queued behind the restore copy so
+the interval is the GPU's time for the step; the scoring interval inside it is the duration of
+the scoring call the roofline uses.  The same steps timed with the host's launch work exposed
+(a synchronisation before each step) are reported beside it.
 
-The single JSON line also carries the same numbers for one layer (BASELINE config 2 shape),
-the CPU baseline (the oracle's reference-style torch path timed on a bounded sample of the
-same workload on this host) and checks of the step's results.
+The single JSON line also carries the same numbers for one layer (the 32k-token one-layer
+workload), the CPU baseline (the oracle's reference-style torch path timed on a bounded sample
+of the same workload on this host) and checks of the step's results.
 """
 from __future__ import annotations
 
@@ -46,7 +49,7 @@ def log(msg):
 def parse(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--seq", type=int, default=32768)
@@ -58,7 +61,7 @@ def parse(argv=None):
     ap.add_argument("--keep", type=float, default=0.10)
     ap.add_argument("--sinks", type=int, default=4)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--cpu-folds", type=int, default=32, help="action-query folds in the CPU baseline sample")
+    ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-single-layer", action="store_true", help="skip the one-layer measurement")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "score_kernel_traffic.json"),
@@ -149,26 +152,45 @@ class Workload:
 
 
 def measure(w, steps, warmup):
+    """Time `steps` eviction steps between two device synchronisations.
+
+    Each step starts from a restored cache.  The restore (a device copy of the whole cache) is
+    queued first and the step's launches are queued behind it with no synchronisation, so the
+    host prepares the step while the GPU copies, as a serving loop prepares step i+1 while step
+    i runs.  Events on the launch stream bracket each step (start, after scoring, end): the step
+    interval is the GPU's time for the step, and the scoring interval is the scoring call itself
+    (kernel + n_seen bump) with no host gap in it.
+
+    The same steps are then timed once more with a synchronisation before each step, so the
+    host's launch work is exposed; that figure is reported beside the first."""
     import torch
     for _ in range(warmup):
         w.restore()
         w.step()
     torch.cuda.synchronize()
-    t_step, t_score, t_evict = [], [], []
+    evs = []
     wall0 = time.perf_counter()
+    for _ in range(steps):
+        w.restore()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        w.step(ev)
+        evs.append(ev)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    t_step = [e[0].elapsed_time(e[2]) * 1e3 for e in evs]
+    t_score = [e[0].elapsed_time(e[1]) * 1e3 for e in evs]
+    t_evict = [e[1].elapsed_time(e[2]) * 1e3 for e in evs]
+    t_sync = []
     for _ in range(steps):
         w.restore()
         torch.cuda.synchronize()
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         w.step(ev)
         torch.cuda.synchronize()
-        t_step.append(ev[0].elapsed_time(ev[2]) * 1e3)
-        t_score.append(ev[0].elapsed_time(ev[1]) * 1e3)
-        t_evict.append(ev[1].elapsed_time(ev[2]) * 1e3)
-    wall = time.perf_counter() - wall0
+        t_sync.append(ev[0].elapsed_time(ev[2]) * 1e3)
     return {"step_us": statistics.mean(t_step), "step_us_median": statistics.median(t_step),
             "score_us": statistics.mean(t_score), "evict_us": statistics.mean(t_evict),
-            "wall_s_incl_restore": wall}
+            "step_us_sync": statistics.mean(t_sync), "wall_s_incl_restore": wall}
 
 
 def check_step(w):
@@ -200,34 +222,50 @@ def check_step(w):
             "layer0_rows_match": ok_rows, "allocator_state_ok": ok_host}, int(src.size), int(drop)
 
 
-def cpu_baseline(w, folds):
-    """The oracle's reference-style torch CPU path on a bounded sample: `folds` action-query folds
-    of one layer (one query per fold, as the reference), then keep mask + compaction of that layer;
-    extrapolated linearly to the whole step (L layers x N folds)."""
-    import numpy as np
+def cpu_baseline(w, layers):
+    """The oracle's reference-style torch CPU path on a bounded sample of the step: all N
+    action-query folds (one query per fold, as the reference) of the first `layers` layers, then
+    the keep mask over those layers and the compaction of their K/V planes; extrapolated
+    linearly in the layer count to the whole step."""
     import torch
     from oracle import reference as ref
 
-    kv_l = w.kv0[0].cpu()
+    ls = max(1, min(layers, w.L))
     table = [w.host0[1][0]]
-    q = w.q[0, 0].cpu()            # [N, Hq, D]
-    lse = w.lse[0, 0].cpu()        # [N, Hq]
-    out = torch.zeros(1, w.hkv, w.width)
-    ns = torch.zeros(1, dtype=torch.int32)
-    folds = min(folds, w.N)
-    t0 = time.perf_counter()
-    for n in range(folds):
-        ref.action_scores_fold(q[n:n + 1], kv_l, table, [w.S], lse[n:n + 1], out, ns)
-    t_fold = (time.perf_counter() - t0) / folds
-    model = ref.PagedCacheModel(w.nb, w.bs, w.hkv, w.d, 1)
-    model.kv = kv_l.unsqueeze(0).view(torch.int16).numpy().copy()
+    out = torch.zeros(ls, w.hkv, w.width)
+    t_fold = 0.0
+    kv_cpu = []
+    for l in range(ls):
+        kv_l = w.kv0[l].cpu()
+        kv_cpu.append(kv_l)
+        q = w.q[l, 0].cpu()            # [N, Hq, D]
+        lse = w.lse[l, 0].cpu()        # [N, Hq]
+        ns = torch.zeros(1, dtype=torch.int32)
+        o = out[l:l + 1]
+        t0 = time.perf_counter()
+        for n in range(w.N):
+            ref.action_scores_fold(q[n:n + 1], kv_l, table, [w.S], lse[n:n + 1], o, ns)
+        t_fold += time.perf_counter() - t0
+    model = ref.PagedCacheModel(w.nb, w.bs, w.hkv, w.d, ls)
+    model.kv = torch.stack(kv_cpu).view(torch.int16).numpy().copy()
     model.free, model.tables, model.seq_used = list(w.host0[0]), {0: list(table[0])}, {0: w.S}
     t1 = time.perf_counter()
-    model.evict(0, out[0], w.budget, protected=w.args.sinks)
-    t_evict_layer = time.perf_counter() - t1
-    total_s = w.L * (w.N * t_fold + t_evict_layer)
-    return {"t_fold_s": t_fold, "t_evict_one_layer_s": t_evict_layer, "extrapolated_step_s": total_s,
-            "threads": torch.get_num_threads(), "sample_s": folds * t_fold + t_evict_layer}
+    model.evict(0, out, w.budget, protected=w.args.sinks)
+    t_evict = time.perf_counter() - t1
+    sample = t_fold + t_evict
+    return {"layers": ls, "t_fold_s": t_fold, "t_evict_s": t_evict, "sample_s": sample,
+            "extrapolated_step_s": sample * w.L / ls, "threads": torch.get_num_threads()}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def load_traffic(path):
@@ -260,16 +298,17 @@ def main(argv=None):
     log(f"checks {checks}; timing {args.warmup} + {args.steps} steps")
     work = w.algorithmic(moved, drop)
     m = measure(w, args.steps, args.warmup)
+    k_us = m["score_us"]
     total_bytes = work["bytes_score"] + work["bytes_keep"] + work["bytes_compact"]
     gbs = total_bytes / (m["step_us"] * 1e-6) / 1e9
-    score_tflops = work["flops_score"] / (m["score_us"] * 1e-6) / 1e12
+    score_tflops = work["flops_score"] / (k_us * 1e-6) / 1e12
     traffic = load_traffic(args.traffic)
     traffic_bytes = None
     if traffic and traffic.get("layers") == args.layers and traffic.get("seq") == args.seq \
             and traffic.get("queries") == args.queries:
         traffic_bytes = traffic.get("hbm_bytes_per_launch")
 
-    log(f"step {m['step_us']:.1f} us, score {m['score_us']:.1f} us")
+    log(f"step {m['step_us']:.1f} us (synchronised launches {m['step_us_sync']:.1f} us), scoring call {k_us:.1f} us")
     single = None
     if not args.no_single_layer and args.layers != 1:
         log("one-layer workload")
@@ -288,15 +327,16 @@ def main(argv=None):
 
     cpu = None
     if not args.no_cpu:
-        log(f"CPU baseline sample ({args.cpu_folds} folds of one layer)")
-        c = cpu_baseline(w, args.cpu_folds)
+        log(f"CPU baseline sample ({args.cpu_layers} layers)")
+        c = cpu_baseline(w, args.cpu_layers)
         cpu = {"value": round(total_bytes / c["extrapolated_step_s"] / 1e9, 4), "unit": "GB/s",
                "cores": c["threads"], "kind": "port",
-               "sample": (f"1 of {args.layers} layers x {min(args.cpu_folds, args.queries)} of {args.queries} "
-                          f"one-query folds (reference torch fold per action token) + keep mask + compaction "
-                          f"of that layer, {c['sample_s']:.1f} s; extrapolated linearly to the whole step "
-                          f"({c['extrapolated_step_s']:.0f} s)"),
-               "step_s_extrapolated": round(c["extrapolated_step_s"], 1)}
+               "sample": (f"{c['layers']} of {args.layers} layers: all {args.queries} one-query folds "
+                          f"(reference torch fold per action token, {c['t_fold_s']:.1f} s) + keep mask + "
+                          f"compaction of those layers ({c['t_evict_s']:.2f} s); extrapolated linearly in "
+                          f"layers to the whole step ({c['extrapolated_step_s']:.0f} s)"),
+               "step_s_extrapolated": round(c["extrapolated_step_s"], 1), "cpu_model": cpu_model(),
+               "os_cpu_count": os.cpu_count()}
 
     result = {
         "metric": "score+compact HBM GB/s (% of 8 TB/s) and evict us/layer, Qwen3-8B shape 32k",
@@ -314,12 +354,14 @@ def main(argv=None):
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "evict_us_per_layer": round(m["step_us"] / args.layers, 3),
         "phases_us": {"score": round(m["score_us"], 2), "keep_mask+compact": round(m["evict_us"], 2),
-                      "step_median": round(m["step_us_median"], 2)},
+                      "step_median": round(m["step_us_median"], 2),
+                      "step_with_host_launch_exposed": round(m["step_us_sync"], 2)},
         "algorithmic": work,
         "roofline": {"kernel": "score_mfma_kernel (actkv_action_scores)", "bound": "mfma",
                      "achieved": round(score_tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(score_tflops / BF16_PEAK_TFLOPS, 4), "traffic": traffic_bytes,
-                     "hbm_GBps_algorithmic": round(work["bytes_score"] / (m["score_us"] * 1e-6) / 1e9, 1)},
+                     "launch_us": round(k_us, 2),
+                     "hbm_GBps_algorithmic": round(work["bytes_score"] / (k_us * 1e-6) / 1e9, 1)},
         "cpu_baseline": cpu,
         "single_layer": single,
         "checks": checks,

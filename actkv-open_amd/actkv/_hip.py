@@ -51,7 +51,7 @@ _SIGNATURES = {
         _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,            # kv planes sp ss row_bytes num_blocks
         _c_p, _c_i64, _c_i32, _c_p,                              # bits bits_sr R seq_used
         _c_p, _c_i64, _c_i32,                                    # block_table bt_sr bs
-        _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_i64,                # perm pin_in pin_out
+        _c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64,          # perm pin_in pin_count pin_out
         _c_p, _c_i64, _c_p, _c_i64,                              # table_out freed
         _c_p, _c_p, _c_i64, _c_p,                                # src_out dst_out pairs_sr counts
         _c_i32, _c_i32, _c_i32, _c_p]),                          # do_copy max_seq max_kept stream

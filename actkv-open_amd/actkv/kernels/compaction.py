@@ -81,7 +81,7 @@ def plan_compaction(keep_mask: torch.Tensor, seq_used: int, block_table_row: tor
         None, 0, 0, 0, 0, 2**31 - 1,
         bits.data_ptr(), bits.shape[1], 1, seq.data_ptr(),
         bt.data_ptr(), bt.shape[1], block_size,
-        perm.data_ptr(), cap, None, 0, None, 0,
+        perm.data_ptr(), cap, None, 0, None, None, 0,
         None, 0, None, 0,
         src.data_ptr(), dst.data_ptr(), cap, counts.data_ptr(),
         0, seq_used, seq_used, st), "actkv_compact(plan)")

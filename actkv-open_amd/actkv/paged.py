@@ -296,9 +296,10 @@ class PagedKVCache:
         self._pin_count[req] = (pinned, pinned._version, cnt)
         return cnt
 
-    def _compact_launch(self, reqs, bits, kept, pinned_in=None):
+    def _compact_launch(self, reqs, bits, kept, pinned_in=None, pin_count=None):
         """One actkv_compact launch over `reqs` with packed keep bits [R, words] and host-known
         kept counts; then the host allocator updates in request order (sequential semantics).
+        pinned_in [R, >=S] bool or pin_count [R] int32 (device) gives the pinned tokens.
         Returns perm [R, max(kept)] int64 and pinned_out [R, max(kept)] bool (or None)."""
         dev = self.kv.device
         bs = self.block_size
@@ -309,7 +310,8 @@ class PagedKVCache:
         mb = bt_dev.shape[1]
         bmax = max(max(kept), 1)
         perm = torch.empty(r_n, bmax, dtype=torch.int64, device=dev)
-        pin_out = None if pinned_in is None else torch.empty(r_n, bmax, dtype=torch.bool, device=dev)
+        pin_out = (None if pinned_in is None and pin_count is None
+                   else torch.empty(r_n, bmax, dtype=torch.bool, device=dev))
         es = self.kv.element_size()
         row = self.n_kv_heads * self.head_dim
         flat = self.kv.view(self.n_layers * 2, -1, row)
@@ -318,7 +320,7 @@ class PagedKVCache:
             bits.data_ptr(), bits.stride(0), r_n, seq_dev.data_ptr(),
             bt_dev.data_ptr(), mb, bs,
             perm.data_ptr(), bmax, _hip.ptr(pinned_in), 0 if pinned_in is None else pinned_in.stride(0),
-            _hip.ptr(pin_out), bmax,
+            _hip.ptr(pin_count), _hip.ptr(pin_out), bmax,
             None, 0, None, 0, None, None, 0, None,
             1, max(seqs), max(kept), _hip.stream(dev))
         _hip.check(rc, "actkv_compact")
@@ -382,13 +384,25 @@ class PagedKVCache:
         prots = list(protected) if isinstance(protected, (list, tuple)) else [protected] * r_n
         dev = self.kv.device
         out = [None] * r_n
-        active, pinneds, kept = [], [], []
+        active, pinneds, kept, counts = [], [], [], []
         for i, req in enumerate(reqs):
             n = self.seq_used[req]
             pinned = self.pinned.get(req)
             if pinned is None:
-                pinned = torch.arange(n, device=dev) < prots[i]
-                self._pin_count[req] = (pinned, pinned._version, min(max(int(prots[i]), 0), n))
+                # first eviction: the protected prefix is a count; the kernels build the
+                # mask of the survivors themselves (no device mask needed beforehand)
+                cnt = min(max(int(prots[i]), 0), n)
+                if n - cnt <= budgets[i]:
+                    pinned = torch.arange(n, device=dev) < prots[i]
+                    self.pinned[req] = pinned
+                    self._pin_count[req] = (pinned, pinned._version, cnt)
+                    out[i] = torch.arange(n, device=dev)
+                    continue
+                active.append(i)
+                pinneds.append(None)
+                kept.append(cnt + max(budgets[i], 0))
+                counts.append(cnt)
+                continue
             cnt = self._pinned_count(req, pinned)
             if pinned.numel() < n:                      # tokens appended since
                 pinned = torch.cat([pinned, pinned.new_zeros(n - pinned.numel())])
@@ -400,6 +414,7 @@ class PagedKVCache:
             active.append(i)
             pinneds.append(pinned)
             kept.append(cnt + max(budgets[i], 0))
+            counts.append(cnt)
         if not active:
             return out
         _hip.require_gpu("PagedKVCache.evict", self.kv)
@@ -440,21 +455,29 @@ class PagedKVCache:
         if sc.stride(-1) != 1:
             sc = sc.contiguous()
         L, _, H, _ = sc.shape
-        if ra == 1:
-            pin_mat = pinneds[0].view(1, -1)
+        params = upload_i32(seqs + [max(budgets[i], 0) for i in active] + counts, dev)
+        if all(p is None for p in pinneds):           # every request's pins are a prefix count
+            pin_mat, prot_count = None, params[2 * ra:]
         else:
-            pin_mat = torch.zeros(ra, smax, dtype=torch.bool, device=dev)
-            for j, p in enumerate(pinneds):
-                pin_mat[j, : p.numel()] = p
-        params = upload_i32(seqs + [max(budgets[i], 0) for i in active], dev)
+            prot_count = None
+            if ra == 1:
+                pin_mat = pinneds[0].view(1, -1)
+            else:
+                pin_mat = torch.zeros(ra, smax, dtype=torch.bool, device=dev)
+                for j, p in enumerate(pinneds):
+                    if p is None:
+                        pin_mat[j, : counts[j]] = True
+                    else:
+                        pin_mat[j, : p.numel()] = p
         _, bits = _keep_mask_launch(sc, L, H, sc.stride(0), sc.stride(1), sc.stride(2), ra,
-                                    params[:ra], params[ra:], None, pin_mat, pin_mat.stride(0),
+                                    params[:ra], params[ra:2 * ra], prot_count, pin_mat,
+                                    0 if pin_mat is None else pin_mat.stride(0),
                                     head_reduce, self.block_size, smax, dev)
-        perm, pin_out = self._compact_launch(a_reqs, bits, kept, pin_mat)
+        perm, pin_out = self._compact_launch(a_reqs, bits, kept, pin_mat, prot_count)
         for j, i in enumerate(active):
             b = kept[j]
             out[i] = perm[j, :b]
             newpin = pin_out[j, :b]
             self.pinned[reqs[i]] = newpin
-            self._pin_count[reqs[i]] = (newpin, newpin._version, self._pin_count[reqs[i]][2])
+            self._pin_count[reqs[i]] = (newpin, newpin._version, counts[j])
         return out

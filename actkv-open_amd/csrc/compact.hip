@@ -37,6 +37,7 @@ struct CompactArgs {
   int64_t perm_sr;
   const uint8_t *pin_in;
   int64_t pin_sr;
+  const int32_t *pin_count;  // instead of pin_in: positions < pin_count[r] are pinned
   uint8_t *pin_out;
   int64_t pout_sr;
   int32_t *table_out;
@@ -148,6 +149,11 @@ __device__ __forceinline__ void copy_rows(unsigned char *kv, int64_t sp, int64_t
   }
 }
 
+// Pinned flag of old logical position pos of request r.
+__device__ __forceinline__ uint8_t pin_of(const CompactArgs &a, int r, int pos) {
+  return a.pin_in ? a.pin_in[(int64_t)r * a.pin_sr + pos] : (uint8_t)(pos < a.pin_count[r]);
+}
+
 // grid (tiles, plane groups, R), CT threads, dynamic LDS 2*(max_words+1) words.
 template <typename U>
 __global__ void __launch_bounds__(CT) compact_kernel(CompactArgs a) {
@@ -195,7 +201,7 @@ __global__ void __launch_bounds__(CT) compact_kernel(CompactArgs a) {
       }
       if (lead) {
         if (a.perm) a.perm[(int64_t)r * a.perm_sr + (dst - start)] = src;
-        if (a.pin_out) a.pin_out[(int64_t)r * a.pout_sr + (dst - start)] = a.pin_in[(int64_t)r * a.pin_sr + src];
+        if (a.pin_out) a.pin_out[(int64_t)r * a.pout_sr + (dst - start)] = pin_of(a, r, src);
         if (a.src_out) a.src_out[(int64_t)r * a.pairs_sr + i] = sslot;
         if (a.dst_out) a.dst_out[(int64_t)r * a.pairs_sr + i] = dslot;
       }
@@ -208,7 +214,7 @@ __global__ void __launch_bounds__(CT) compact_kernel(CompactArgs a) {
       const int pos = start + j;
       if ((words[pos >> 5] >> (pos & 31)) & 1u) {
         if (a.perm) a.perm[(int64_t)r * a.perm_sr + j] = pos;
-        if (a.pin_out) a.pin_out[(int64_t)r * a.pout_sr + j] = a.pin_in[(int64_t)r * a.pin_sr + pos];
+        if (a.pin_out) a.pin_out[(int64_t)r * a.pout_sr + j] = pin_of(a, r, pos);
       }
     }
   }
@@ -321,7 +327,8 @@ extern "C" int actkv_compact(void *kv, int64_t planes, int64_t stride_plane_byte
                              const uint32_t *keep_bits, int64_t bits_sr, int R,
                              const int32_t *seq_used, const int32_t *block_table, int64_t bt_sr,
                              int block_size, int64_t *perm_out, int64_t perm_sr,
-                             const uint8_t *pinned_in, int64_t pin_sr, uint8_t *pinned_out,
+                             const uint8_t *pinned_in, int64_t pin_sr, const int32_t *pin_count,
+                             uint8_t *pinned_out,
                              int64_t pout_sr, int32_t *table_out, int64_t tout_sr,
                              int32_t *freed_out, int64_t freed_sr, int64_t *src_out,
                              int64_t *dst_out, int64_t pairs_sr, int32_t *counts_out, int do_copy,
@@ -330,7 +337,9 @@ extern "C" int actkv_compact(void *kv, int64_t planes, int64_t stride_plane_byte
       max_kept < 0)
     return ACTKV_ERR_INVALID_ARG;
   if (do_copy && (!kv || planes < 1 || row_bytes < 1)) return ACTKV_ERR_INVALID_ARG;
-  if ((pinned_out != nullptr) != (pinned_in != nullptr)) return ACTKV_ERR_INVALID_ARG;
+  // pinned_out needs exactly one source: a mask or a leading count
+  if (pinned_in && pin_count) return ACTKV_ERR_INVALID_ARG;
+  if ((pinned_out != nullptr) != (pinned_in != nullptr || pin_count != nullptr)) return ACTKV_ERR_INVALID_ARG;
   const int64_t padded = ((int64_t)(max_seq + block_size - 1) / block_size) * block_size;
   const int64_t max_words = (padded + 31) / 32;
   const size_t shm = (size_t)(2 * max_words + 2) * sizeof(uint32_t);
@@ -340,7 +349,7 @@ extern "C" int actkv_compact(void *kv, int64_t planes, int64_t stride_plane_byte
   a.ss = stride_slot_bytes; a.row_bytes = row_bytes; a.num_blocks = num_blocks;
   a.bits = keep_bits; a.bits_sr = bits_sr; a.R = R; a.seq_used = seq_used;
   a.bt = block_table; a.bt_sr = bt_sr; a.BS = block_size;
-  a.perm = perm_out; a.perm_sr = perm_sr; a.pin_in = pinned_in; a.pin_sr = pin_sr;
+  a.perm = perm_out; a.perm_sr = perm_sr; a.pin_in = pinned_in; a.pin_sr = pin_sr; a.pin_count = pin_count;
   a.pin_out = pinned_out; a.pout_sr = pout_sr; a.table_out = table_out; a.tout_sr = tout_sr;
   a.freed = freed_out; a.freed_sr = freed_sr; a.src_out = src_out; a.dst_out = dst_out;
   a.pairs_sr = pairs_sr; a.counts = counts_out; a.do_copy = do_copy;

@@ -165,7 +165,10 @@ int actkv_pack_keep(const uint8_t *keep, int64_t keep_sr, int R, const int32_t *
  * allocations that are stream-ordered after it.
  * Outputs (each optional, NULL to skip; row strides in elements):
  *   perm_out   int64 [R, >=B]: new logical -> old logical (compaction.py:67-68)
- *   pinned_in/pinned_out bool: pinned_out[r, j] = pinned_in[r, perm[j]] (paged.py:156)
+ *   pinned_in/pinned_out bool: pinned_out[r, j] = pinned_in[r, perm[j]] (paged.py:156);
+ *              with pin_count instead of pinned_in (int32 [R], a request's first
+ *              pin_count[r] tokens pinned, paged.py:150-151):
+ *              pinned_out[r, j] = perm[j] < pin_count[r].  At most one of the two.
  *   table_out  int32 [R, >=X]: block_table[r, drop:drop+X] (paged.py:136)
  *   freed_out  int32 [R, >=drop]: freed blocks in free-list push order,
  *              i.e. block_table[r, drop-1-j] (paged.py:135-137)
@@ -180,7 +183,8 @@ int actkv_compact(void *kv, int64_t planes, int64_t stride_plane_bytes,
                   const uint32_t *keep_bits, int64_t bits_sr, int R, const int32_t *seq_used,
                   const int32_t *block_table, int64_t bt_sr, int block_size,
                   int64_t *perm_out, int64_t perm_sr, const uint8_t *pinned_in, int64_t pin_sr,
-                  uint8_t *pinned_out, int64_t pout_sr, int32_t *table_out, int64_t tout_sr,
+                  const int32_t *pin_count, uint8_t *pinned_out, int64_t pout_sr,
+                  int32_t *table_out, int64_t tout_sr,
                   int32_t *freed_out, int64_t freed_sr, int64_t *src_out, int64_t *dst_out,
                   int64_t pairs_sr, int32_t *counts_out, int do_copy, int max_seq, int max_kept,
                   void *stream);

@@ -81,8 +81,11 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     km[20] = None
     assert lib.actkv_keep_mask(*km) == 3
     # compact: pinned_in without pinned_out
-    cp = [fake, 2, 0, 0, 16, 10, fake, 1, 1, fake, fake, 1, 16, None, 0, fake, 0, None, 0,
+    cp = [fake, 2, 0, 0, 16, 10, fake, 1, 1, fake, fake, 1, 16, None, 0, fake, 0, None, None, 0,
           None, 0, None, 0, None, None, 0, None, 1, 16, 16, None]
+    assert lib.actkv_compact(*cp) == 1
+    # compact: both a pinned mask and a pinned count
+    cp[17], cp[18] = fake, fake
     assert lib.actkv_compact(*cp) == 1
 
 

@@ -357,3 +357,23 @@ def test_keep_mask_ties_keep_the_lower_index():
     want = ref.keep_mask_lowest_index_ties(scores, S, 350, protected=3)
     assert torch.equal(keep, want)
     assert keep[:3].all() and keep[3000:3050].all() and keep[100:400].all() and not keep[400:1100].any()
+
+
+def test_batched_evict_mixes_first_and_repeated_evictions():
+    """evict_batch over requests whose pins are a prefix count (first eviction) and requests
+    that carry a pinned mask from an earlier eviction equals sequential oracle evicts."""
+    cache = _filled_cache([90, 120, 75], hkv=2, d=16, layers=2, seed=7)
+    model = _model_of(cache)
+    g = torch.Generator().manual_seed(8)
+    s1 = torch.rand(2, 2, 120, generator=g)
+    cache.evict(1, s1.cuda(), budget=40, protected=6)           # request 1 now has a pinned mask
+    model.evict(1, s1, budget=40, protected=6, tie_rule="lowest")
+    _assert_same_state(cache, model)
+    scores = [torch.rand(2, 2, cache.seq_used[r], generator=g) for r in range(3)]
+    budgets, prots = [30, 20, 25], [5, 9, 0]
+    perms = cache.evict_batch([0, 1, 2], [s.cuda() for s in scores], budgets, prots)
+    for r in range(3):
+        perm_o = model.evict(r, scores[r], budget=budgets[r], protected=prots[r], tie_rule="lowest")
+        assert np.array_equal(perms[r].cpu().numpy(), perm_o), r
+        assert np.array_equal(cache.pinned[r].cpu().numpy(), model.pinned[r]), r
+    _assert_same_state(cache, model)

@@ -275,12 +275,13 @@ static int unit_bytes(const void *base, int64_t sp, int64_t ss, int64_t row_byte
   return 1;
 }
 
-// Pairs per tile and planes per group: about 1024 workgroups, each moving 32 KiB
-// .. 2 MiB, so the per-workgroup plan (scan + selects) stays a small fraction of
-// its row moves.
+// Pairs per tile and planes per group: about 16k workgroups, each moving 32 KiB
+// .. 2 MiB.  Many small workgroups keep the tail of the launch short (every CU
+// stays busy until the end); the per-workgroup plan (scan + selects) stays a
+// small fraction of its row moves.
 static void copy_shape(int64_t max_pairs, int64_t planes, int64_t row_bytes, int *P, int *PG) {
   const int64_t bytes = std::max<int64_t>(1, max_pairs) * planes * row_bytes;
-  int64_t per_wg = std::max<int64_t>(32 * 1024, std::min<int64_t>(2048 * 1024, bytes / 1024));
+  int64_t per_wg = std::max<int64_t>(32 * 1024, std::min<int64_t>(2048 * 1024, bytes / 16384));
   int64_t pairs_cap = std::max<int64_t>(1, per_wg / std::max<int64_t>(1, row_bytes));
   int p = (int)std::min<int64_t>(MAX_PAIRS, std::max<int64_t>(4, std::min<int64_t>(pairs_cap, max_pairs)));
   int64_t pg = std::max<int64_t>(1, per_wg / ((int64_t)p * row_bytes));

@@ -86,7 +86,8 @@ def test_action_scores_matches_oracle(lens, hq, hkv, d, bs, dtype):
 
 
 @pytest.mark.parametrize("n_q,hq,hkv,dtype", [(37, 32, 8, torch.bfloat16), (129, 32, 8, torch.bfloat16),
-                                              (40, 16, 8, torch.float16), (9, 6, 3, torch.float32)])
+                                              (40, 16, 8, torch.float16), (9, 6, 3, torch.float32),
+                                              (300, 16, 8, torch.float16), (600, 8, 8, torch.bfloat16)])
 def test_action_scores_n_queries_in_one_launch(n_q, hq, hkv, dtype):
     """N action tokens folded by one call == N reference folds (additive extension)."""
     lens = [200, 1000, 17]
@@ -275,13 +276,16 @@ def test_evict_keeps_the_protected_tokens_across_repeated_evictions():
     _assert_same_state(cache, model)
 
 
-@pytest.mark.parametrize("dtype,hq,hkv,d,bs", [(torch.bfloat16, 32, 8, 128, 16), (torch.float16, 16, 8, 128, 32),
-                                               (torch.bfloat16, 8, 8, 128, 16), (torch.float32, 6, 3, 24, 8)])
-def test_action_scores_causal_region_and_ragged_query_counts(dtype, hq, hkv, d, bs):
+@pytest.mark.parametrize("dtype,hq,hkv,d,bs,n_q", [
+    (torch.bfloat16, 32, 8, 128, 16, 23), (torch.float16, 16, 8, 128, 32, 23),
+    (torch.bfloat16, 8, 8, 128, 16, 23), (torch.float32, 6, 3, 24, 8, 23),
+    # query tiles of more than 256 rows (the query-stationary kernel)
+    (torch.bfloat16, 32, 8, 128, 16, 100), (torch.float16, 16, 8, 128, 16, 150),
+    (torch.bfloat16, 8, 8, 128, 16, 300)])
+def test_action_scores_causal_region_and_ragged_query_counts(dtype, hq, hkv, d, bs, n_q):
     """kv_len (query n sees tokens t < kv_len[r, n]) and n_valid (request r folds its first
     n_valid[r] queries): the causal action region of an agent round (additive extension)."""
     lens = [700, 90, 1500]
-    n_q = 23
     cache = _filled_cache(lens, bs=bs, hkv=hkv, d=d, dtype=dtype, seed=11)
     reqs = list(range(len(lens)))
     bt, seq = cache.block_table(reqs), cache.seq_tensor(reqs)
@@ -291,7 +295,7 @@ def test_action_scores_causal_region_and_ragged_query_counts(dtype, hq, hkv, d, 
     kv0 = cache.kv[0].cpu()
     tables = [cache.tables[r] for r in reqs]
     lse = torch.stack([ref.decode_lse(q[:, n], kv0, tables, lens) for n in range(n_q)], 1)
-    n_valid = torch.tensor([23, 5, 17], dtype=torch.int32)
+    n_valid = torch.tensor([n_q, 5, 17], dtype=torch.int32)
     kv_len = torch.stack([torch.randint(1, s + 1, (n_q,), generator=g) for s in lens]).to(torch.int32)
     kv_len[0, 3] = lens[0]
     out0 = torch.rand(len(reqs), hkv, width, generator=g)

@@ -56,6 +56,15 @@ _SIGNATURES = {
         _c_p, _c_p, _c_i64, _c_p,                                # src_out dst_out pairs_sr counts
         _c_i32, _c_i32, _c_i32, _c_p]),                          # do_copy max_seq max_kept stream
     "actkv_workspace_size": (_c_sz, [_c_i32, _c_i32, _c_i32]),
+    "actkv_lrfu_update": (_c_i32, [
+        _c_p, _c_i64, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32,   # scores, strides, L H R
+        _c_p, _c_p, _c_p, _c_i64, _c_p,                          # seq_used prot_count prot_mask pm_sr active
+        _c_p, _c_i64, _c_i64,                                    # ks, strides
+        _c_p, _c_i64, _c_i64,                                    # hit_out, strides
+        _c_f, _c_f, _c_i32, _c_i32, _c_p, _c_sz, _c_p]),         # decay top_p reduce max_seq ws stream
+    "actkv_lrfu_workspace_size": (_c_sz, [_c_i32, _c_i32, _c_i32]),
+    "actkv_gather_tokens": (_c_i32, [_c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32,
+                                     _c_p, _c_i64, _c_p, _c_p]),
 }
 
 _lib = None
@@ -117,6 +126,17 @@ def stream(device: torch.device) -> int:
 
 
 _workspaces: dict = {}
+
+
+def scratch(device: torch.device, key, nbytes: int) -> torch.Tensor:
+    """A cached uint8 device buffer of at least nbytes for `key`, grown on demand (contents
+    undefined).  Calls sharing it are ordered on the current stream."""
+    full = (device, key)
+    buf = _workspaces.get(full)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(int(nbytes), 1 << 16), dtype=torch.uint8, device=device)
+        _workspaces[full] = buf
+    return buf
 
 
 def workspace(device: torch.device, kind: int, r: int, max_seq: int) -> torch.Tensor:

@@ -296,10 +296,11 @@ class PagedKVCache:
         self._pin_count[req] = (pinned, pinned._version, cnt)
         return cnt
 
-    def _compact_launch(self, reqs, bits, kept, pinned_in=None, pin_count=None):
+    def _compact_launch(self, reqs, bits, kept, pinned_in=None, pin_count=None, pin_out=None):
         """One actkv_compact launch over `reqs` with packed keep bits [R, words] and host-known
         kept counts; then the host allocator updates in request order (sequential semantics).
-        pinned_in [R, >=S] bool or pin_count [R] int32 (device) gives the pinned tokens.
+        pinned_in [R, >=S] bool or pin_count [R] int32 (device) gives the pinned tokens;
+        pin_out (optional, bool [R, >=max(kept)]) receives the survivors' pins.
         Returns perm [R, max(kept)] int64 and pinned_out [R, max(kept)] bool (or None)."""
         dev = self.kv.device
         bs = self.block_size
@@ -310,8 +311,8 @@ class PagedKVCache:
         mb = bt_dev.shape[1]
         bmax = max(max(kept), 1)
         perm = torch.empty(r_n, bmax, dtype=torch.int64, device=dev)
-        pin_out = (None if pinned_in is None and pin_count is None
-                   else torch.empty(r_n, bmax, dtype=torch.bool, device=dev))
+        if pin_out is None and (pinned_in is not None or pin_count is not None):
+            pin_out = torch.empty(r_n, bmax, dtype=torch.bool, device=dev)
         es = self.kv.element_size()
         row = self.n_kv_heads * self.head_dim
         flat = self.kv.view(self.n_layers * 2, -1, row)
@@ -320,7 +321,7 @@ class PagedKVCache:
             bits.data_ptr(), bits.stride(0), r_n, seq_dev.data_ptr(),
             bt_dev.data_ptr(), mb, bs,
             perm.data_ptr(), bmax, _hip.ptr(pinned_in), 0 if pinned_in is None else pinned_in.stride(0),
-            _hip.ptr(pin_count), _hip.ptr(pin_out), bmax,
+            _hip.ptr(pin_count), _hip.ptr(pin_out), bmax if pin_out is None else pin_out.stride(0),
             None, 0, None, 0, None, None, 0, None,
             1, max(seqs), max(kept), _hip.stream(dev))
         _hip.check(rc, "actkv_compact")

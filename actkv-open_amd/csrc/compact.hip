@@ -265,6 +265,24 @@ __global__ void __launch_bounds__(CT) copy_slots_kernel(unsigned char *kv, int64
   copy_rows<U>(kv, sp, ss, row_bytes, src_slot, dst_slot, np, p0, npl);
 }
 
+// grid (ceil(W/256), L, R): per-token metadata follows the compaction
+// permutation: dst[l, r, i] = src[l, r, perm[r, i]] for i < kept[r], 0 for
+// kept[r] <= i < W (a permutation entry outside [0, W) also reads as 0).
+__global__ void __launch_bounds__(256) gather_tokens_kernel(const float *src, int64_t s_sl, int64_t s_sr,
+                                                            float *dst, int64_t d_sl, int64_t d_sr, int W,
+                                                            const int64_t *perm, int64_t perm_sr,
+                                                            const int32_t *kept) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int l = blockIdx.y, r = blockIdx.z;
+  if (i >= W) return;
+  float v = 0.f;
+  if (i < kept[r]) {
+    const int64_t j = perm[(int64_t)r * perm_sr + i];
+    if (j >= 0 && j < W) v = src[(int64_t)l * s_sl + (int64_t)r * s_sr + j];
+  }
+  dst[(int64_t)l * d_sl + (int64_t)r * d_sr + i] = v;
+}
+
 // Widest access unit dividing every byte offset the copy touches.
 static int unit_bytes(const void *base, int64_t sp, int64_t ss, int64_t row_bytes) {
   const uint64_t m = (uint64_t)(uintptr_t)base | (uint64_t)sp | (uint64_t)ss | (uint64_t)row_bytes;
@@ -292,6 +310,20 @@ static void copy_shape(int64_t max_pairs, int64_t planes, int64_t row_bytes, int
 }  // namespace actkv
 
 using namespace actkv;
+
+extern "C" int actkv_gather_tokens(const float *src, int64_t src_sl, int64_t src_sr, float *dst,
+                                   int64_t dst_sl, int64_t dst_sr, int L, int R, int W,
+                                   const int64_t *perm, int64_t perm_sr, const int32_t *kept,
+                                   void *stream) {
+  if (!src || !dst || !perm || !kept || L < 1 || R < 1 || W < 0) return ACTKV_ERR_INVALID_ARG;
+  if (src == dst) return ACTKV_ERR_INVALID_ARG;  // a gather cannot run in place
+  if (L > 65535 || R > 65535) return ACTKV_ERR_UNSUPPORTED;
+  if (W == 0) return ACTKV_OK;
+  dim3 grid((unsigned)((W + 255) / 256), (unsigned)L, (unsigned)R);
+  hipLaunchKernelGGL(gather_tokens_kernel, grid, dim3(256), 0, (hipStream_t)stream, src, src_sl, src_sr, dst,
+                     dst_sl, dst_sr, W, perm, perm_sr, kept);
+  return actkv_check_launch();
+}
 
 extern "C" int actkv_copy_slots(void *kv_flat, int64_t planes, int64_t stride_plane_bytes,
                                 int64_t stride_slot_bytes, int64_t row_bytes, int64_t num_slots,

@@ -1,0 +1,301 @@
+// LRFU keep-score update (ActKV Algorithm 1 steps 2-4) for the paged cache,
+// gfx950.
+//
+// Reference: actkv/eviction.py:36-50 (top_p_mask) and :209-218
+// (ActionLRFU.update_scores), applied to the paged cache's per-token action
+// scores.  One workgroup per (layer, request) segment:
+//   act[t]  = head reduction (mean in torch's CPU float32 order, or max) of the
+//             action-region scores [Hkv, t] for t < seq_used (eviction.py:20-33)
+//   hit     = nucleus of act over [protected, seq_used): entries taken in
+//             descending order (equal values: lower index first) until the
+//             running sum reaches top_p * total, positive entries only
+//   ks[t]   = decay * ks[t], then + act[t] where hit (two roundings, as
+//             ks.mul_(decay); ks[hit] += a[hit])
+// The nucleus is found without sorting: three radix passes (11/11/10 bits of
+// the float key) over LDS histograms holding, per bin, the count and the
+// float64 sum of the values; walking the bins from the top finds the bin where
+// the running sum crosses the threshold, the last pass fixes the exact value,
+// and the tied entries at that value are taken in index order.  Sums are
+// float64 and compared after rounding to float32, as torch's cumsum stores
+// float64 running sums as float32.
+#include "common.h"
+#include "torch_order.h"
+
+namespace actkv {
+
+constexpr int LT = 1024;        // threads per segment workgroup
+constexpr int LB = 2048;        // histogram bins (passes use 2048, 2048, 1024)
+
+struct LrfuArgs {
+  const float *scores;
+  int64_t s_sl, s_sr, s_sh;
+  int L, H, R;
+  const int32_t *seq_used, *prot, *active;
+  const uint8_t *pmask;  // instead of prot: pinned tokens (excluded, ks untouched)
+  int64_t pm_sr;
+  float *ks;
+  int64_t ks_sl, ks_sr;
+  uint8_t *hit;
+  int64_t hit_sl, hit_sr;
+  float decay, top_p;
+  int head_reduce, max_seq;
+  float *act;  // workspace [L*R, act_sr]
+  int64_t act_sr;
+};
+
+// Block sum of doubles (1024 threads).
+__device__ double block_sum_f64(double v, double *scratch) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[w] = v;
+  __syncthreads();
+  double tot = 0.0;
+  for (int i = 0; i < LT / 64; ++i) tot += scratch[i];
+  __syncthreads();
+  return tot;
+}
+
+// Walk nb bins from the top (bin nb-1 first) with running float64 sum `base`:
+// find the first bin where the rounded running sum reaches thr.  Thread i owns
+// bins nb-1-2i and nb-2-2i.  Returns the bin (or -1 if the sum never reaches
+// thr); *above = base + sum of the bins above it.
+__device__ int crossing_bin(const uint32_t *cnt, const double *sum, int nb, double base, float thr,
+                            double *above, double *scratch_d, int *found) {
+  const int per = nb / LT;  // 2 or 1
+  const int top = nb - 1 - (int)threadIdx.x * per;
+  double s = 0.0;
+  for (int j = 0; j < per; ++j) s += sum[top - j];
+  // inclusive scan over threads in descending-bin order
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  double inc = s;
+  for (int o = 1; o < 64; o <<= 1) {
+    const double v = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += v;
+  }
+  if (threadIdx.x == 0) *found = -1;
+  __syncthreads();
+  if (lane == 63) scratch_d[w] = inc;
+  __syncthreads();
+  double before = base;
+  for (int i = 0; i < w; ++i) before += scratch_d[i];
+  double run = before + inc - s;  // everything above my bins
+  for (int j = 0; j < per; ++j) {
+    const int b = top - j;
+    const double next = run + sum[b];
+    if (cnt[b] != 0 && (float)run < thr && (float)next >= thr) {
+      *found = b;
+      scratch_d[LT / 64] = run;
+    }
+    run = next;
+  }
+  __syncthreads();
+  const int b = *found;
+  if (b >= 0) *above = scratch_d[LT / 64];
+  __syncthreads();
+  return b;
+}
+
+// grid (L, R), LT threads.
+__global__ void __launch_bounds__(LT) lrfu_update_kernel(LrfuArgs a) {
+  __shared__ uint32_t cnt[LB];
+  __shared__ double sum[LB];
+  __shared__ double scratch_d[LT / 64 + 1];
+  __shared__ uint32_t scratch_u[LT / 64];
+  __shared__ int found;
+  __shared__ int cut_s;
+  const int l = blockIdx.x, r = blockIdx.y;
+  const int S = min(max(a.seq_used[r], 0), a.max_seq);
+  // protected tokens: a prefix count, or a pinned mask (then the loops start at 0)
+  const int P = a.prot ? min(max(a.prot[r], 0), S) : 0;
+  const uint8_t *pin = a.pmask ? a.pmask + (int64_t)r * a.pm_sr : nullptr;
+  const bool active = a.active ? a.active[r] != 0 : true;
+  float *act = a.act + ((int64_t)l * a.R + r) * a.act_sr;
+  const float *sbase = a.scores + (int64_t)l * a.s_sl + (int64_t)r * a.s_sr;
+  float *ks = a.ks + (int64_t)l * a.ks_sl + (int64_t)r * a.ks_sr;
+  uint8_t *hit = a.hit ? a.hit + (int64_t)l * a.hit_sl + (int64_t)r * a.hit_sr : nullptr;
+
+  // ---- per-token action score and the float64 total over [P, S)
+  const int body_end = S & ~31;
+  double part = 0.0;
+  for (int t = P + threadIdx.x; t < S; t += LT) {
+    const float *col = sbase + t;
+    float v;
+    if (a.head_reduce == ACTKV_REDUCE_MAX) {
+      v = col[0];
+      for (int hh = 1; hh < a.H; ++hh) v = nanmax(v, col[(int64_t)hh * a.s_sh]);
+    } else {
+      auto ld = [&](int hh) { return col[(int64_t)hh * a.s_sh]; };
+      v = __fdiv_rn(torch_sum(ld, a.H, t < body_end), (float)a.H);
+    }
+    act[t] = v;
+    if (!pin || !pin[t]) part += (double)v;
+  }
+  const double total = block_sum_f64(part, scratch_d);  // (its barriers publish act)
+  const float total_f = (float)total;
+  const float thr = __fmul_rn(a.top_p, total_f);
+  // keys: act >= 0 (means of probabilities), so the float bits order the values
+  uint32_t kthr = 0xFFFFFFFFu;  // hit: key > kthr, or key == kthr and t < cut
+  int cut = 0;
+  if (active && S > P && total_f > 0.f) {
+    // pass 1: top 11 bits
+    for (int b = threadIdx.x; b < LB; b += LT) { cnt[b] = 0; sum[b] = 0.0; }
+    __syncthreads();
+    for (int t = P + threadIdx.x; t < S; t += LT) {
+      if (pin && pin[t]) continue;
+      const float v = act[t];
+      const uint32_t k = __float_as_uint(v);
+      atomicAdd(&cnt[k >> 21], 1u);
+      atomicAdd(&sum[k >> 21], (double)v);
+    }
+    __syncthreads();
+    double above;
+    const int b1 = crossing_bin(cnt, sum, LB, 0.0, thr, &above, scratch_d, &found);
+    if (b1 < 0) {
+      kthr = 0u;          // the sum never reaches the threshold: every positive entry
+      cut = 0;
+    } else {
+      // pass 2: bits [20:10] within bin b1
+      for (int b = threadIdx.x; b < LB; b += LT) { cnt[b] = 0; sum[b] = 0.0; }
+      __syncthreads();
+      for (int t = P + threadIdx.x; t < S; t += LT) {
+        if (pin && pin[t]) continue;
+        const float v = act[t];
+        const uint32_t k = __float_as_uint(v);
+        if ((int)(k >> 21) == b1) {
+          atomicAdd(&cnt[(k >> 10) & 2047u], 1u);
+          atomicAdd(&sum[(k >> 10) & 2047u], (double)v);
+        }
+      }
+      __syncthreads();
+      double above2;
+      int b2 = crossing_bin(cnt, sum, LB, above, thr, &above2, scratch_d, &found);
+      // rounding of the float64 partial sums can only move the crossing by one
+      // bin; fall back to the lowest non-empty bin if it slipped past the end
+      if (b2 < 0) {
+        b2 = 0;
+        above2 = above;
+        for (int b = LB - 1; b >= 0; --b) {
+          if (cnt[b]) { b2 = b; }
+        }
+        double run = above;
+        for (int b = LB - 1; b > b2; --b) run += sum[b];
+        above2 = run;
+      }
+      // pass 3: bits [9:0] within (b1, b2)
+      const uint32_t pre22 = ((uint32_t)b1 << 11) | (uint32_t)b2;
+      for (int b = threadIdx.x; b < LB; b += LT) { cnt[b] = 0; sum[b] = 0.0; }
+      __syncthreads();
+      for (int t = P + threadIdx.x; t < S; t += LT) {
+        if (pin && pin[t]) continue;
+        const float v = act[t];
+        const uint32_t k = __float_as_uint(v);
+        if ((k >> 10) == pre22) {
+          atomicAdd(&cnt[k & 1023u], 1u);
+          atomicAdd(&sum[k & 1023u], (double)v);
+        }
+      }
+      __syncthreads();
+      double above3;
+      int b3 = crossing_bin(cnt, sum, 1024, above2, thr, &above3, scratch_d, &found);
+      if (b3 < 0) {
+        b3 = 0;
+        for (int b = 1023; b >= 0; --b) {
+          if (cnt[b]) { b3 = b; }
+        }
+        double run = above2;
+        for (int b = 1023; b > b3; --b) run += sum[b];
+        above3 = run;
+      }
+      kthr = (pre22 << 10) | (uint32_t)b3;
+      // ties at the crossing value: the j smallest indices, j = first count at which
+      // the running float64 sum, rounded to float32, reaches thr
+      const float vstar = __uint_as_float(kthr);
+      const uint32_t ties = cnt[b3];
+      uint32_t need = ties;
+      {
+        double run = above3;
+        for (uint32_t j = 1; j <= ties; ++j) {
+          run += (double)vstar;
+          if ((float)run >= thr) { need = j; break; }
+        }
+      }
+      // ordered scan for the index just past the need-th tie
+      if (threadIdx.x == 0) cut_s = 0x7fffffff;
+      uint32_t running = 0;
+      for (int base = P; base < S; base += LT) {
+        const int t = base + threadIdx.x;
+        const bool f = t < S && !(pin && pin[t]) && __float_as_uint(act[t]) == kthr;
+        const unsigned long long bal = __ballot(f);
+        const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+        __syncthreads();
+        if (lane == 0) scratch_u[w] = (uint32_t)__popcll(bal);
+        __syncthreads();
+        uint32_t before = running;
+        for (int i = 0; i < w; ++i) before += scratch_u[i];
+        before += (uint32_t)__popcll(bal & ((1ull << lane) - 1ull));
+        if (f && before + 1 == need) cut_s = t + 1;
+        uint32_t tot = 0;
+        for (int i = 0; i < LT / 64; ++i) tot += scratch_u[i];
+        running += tot;
+        __syncthreads();
+        if (running >= need) break;
+      }
+      __syncthreads();
+      cut = cut_s;
+    }
+  }
+  // ---- keep-score update over [P, S)
+  for (int t = P + threadIdx.x; t < S; t += LT) {
+    if (pin && pin[t]) {
+      if (hit) hit[t] = 0;
+      continue;
+    }
+    const float v = act[t];
+    const uint32_t k = __float_as_uint(v);
+    const bool h = v > 0.f && (k > kthr || (k == kthr && t < cut));
+    float x = __fmul_rn(a.decay, ks[t]);
+    if (h) x = __fadd_rn(x, v);
+    ks[t] = x;
+    if (hit) hit[t] = h ? 1 : 0;
+  }
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace actkv
+
+using namespace actkv;
+
+extern "C" size_t actkv_lrfu_workspace_size(int L, int R, int max_seq) {
+  if (L < 1 || R < 1 || max_seq < 0) return 0;
+  return align256((size_t)L * R * (size_t)max_seq * sizeof(float));
+}
+
+extern "C" int actkv_lrfu_update(const float *scores, int64_t s_sl, int64_t s_sr, int64_t s_sh, int L,
+                                 int H, int R, const int32_t *seq_used, const int32_t *protected_count,
+                                 const uint8_t *protected_mask, int64_t pm_sr,
+                                 const int32_t *active, float *ks, int64_t ks_sl, int64_t ks_sr,
+                                 uint8_t *hit_out, int64_t hit_sl, int64_t hit_sr, float decay,
+                                 float top_p, int head_reduce, int max_seq, void *workspace,
+                                 size_t workspace_bytes, void *stream) {
+  if (!scores || !seq_used || !ks || L < 1 || H < 1 || R < 1 || max_seq < 0)
+    return ACTKV_ERR_INVALID_ARG;
+  if (head_reduce != ACTKV_REDUCE_MEAN && head_reduce != ACTKV_REDUCE_MAX) return ACTKV_ERR_INVALID_ARG;
+  if (protected_count && protected_mask) return ACTKV_ERR_INVALID_ARG;
+  if (!(top_p >= 0.f) || !(decay == decay)) return ACTKV_ERR_INVALID_ARG;
+  if (L > 65535 || R > 65535) return ACTKV_ERR_UNSUPPORTED;
+  if (!workspace || workspace_bytes < actkv_lrfu_workspace_size(L, R, max_seq)) return ACTKV_ERR_WORKSPACE;
+  if (max_seq == 0) return ACTKV_OK;
+  LrfuArgs a;
+  a.scores = scores; a.s_sl = s_sl; a.s_sr = s_sr; a.s_sh = s_sh;
+  a.L = L; a.H = H; a.R = R;
+  a.seq_used = seq_used; a.prot = protected_count; a.active = active;
+  a.pmask = protected_mask; a.pm_sr = pm_sr;
+  a.ks = ks; a.ks_sl = ks_sl; a.ks_sr = ks_sr;
+  a.hit = hit_out; a.hit_sl = hit_sl; a.hit_sr = hit_sr;
+  a.decay = decay; a.top_p = top_p; a.head_reduce = head_reduce; a.max_seq = max_seq;
+  a.act = (float *)workspace; a.act_sr = max_seq;
+  hipLaunchKernelGGL(lrfu_update_kernel, dim3(L, R), dim3(LT), 0, (hipStream_t)stream, a);
+  return actkv_check_launch();
+}

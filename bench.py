@@ -67,6 +67,10 @@ def parse(argv=None):
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "score_kernel_traffic.json"),
                     help="rocprofv3 FETCH_SIZE/WRITE_SIZE summary of the scoring kernel (JSON)")
     ap.add_argument("--out", help="also write the JSON line here")
+    ap.add_argument("--ora", action="store_true",
+                    help="run the agent-loop workload instead (rounds of append + causal action scoring + "
+                         "LRFU keep + compaction on a 36-layer batch of 4) and print its own JSON line")
+    ap.add_argument("--ora-rounds", type=int, default=50)
     return ap.parse_args(argv)
 
 
@@ -276,11 +280,113 @@ def load_traffic(path):
         return None
 
 
+def run_ora(args, dev):
+    """Agent-loop workload: 50 rounds on a Qwen3-8B-shaped 36-layer cache holding 4 sequences.
+    Each round appends, per sequence, U[512, 2048] observation + U[128, 512] reasoning +
+    U[32, 64] action tokens (bf16 K/V ~ N(0,1), seeded), scores the action tokens against the
+    cache with causal limits (action token j sees the prefix and action tokens <= j, exact
+    lse), updates the LRFU keep scores (decay 0.5, top-p 0.9), keeps 4 sinks plus the top
+    `budget` tokens by the layer-average keep score (budget rising linearly 4096 -> 16384) and
+    compacts.  Timed per round with HIP events: scoring + LRFU update + keep + compaction."""
+    import torch
+    from actkv.kernels.lrfu import LRFUConfig, PagedLRFU
+    from actkv.paged import PagedKVCache
+
+    L, hq, hkv, d, bs, R = args.layers, args.q_heads, args.kv_heads, args.head_dim, args.block_size, 4
+    rounds = args.ora_rounds
+    b_lo, b_hi, sinks = 4096, 16384, 4
+    cap = ((b_hi + sinks + 2048 + 512 + 64 + bs - 1) // bs) * bs
+    nb = R * (cap // bs + 2) + 64
+    gcpu = torch.Generator().manual_seed(args.seed)
+    cache = PagedKVCache(nb, bs, hkv, d, n_layers=L, dtype=torch.bfloat16, device=dev)
+    cache.free = torch.randperm(nb, generator=gcpu).tolist()
+    gdev = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    rng = np.random.default_rng(args.seed)
+    reqs = list(range(R))
+    lr = PagedLRFU(cache, reqs, cap, LRFUConfig(decay=0.5, top_p=0.9))
+    scale = d ** -0.5
+    per_round = []
+    log(f"agent loop: {rounds} rounds, {R} sequences, {L} layers")
+    for rnd in range(rounds):
+        budget = int(round(b_lo + (b_hi - b_lo) * rnd / max(rounds - 1, 1)))
+        n_act = []
+        for r in reqs:
+            n_new = int(rng.integers(512, 2049)) + int(rng.integers(128, 513))
+            a = int(rng.integers(32, 65))
+            n_act.append(a)
+            k = torch.randn(L, n_new + a, hkv, d, generator=gdev, device=dev, dtype=torch.bfloat16)
+            v = torch.randn(L, n_new + a, hkv, d, generator=gdev, device=dev, dtype=torch.bfloat16)
+            cache.append(r, k, v)
+            del k, v
+        nmax = max(n_act)
+        q = torch.randn(L, R, nmax, hq, d, generator=gdev, device=dev, dtype=torch.bfloat16)
+        kv_len = torch.zeros(R, nmax, dtype=torch.int32, device=dev)
+        lse = torch.zeros(L, R, nmax, hq, device=dev)
+        g = hq // hkv
+        for j, r in enumerate(reqs):
+            S = cache.seq_used[r]
+            kv_len[j, : n_act[j]] = torch.arange(S - n_act[j] + 1, S + 1, device=dev, dtype=torch.int32)
+            slots = cache.slot_map(r)
+            pos = torch.arange(S, device=dev)
+            mask = pos[None, :] < kv_len[j, : n_act[j], None].long()              # [a, S]
+            for l in range(L):
+                kf = cache.kv[l, 0].reshape(-1, hkv, d)[slots].float()           # [S, Hkv, D]
+                for h in range(hkv):
+                    qh = q[l, j, : n_act[j], h * g:(h + 1) * g].float()           # [a, G, D]
+                    lg = (qh @ kf[:, h].t().contiguous()) * scale                 # [a, G, S]
+                    lg = lg.masked_fill(~mask[:, None, :], float("-inf"))
+                    lse[l, j, : n_act[j], h * g:(h + 1) * g] = torch.logsumexp(lg, -1)
+        n_valid = torch.tensor(n_act, dtype=torch.int32, device=dev)
+        tokens_before = sum(cache.seq_used[r] for r in reqs)
+        free_before = len(cache.free)
+        lr.begin_round()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        ev[0].record()
+        cache.cal_attn(reqs, q, lse, lr.scores, lr.n_seen, layer=None, n_valid=n_valid, kv_len=kv_len)
+        ev[1].record()
+        lr.evict(budget, protected=sinks, n_action=n_act)
+        ev[2].record()
+        torch.cuda.synchronize()
+        per_round.append({"round": rnd, "budget": budget, "tokens_before": tokens_before,
+                          "tokens_after": sum(cache.seq_used[r] for r in reqs),
+                          "blocks_reclaimed": len(cache.free) - free_before,
+                          "score_us": ev[0].elapsed_time(ev[1]) * 1e3,
+                          "lrfu_keep_compact_us": ev[1].elapsed_time(ev[2]) * 1e3,
+                          "evict_us": ev[0].elapsed_time(ev[2]) * 1e3})
+        if rnd % 10 == 0 or rnd == rounds - 1:
+            pr = per_round[-1]
+            log(f"round {rnd}: {pr['tokens_before']} -> {pr['tokens_after']} tokens, "
+                f"{pr['blocks_reclaimed']} blocks reclaimed, {pr['evict_us']:.0f} us")
+    lat = sorted(p["evict_us"] for p in per_round)
+    result = {
+        "metric": "agent-loop evict latency per round (score action region + LRFU keep + compact)",
+        "value": round(statistics.median(lat), 1), "unit": "us", "n_gpus": 1, "rounds": rounds,
+        "higher_is_better": False, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"agent loop: {rounds} rounds, batch {R}, {L} layers, Hq {hq} / Hkv {hkv}, "
+                               f"head_dim {d}, block {bs}, bf16; per round per sequence U[512,2048] obs + "
+                               f"U[128,512] reasoning + U[32,64] action tokens; LRFU decay 0.5 top-p 0.9; "
+                               f"budget {b_lo}->{b_hi} + {sinks} sinks", "parallelism": "single-gpu"},
+        "evict_us": {"mean": round(statistics.mean(lat), 1), "median": round(statistics.median(lat), 1),
+                     "p90": round(lat[int(0.9 * (len(lat) - 1))], 1), "max": round(lat[-1], 1)},
+        "evict_us_per_layer_median": round(statistics.median(lat) / L, 2),
+        "blocks_reclaimed_total": sum(p["blocks_reclaimed"] for p in per_round),
+        "per_round": [{k: (round(v, 1) if isinstance(v, float) else v) for k, v in p.items()} for p in per_round],
+        "gpu": torch.cuda.get_device_name(dev),
+    }
+    line = json.dumps(result)
+    print(line)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(line + "\n")
+    return 0
+
+
 def main(argv=None):
     args = parse(argv)
     if args.gpus != 1:
-        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (the eviction path "
-              "shards by request or KV head, see DESIGN.md), run with --gpus 1", file=sys.stderr)
+        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (one GPU only: the "
+              "eviction path shards by request or by KV head), run with --gpus 1", file=sys.stderr)
         return 2
     import torch
     from actkv import _hip
@@ -290,6 +396,8 @@ def main(argv=None):
         return 1
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.ora:
+        return run_ora(args, dev)
 
     log(f"building the {args.layers}-layer workload")
     w = Workload(args, args.layers, dev)

@@ -192,6 +192,56 @@ int actkv_compact(void *kv, int64_t planes, int64_t stride_plane_bytes,
 /* Bytes of caller workspace an entry point needs (kind = ACTKV_WS_*). */
 size_t actkv_workspace_size(int kind, int R, int max_seq);
 
+/*
+ * actkv_gather_tokens -- per-token metadata follows a compaction: for every
+ * layer l < L and request r < R,
+ *   dst[l, r, i] = src[l, r, perm[r, i]]  for i < kept[r]
+ *   dst[l, r, i] = 0                      for kept[r] <= i < W
+ * (perm as written by actkv_compact: new logical -> old logical; an entry
+ * outside [0, W) reads as 0).  The reference permutes such state by indexing
+ * with the permutation (actkv/kernels/compaction.py:16-18,
+ * actkv/eviction.py:222-224).  src and dst are float32 with strides (sl, sr)
+ * and a unit last stride, and must not overlap.
+ */
+int actkv_gather_tokens(const float *src, int64_t src_sl, int64_t src_sr, float *dst,
+                        int64_t dst_sl, int64_t dst_sr, int L, int R, int W, const int64_t *perm,
+                        int64_t perm_sr, const int32_t *kept, void *stream);
+
+/*
+ * actkv_lrfu_update -- LRFU keep-score update (ActKV Algorithm 1 steps 2-4)
+ * of the paged cache, one (layer, request) segment per workgroup.
+ *
+ * Replaces actkv/eviction.py:209-218 (ActionLRFU.update_scores) with its
+ * nucleus actkv/eviction.py:36-50 (top_p_mask), for a paged cache whose
+ * per-token action scores come from actkv_action_scores.  For layer l,
+ * request r, S = seq_used[r], P = protected_count[r] (0 if NULL), or, with
+ * protected_mask (bool [R, >=S], row stride pm_sr) instead, the pinned tokens
+ * (excluded from the nucleus, ks untouched; at most one of the two):
+ *   act[t] = mean (torch CPU float32 order) or max over the H heads of
+ *            scores[l, r, h, t]                               (eviction.py:20-33)
+ *   hit    = over t in [P, S): the entries taken in descending act order
+ *            (equal values: lower index first) until the running sum reaches
+ *            top_p * total (float64 running sums compared as float32, as
+ *            torch's cumsum), positive entries only; no hits when
+ *            active[r] == 0 or total <= 0                   (eviction.py:36-50)
+ *   ks[l, r, t] = decay * ks[l, r, t]  (+ act[t] where hit), t in [P, S)
+ * ks entries below P and at or past S are not touched.
+ * scores float32 [L, R, H, >=S] (strides s_sl s_sr s_sh, unit last);
+ * ks float32 [L, R, >=S] (strides ks_sl ks_sr, unit last), in place;
+ * hit_out (optional) bool [L, R, >=S]: the hit mask over [P, S).
+ * workspace: actkv_lrfu_workspace_size(L, R, max_seq) bytes, any contents.
+ */
+int actkv_lrfu_update(const float *scores, int64_t s_sl, int64_t s_sr, int64_t s_sh, int L, int H,
+                      int R, const int32_t *seq_used, const int32_t *protected_count,
+                      const uint8_t *protected_mask, int64_t pm_sr,
+                      const int32_t *active, float *ks, int64_t ks_sl, int64_t ks_sr,
+                      uint8_t *hit_out, int64_t hit_sl, int64_t hit_sr, float decay, float top_p,
+                      int head_reduce, int max_seq, void *workspace, size_t workspace_bytes,
+                      void *stream);
+
+/* Workspace bytes for actkv_lrfu_update (one float per layer, request and token). */
+size_t actkv_lrfu_workspace_size(int L, int R, int max_seq);
+
 #ifdef __cplusplus
 }
 #endif

@@ -333,3 +333,93 @@ class PagedCacheModel:
         perm = self.compact(req, keep)
         self.pinned[req] = pinned[perm]
         return perm
+
+
+# ============================================================================ LRFU keep score
+
+def top_p_mask(scores: torch.Tensor, p: float, stable: bool = False, total64: bool = False) -> torch.Tensor:
+    """Nucleus mask (eviction.py:36-50): the smallest set of entries, taken in descending order,
+    whose cumulative sum reaches p * total, restricted to positive entries.  torch CPU
+    semantics: float32 total, float32 threshold p * total, cumsum accumulated in float64 and
+    stored as float32, left searchsorted.  stable=False sorts exactly as the reference (torch's
+    default sort, whose order among equal scores is unspecified); stable=True takes equal
+    scores lower index first, the rule the device kernel follows.  total64=True rounds the
+    float64 total to float32 (the device kernel's total) instead of torch's float32
+    summation order, which depends on the host's SIMD width; the two totals differ by a few
+    ulps, which moves the nucleus boundary only when a running sum lies that close to it."""
+    if scores.numel() == 0:
+        return torch.zeros_like(scores, dtype=torch.bool)
+    total = scores.double().sum().float() if total64 else scores.sum()
+    if total <= 0:
+        return torch.zeros_like(scores, dtype=torch.bool)
+    vals, order = torch.sort(scores, descending=True, stable=stable)
+    csum = torch.cumsum(vals, 0)
+    n_keep = int(torch.searchsorted(csum, p * total).item()) + 1
+    n_keep = min(n_keep, scores.numel())
+    mask = torch.zeros_like(scores, dtype=torch.bool)
+    mask[order[:n_keep]] = True
+    return mask & (scores > 0)
+
+
+def top_p_mask_bruteforce(scores, p: float):
+    """The nucleus from its definition with Python loops and float64 sums (small inputs):
+    walk the entries in descending order (ties: lower index first) until the running sum
+    reaches p * total; keep those entries that are positive."""
+    vals = [float(x) for x in scores]
+    total = sum(vals)
+    if not vals or total <= 0:
+        return [False] * len(vals)
+    order = sorted(range(len(vals)), key=lambda i: (-vals[i], i))
+    keep = [False] * len(vals)
+    run = 0.0
+    for i in order:
+        keep[i] = vals[i] > 0
+        run += vals[i]
+        if run >= p * total:
+            break
+    return keep
+
+
+def lrfu_update(ks: torch.Tensor, act: torch.Tensor, seq_used: int, protected: int, decay: float,
+                top_p: float, active: bool = True, stable: bool = False):
+    """Algorithm 1 steps 2-4 for one layer row (eviction.py:209-218): over entries
+    [protected, seq_used), hit = top_p_mask(act) (none when the round had no action tokens),
+    ks = decay * ks, then ks[hit] += act[hit].  ks, act: float32 [>= seq_used], ks in place.
+    Returns the hit mask over [protected, seq_used)."""
+    a = act[protected:seq_used]
+    hit = top_p_mask(a, top_p, stable) if active else torch.zeros_like(a, dtype=torch.bool)
+    k = ks[protected:seq_used]
+    k.mul_(decay)
+    k[hit] += a[hit]
+    return hit
+
+
+def paged_lrfu_act(scores: torch.Tensor, seq_used: int, head_reduce: str = "mean") -> torch.Tensor:
+    """Per-layer, per-token action score of the paged cache: the action-region scores
+    [L, Hkv, W] (running mean over the round's action queries of the GQA-group max,
+    lse_attn.py:63-78) reduced over KV heads (eviction.py:20-33) -> [L, seq_used] float32."""
+    x = scores[..., :seq_used].float()
+    return x.amax(-2) if head_reduce == "max" else x.mean(-2)
+
+
+def paged_lrfu_update(ks: torch.Tensor, act: torch.Tensor, seq_used: int, pinned, decay: float,
+                      top_p: float, active: bool = True, stable: bool = True,
+                      total64: bool = False) -> torch.Tensor:
+    """lrfu_update for every layer of one request of the paged cache: ks [L, >=S] (in place),
+    act [L, >=S].  `pinned` is a prefix count or a bool mask [>=S] of protected tokens; the
+    nucleus runs over the other tokens in index order (a prefix count gives exactly
+    eviction.py:209-218's act[layer, protected:]).  Returns hits [L, S] bool."""
+    S = seq_used
+    if isinstance(pinned, torch.Tensor):
+        free = torch.nonzero(~pinned[:S].bool()).flatten()
+    else:
+        free = torch.arange(min(max(int(pinned), 0), S), S)
+    hits = torch.zeros(ks.shape[0], S, dtype=torch.bool)
+    for l in range(ks.shape[0]):
+        a = act[l, free]
+        hit = top_p_mask(a, top_p, stable, total64) if active else torch.zeros_like(a, dtype=torch.bool)
+        k = ks[l, free] * decay
+        k[hit] += a[hit]
+        ks[l, free] = k
+        hits[l, free] = hit
+    return hits

@@ -357,3 +357,83 @@ def test_model_free_list_is_a_stack():
     assert m.tables[0] == [2] and m.seq_used[0] == 2
     # dropped blocks go back reversed: the first freed block is popped next
     assert m.free == [5, 4, 3, 1, 0]
+
+
+# ---------------------------------------------------------------- LRFU keep score
+
+def test_top_p_mask_known_answer():
+    """tests/test_algorithms.py:16-19 of the reference."""
+    s = torch.tensor([0.5, 0.05, 0.3, 0.15, 0.0])
+    assert ref.top_p_mask(s, 0.9).tolist() == [True, False, True, True, False]
+    assert ref.top_p_mask(s, 0.9, stable=True).tolist() == [True, False, True, True, False]
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_top_p_mask_matches_brute_force(seed):
+    g = torch.Generator().manual_seed(seed)
+    n = int(torch.randint(1, 60, (1,), generator=g))
+    x = torch.rand(n, generator=g) ** 3
+    x[torch.rand(n, generator=g) < 0.2] = 0.0
+    if seed % 4 == 0:                                  # ties
+        x = torch.round(x * 8) / 8
+    p = float(torch.rand(1, generator=g)) * 0.98 + 0.01
+    assert ref.top_p_mask(x, p, stable=True).tolist() == ref.top_p_mask_bruteforce(x, p)
+
+
+def test_top_p_mask_edge_cases():
+    assert ref.top_p_mask(torch.zeros(0), 0.9).tolist() == []
+    assert ref.top_p_mask(torch.zeros(4), 0.9).tolist() == [False] * 4
+    assert ref.top_p_mask(torch.tensor([0.0, 2.0, 0.0]), 0.5).tolist() == [False, True, False]
+    assert ref.top_p_mask(torch.tensor([1.0, 1.0, 1.0]), 1.0, stable=True).tolist() == [True] * 3
+
+
+def test_lrfu_update_known_answers():
+    """tests/test_algorithms.py:22-48 of the reference (Algorithm 1 update, and a round without
+    an action region only decays)."""
+    ks = torch.zeros(4)
+    ref.lrfu_update(ks, torch.tensor([0.05, 0.05, 0.8, 0.1]), 4, 0, 0.5, 0.9)
+    torch.testing.assert_close(ks, torch.tensor([0.0, 0.0, 0.8, 0.1]))
+    ks2 = torch.cat([ks, torch.zeros(2)])
+    ref.lrfu_update(ks2, torch.tensor([0.0, 0.0, 0.0, 0.05, 0.95, 0.0]), 6, 0, 0.5, 0.9)
+    torch.testing.assert_close(ks2, torch.tensor([0.0, 0.0, 0.4, 0.05, 0.95, 0.0]))
+    ks3 = torch.cat([ks, torch.zeros(2)])
+    ref.lrfu_update(ks3, torch.zeros(6), 6, 0, 0.5, 0.9, active=False)
+    torch.testing.assert_close(ks3, torch.tensor([0.0, 0.0, 0.4, 0.05, 0.0, 0.0]))
+
+
+def test_paged_lrfu_update_with_a_prefix_equals_the_reference_form():
+    g = torch.Generator().manual_seed(3)
+    act = torch.rand(3, 50, generator=g)
+    ks_a = torch.rand(3, 50, generator=g)
+    ks_b = ks_a.clone()
+    ref.paged_lrfu_update(ks_a, act, 50, 6, 0.5, 0.9, stable=False)
+    for l in range(3):
+        ref.lrfu_update(ks_b[l], act[l], 50, 6, 0.5, 0.9)
+    assert torch.equal(ks_a, ks_b)
+    # a pinned mask equal to the prefix gives the same result
+    ks_c = ks_b.clone()
+    ks_d = ks_b.clone()
+    pin = torch.arange(50) < 6
+    ref.paged_lrfu_update(ks_c, act, 50, pin, 0.5, 0.9)
+    ref.paged_lrfu_update(ks_d, act, 50, 6, 0.5, 0.9)
+    assert torch.equal(ks_c, ks_d)
+
+
+def test_top_p_mask_total_orders_agree_away_from_the_boundary():
+    """The float64-rounded total (the device's) and torch's float32 total give the same nucleus
+    unless a running sum lies within a few ulps of p * total: on random heavy-tailed inputs the
+    masks agree almost always, and where they differ the boundary is that close."""
+    g = torch.Generator().manual_seed(9)
+    differ = 0
+    for _ in range(300):
+        x = (torch.rand(2000, generator=g) ** 8) * 1e-2
+        a = ref.top_p_mask(x, 0.9, stable=True)
+        b = ref.top_p_mask(x, 0.9, stable=True, total64=True)
+        if not torch.equal(a, b):
+            differ += 1
+            vals = torch.sort(x, descending=True, stable=True).values
+            csum = torch.cumsum(vals, 0)
+            thr_a, thr_b = 0.9 * x.sum(), 0.9 * x.double().sum().float()
+            lo, hi = min(float(thr_a), float(thr_b)), max(float(thr_a), float(thr_b))
+            assert bool(((csum >= lo) & (csum <= hi)).any())
+    assert differ <= 30

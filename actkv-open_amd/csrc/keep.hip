@@ -105,6 +105,90 @@ __global__ void __launch_bounds__(REDUCE_THREADS) keep_reduce_kernel(KeepArgs a)
   }
 }
 
+// Histogram of candidate keys (key != 0) by their top 11 bits, one atomic per
+// distinct bin of the wave.
+__device__ __forceinline__ void hist_add_wave(uint32_t *hist, uint32_t key) {
+  bool pending = key != 0;
+  const int bin = (int)(key >> 21);
+  while (true) {
+    const unsigned long long act = __ballot(pending);
+    if (act == 0ull) break;
+    const int leader = __ffsll((long long)act) - 1;
+    const int lbin = __shfl(bin, leader, 64);
+    const unsigned long long same = __ballot(pending && bin == lbin);
+    if ((int)(threadIdx.x & 63) == leader) atomicAdd(&hist[lbin], (uint32_t)__popcll(same));
+    if (pending && bin == lbin) pending = false;
+  }
+}
+
+// float32 scores with 16-byte aligned token rows: grid (ceil(max_seq/256), R),
+// REDUCE_THREADS threads.  Phase 1: thread (layer group tid/64, quad tid%64)
+// reduces the heads of 4 consecutive tokens with 16-byte loads; phase 2: each of
+// the first 256 threads averages the layers of one token.  Same per-token float
+// order as keep_reduce_kernel (a 4-token quad lies wholly in or out of the
+// 32-column-aligned body).
+template <int HH>
+__global__ void __launch_bounds__(REDUCE_THREADS) keep_reduce4_kernel(KeepArgs a) {
+  extern __shared__ float lvals[];  // [L][256]
+  const int r = blockIdx.y;
+  const int S = min(a.seq_used[r], a.max_seq);
+  const int t0 = blockIdx.x * 256;
+  if (t0 >= S) return;
+  const int quad = threadIdx.x & 63, lg = threadIdx.x >> 6;
+  const int tq = t0 + 4 * quad;
+  const bool body4 = tq < (S & ~31);
+  const float *sbase = (const float *)a.scores + (int64_t)r * a.s_sr;
+  // the quad's 4 scores of one (layer, head) row; the last quad of a sequence
+  // reads only its tokens below S
+  const int nin = min(S - tq, 4);
+  auto load4 = [&](const float *p) {
+    if (nin == 4) return *(const f32x4 *)p;
+    f32x4 x = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < nin; ++j) x[j] = p[j];
+    return x;
+  };
+  if (tq < S) {
+    for (int l = lg; l < a.L; l += REDUCE_THREADS / 64) {
+      const float *col = sbase + (int64_t)l * a.s_sl + tq;
+      f32x4 v;
+      if (a.head_reduce == ACTKV_REDUCE_MAX) {
+        v = load4(col);
+#pragma unroll
+        for (int hh = 1; hh < HH; ++hh) {
+          const f32x4 x = load4(col + (int64_t)hh * a.s_sh);
+          v[0] = nanmax(v[0], x[0]); v[1] = nanmax(v[1], x[1]);
+          v[2] = nanmax(v[2], x[2]); v[3] = nanmax(v[3], x[3]);
+        }
+      } else {
+        // the heads of the 4 tokens, loaded once, summed per token
+        f32x4 hv[HH];
+#pragma unroll
+        for (int hh = 0; hh < HH; ++hh) hv[hh] = load4(col + (int64_t)hh * a.s_sh);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          auto ld = [&](int hh) { return hv[hh][j]; };
+          v[j] = __fdiv_rn(torch_sum(ld, HH, body4), (float)HH);
+        }
+      }
+      *(f32x4 *)&lvals[l * 256 + 4 * quad] = v;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x >= 256) return;
+  const int tok = threadIdx.x;
+  const int t = t0 + tok;
+  const bool body = t < (S & ~31);
+  uint32_t key = 0;
+  const bool in = t < S;
+  if (in && !is_protected(a, r, t)) {
+    auto ld = [&](int l) { return lvals[l * 256 + tok]; };
+    const float sc = __fdiv_rn(torch_sum(ld, a.L, body), (float)a.L);
+    key = float_key(sc);
+  }
+  if (in) a.keys[(int64_t)r * a.keys_sr + t] = key;
+  hist_add_wave(a.hist + (int64_t)r * HIST_BINS, key);
+}
+
 // Block-wide helpers for 1024 threads (16 waves).
 __device__ __forceinline__ uint32_t block_sum_u32(uint32_t v, uint32_t *scratch) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -372,9 +456,22 @@ extern "C" int actkv_keep_mask(const void *scores, int scores_dtype, int64_t s_s
 
   const int64_t nh = (int64_t)R * HIST_BINS;
   hipLaunchKernelGGL(zero_u32_kernel, dim3((unsigned)((nh + 255) / 256)), dim3(256), 0, st, a.hist, nh);
+  const bool vec4 = scores_dtype == ACTKV_F32 && ((uintptr_t)scores & 15) == 0 && s_sl % 4 == 0 &&
+                    s_sr % 4 == 0 && s_sh % 4 == 0 && (H == 1 || H == 2 || H == 4 || H == 8 || H == 16) &&
+                    (size_t)L * 256 * sizeof(float) <= 64 * 1024;
   dim3 g1((max_seq + 63) / 64, R);
   const size_t shm = (size_t)L * 64 * sizeof(float);
-  switch (scores_dtype) {
+  if (vec4) {
+    const dim3 g4((max_seq + 255) / 256, R);
+    const size_t shm4 = (size_t)L * 256 * sizeof(float);
+    switch (H) {
+      case 1: hipLaunchKernelGGL(keep_reduce4_kernel<1>, g4, dim3(REDUCE_THREADS), shm4, st, a); break;
+      case 2: hipLaunchKernelGGL(keep_reduce4_kernel<2>, g4, dim3(REDUCE_THREADS), shm4, st, a); break;
+      case 4: hipLaunchKernelGGL(keep_reduce4_kernel<4>, g4, dim3(REDUCE_THREADS), shm4, st, a); break;
+      case 8: hipLaunchKernelGGL(keep_reduce4_kernel<8>, g4, dim3(REDUCE_THREADS), shm4, st, a); break;
+      default: hipLaunchKernelGGL(keep_reduce4_kernel<16>, g4, dim3(REDUCE_THREADS), shm4, st, a); break;
+    }
+  } else switch (scores_dtype) {
     case ACTKV_F32: hipLaunchKernelGGL(keep_reduce_kernel<float>, g1, dim3(REDUCE_THREADS), shm, st, a); break;
     case ACTKV_F16: hipLaunchKernelGGL(keep_reduce_kernel<_Float16>, g1, dim3(REDUCE_THREADS), shm, st, a); break;
     default: hipLaunchKernelGGL(keep_reduce_kernel<__bf16>, g1, dim3(REDUCE_THREADS), shm, st, a); break;

@@ -339,6 +339,8 @@ def test_action_scores_every_layer_in_one_launch():
     (1, 8, 777, 800, 77, 4, "mean"),
     (3, 3, 200, 200, 20, 0, "mean"),
     (40, 16, 513, 520, 64, 2, "mean"),       # 16 heads: a full cascade block per layer
+    (5, 8, 1001, 1001, 99, 3, "mean"),       # rows not 16-byte aligned: the 4-byte load path
+    (2, 4, 2050, 2052, 200, 0, "max"),       # 4 heads, a last quad with 2 tokens
 ])
 def test_keep_mask_bit_exact_with_the_oracle(L, H, S, W, budget, prot, reduce):
     """The device reduction reproduces torch's CPU mean bit for bit, so the keep mask equals

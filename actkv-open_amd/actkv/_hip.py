@@ -121,7 +121,15 @@ def ptr(t) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+# torch's current-stream lookup without building a Stream object (several microseconds per
+# call through torch.cuda.current_stream); the public route stays as the fallback.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream(device: torch.device) -> int:
+    """The hipStream_t of torch's current stream on `device` (the stream every launch uses)."""
+    if _raw_stream is not None:
+        return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(device).cuda_stream
 
 

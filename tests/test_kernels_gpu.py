@@ -383,3 +383,28 @@ def test_batched_evict_mixes_first_and_repeated_evictions():
         assert np.array_equal(perms[r].cpu().numpy(), perm_o), r
         assert np.array_equal(cache.pinned[r].cpu().numpy(), model.pinned[r]), r
     _assert_same_state(cache, model)
+
+
+def test_launches_follow_torch_current_stream():
+    """The library launches on torch's current stream, including inside `torch.cuda.stream`."""
+    from actkv import _hip
+    dev = torch.device("cuda")
+    assert _hip.stream(dev) == torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert _hip.stream(dev) == side.cuda_stream
+        assert _hip.stream(torch.device("cuda", torch.cuda.current_device())) == side.cuda_stream
+        # a scoring call queued on the side stream gives the same result as on the default one
+        cache = _filled_cache([200, 150], hkv=2, d=128, layers=1, seed=11, dtype=torch.bfloat16)
+        g = torch.Generator().manual_seed(12)
+        q = torch.randn(2, 8, 128, generator=g).to(torch.bfloat16).cuda()
+        lse = torch.full((2, 8), 6.0, device="cuda")
+        width = max(len(cache.tables[r]) for r in (0, 1)) * cache.block_size
+        a = torch.zeros(2, 2, width, device="cuda")
+        na = torch.zeros(2, dtype=torch.int32, device="cuda")
+        cache.cal_attn([0, 1], q, lse, a, na, layer=0)
+    side.synchronize()
+    b = torch.zeros_like(a)
+    nb = torch.zeros_like(na)
+    cache.cal_attn([0, 1], q, lse, b, nb, layer=0)
+    assert torch.equal(a, b) and na.tolist() == nb.tolist() == [1, 1]

@@ -65,6 +65,16 @@ _SIGNATURES = {
     "actkv_lrfu_workspace_size": (_c_sz, [_c_i32, _c_i32, _c_i32]),
     "actkv_gather_tokens": (_c_i32, [_c_p, _c_i64, _c_i64, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32,
                                      _c_p, _c_i64, _c_p, _c_p]),
+    "actkv_paged_attention": (_c_i32, [
+        _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64,            # q
+        _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,    # kv, sl sv sb ss sh
+        _c_i64,                                                  # num_blocks
+        _c_p, _c_i64, _c_i32,                                    # block_table, bt_sr, max_blocks
+        _c_p, _c_p, _c_p,                                        # seq_used n_valid kv_len
+        _c_p, _c_i64, _c_i64, _c_i64, _c_i64,                    # out, strides
+        _c_p, _c_i64, _c_i64, _c_i64,                            # lse, strides
+        _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,  # L R N Hq Hkv D bs
+        _c_f, _c_p]),
 }
 
 _lib = None

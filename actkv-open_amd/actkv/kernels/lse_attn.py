@@ -175,3 +175,64 @@ def action_scores(q, kv, block_table, seq_used, lse, out, n_seen, scale=None, *,
         L, r_n, n_q, hq, hkv, d, bs, float(scale), _hip.stream(dev))
     _hip.check(rc, "actkv_action_scores")
     return out
+
+
+def paged_decode_attention(q, kv, block_table, seq_used, scale=None, *, n_valid=None, kv_len=None):
+    """Paged attention with the LSE by-product on the GPU: returns (out, lse), float32.
+
+    Same call and results as paged_decode_attention_ref (lse_attn.py:42-60), which stands in for
+    the paged FlashAttention backend whose LSE Algorithm 3 consumes: q [R, Hq, D] ->
+    out [R, Hq, D], lse [R, Hq].  Additive forms: q [R, N, Hq, D] (N queries per request) ->
+    out [R, N, Hq, D], lse [R, N, Hq]; with kv [L, 2, NB, BS, Hkv, D], q [L, R, N, Hq, D] ->
+    out [L, R, N, Hq, D], lse [L, R, N, Hq].  n_valid [R]: queries used per request (rows past it
+    are zero); kv_len [R, N]: query n sees tokens t < kv_len[r, n] (causal limits).  A query
+    that sees no token gets lse = -inf and out = 0.
+    """
+    dev = _hip.require_gpu("paged_decode_attention", q, kv, block_table, seq_used, n_valid, kv_len)
+    if kv.dim() == 6:
+        L, _, nb, bs, hkv, d = kv.shape
+        if q.dim() != 5:
+            raise ValueError("a [L, 2, NB, BS, Hkv, D] cache takes q [L, R, N, Hq, D]")
+        q5, kv_sl, kv_sv, kv_k = q, kv.stride(0), kv.stride(1), kv[:, 0]
+        squeeze = ()
+    elif kv.dim() == 5:
+        _, nb, bs, hkv, d = kv.shape
+        L = 1
+        if q.dim() == 3:
+            q5, squeeze = q.unsqueeze(1).unsqueeze(0), (0, 2)
+        elif q.dim() == 4:
+            q5, squeeze = q.unsqueeze(0), (0,)
+        else:
+            raise ValueError(f"q must be [R, Hq, D] or [R, N, Hq, D] for a one-layer cache, got {tuple(q.shape)}")
+        kv_sl, kv_sv, kv_k = 0, kv.stride(0), kv[0]
+    else:
+        raise ValueError(f"kv must be [2, NB, BS, Hkv, D] or [L, 2, NB, BS, Hkv, D], got {tuple(kv.shape)}")
+    _, r_n, n_q, hq, dq = q5.shape
+    assert hq % hkv == 0
+    assert dq == d
+    assert kv.stride(-1) == 1 and q.stride(-1) == 1
+    scale = scale if scale is not None else d ** -0.5
+    bt = _as_i32(block_table, dev)
+    if bt.stride(-1) != 1:
+        bt = bt.contiguous()
+    seq = _as_i32(seq_used, dev).contiguous()
+    nv = None if n_valid is None else _as_i32(n_valid, dev).contiguous()
+    kl = None if kv_len is None else _as_i32(kv_len, dev).contiguous()
+    if kl is not None and tuple(kl.shape) != (r_n, n_q):
+        raise ValueError(f"kv_len must be [R, N] = {(r_n, n_q)}")
+    alloc = torch.empty if nv is None else torch.zeros
+    out = alloc(L, r_n, n_q, hq, d, dtype=torch.float32, device=dev)
+    lse = alloc(L, r_n, n_q, hq, dtype=torch.float32, device=dev)
+    rc = _hip.lib().actkv_paged_attention(
+        q5.data_ptr(), _hip.dtype_code(q5.dtype), q5.stride(0), q5.stride(1), q5.stride(2), q5.stride(3),
+        kv_k.data_ptr(), _hip.dtype_code(kv.dtype), kv_sl, kv_sv, kv_k.stride(-4), kv_k.stride(-3),
+        kv_k.stride(-2), nb,
+        bt.data_ptr(), bt.stride(0), bt.shape[1],
+        seq.data_ptr(), _hip.ptr(nv), _hip.ptr(kl),
+        out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), out.stride(3),
+        lse.data_ptr(), lse.stride(0), lse.stride(1), lse.stride(2),
+        L, r_n, n_q, hq, hkv, d, bs, float(scale), _hip.stream(dev))
+    _hip.check(rc, "actkv_paged_attention")
+    for dim in reversed(squeeze):
+        out, lse = out.squeeze(dim), lse.squeeze(dim)
+    return out, lse

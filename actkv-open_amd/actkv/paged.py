@@ -24,7 +24,7 @@ import torch
 
 from . import _hip
 from .kernels.compaction import keep_words, upload_i32
-from .kernels.lse_attn import action_scores, paged_decode_attention_ref
+from .kernels.lse_attn import action_scores, paged_decode_attention, paged_decode_attention_ref
 
 
 class OutOfBlocks(RuntimeError):
@@ -273,10 +273,15 @@ class PagedKVCache:
         return flat[0, slots], flat[1, slots]
 
     # ---------------------------------------------------------------- primitives
-    def decode_attention(self, reqs, q, layer=0, scale=None):
-        """Reference paged decode attention -> (out, lse); stands in for the paged FA backend."""
-        return paged_decode_attention_ref(q, self.kv[layer], self.block_table(reqs),
-                                          self.seq_tensor(reqs), scale)
+    def decode_attention(self, reqs, q, layer=0, scale=None, *, n_valid=None, kv_len=None):
+        """Paged attention -> (out, lse) on the GPU: the paged FlashAttention backend whose LSE
+        by-product cal_attn consumes (the reference stands in for it with the torch
+        paged_decode_attention_ref).  q [R, Hq, D] or [R, N, Hq, D]; layer=None attends every
+        layer at once with q [L, R, N, Hq, D].  kv_len [R, N]: causal limits per query.
+        Reference: actkv/paged.py:115-118."""
+        kv = self.kv if layer is None else self.kv[layer]
+        seq, bt = self._device_tables(reqs)
+        return paged_decode_attention(q, kv, bt, seq, scale, n_valid=n_valid, kv_len=kv_len)
 
     def cal_attn(self, reqs, q, lse, out, n_seen, layer=0, scale=None, *, n_valid=None, kv_len=None):
         """Primitive 1: AttnScore <- CalAttn(target_q, KCache) via LSE recovery (Algorithm 3).

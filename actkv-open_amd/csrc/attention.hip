@@ -1,0 +1,467 @@
+// Paged attention that emits the softmax log-sum-exp (the lse producer ActKV
+// Algorithm 3 consumes) for gfx950.
+//
+// Reference: actkv/kernels/lse_attn.py:42-60 (paged_decode_attention_ref, the
+// stand-in for "the paged FlashAttention backend whose LSE by-product
+// Algorithm 3 consumes") and actkv/paged.py:115-118 (decode_attention).  For
+// every query row (query n of request r, query head hq) and the tokens t it
+// sees (t < seq_used[r], and t < kv_len[r, n] when causal limits are given):
+//   s_t = scale * q . k_t,  lse = logsumexp_t s_t,  out = sum_t softmax(s)_t v_t
+// out and lse are float32.  A row that sees no token gets lse = -inf, out = 0
+// (torch's logsumexp and softmax-einsum over an empty set).
+//
+// MFMA path (bf16/fp16, head_dim 128, GQA group 1/2/4): FlashAttention-style,
+// one workgroup per (layer, request, KV head, group of NW row tiles), NW waves,
+// each owning one 32-row tile of the pair's query rows (n, g) and streaming all
+// of the request's tokens.  The transposed products keep every per-query
+// quantity inside one lane:
+//   S^T = K . Q^T   (v_mfma_f32_32x32x16: A = K rows from LDS, B = Q in registers)
+//   lane (lcol, lh) holds s for query row lcol and 16 of the slice's 32 tokens,
+//   so the running max / sum of a row are lane-local plus one v_permlane32_swap;
+//   O^T += V^T . P^T (A = V^T from LDS, B = P^T: the lane's own 16 probabilities,
+//   taken in the token order tau(kb, lh, j) = 16kb + 8(j/4) + 4lh + j%4 that
+//   matches the S^T register layout, so no shuffle is needed).
+// K and V move through a two-slot LDS stage buffer: the workgroup loads stage
+// g+1 into registers while stage g is multiplied, then writes K rows (padded to
+// 272 bytes: conflict-free B-operand reads) and V transposed (dim-major rows,
+// padded: conflict-free 8-byte reads), one barrier per stage.
+//
+// Generic path (any other dtype / head_dim / group): one workgroup per query row,
+// float32 dot products, an online max/sum pass for lse and a second pass that
+// accumulates out through LDS-staged probabilities.
+#include "common.h"
+
+#include <algorithm>
+
+namespace actkv {
+
+struct AttnArgs {
+  const void *q;
+  int64_t q_sl, q_sr, q_sn, q_sh;
+  const void *kv;  // K plane of layer 0; the V plane is kv + kv_sv elements
+  int64_t kv_sl, kv_sv, kv_sb, kv_ss, kv_sh;
+  int64_t num_blocks;
+  const int32_t *bt;
+  int64_t bt_sr;
+  int max_blocks;
+  const int32_t *seq_used, *n_valid, *kv_len;
+  float *out;
+  int64_t o_sl, o_sr, o_sn, o_sh;
+  float *lse;
+  int64_t lse_sl, lse_sr, lse_sn;
+  int L, R, N, Hq, Hkv, D, G, BS;
+  float scale;
+};
+
+__device__ __forceinline__ int attn_seq_len(const AttnArgs &a, int r) {
+  const int s = a.seq_used[r];
+  const int span = a.max_blocks * a.BS;
+  return s < 0 ? 0 : (s > span ? span : s);
+}
+
+__device__ __forceinline__ int attn_nq(const AttnArgs &a, int r) {
+  return a.n_valid ? min(max(a.n_valid[r], 0), a.N) : a.N;
+}
+
+// tokens query n of request r sees: [0, lim)
+__device__ __forceinline__ int attn_lim(const AttnArgs &a, int r, int n, int S) {
+  return a.kv_len ? min(max(a.kv_len[(int64_t)r * a.N + n], 0), S) : S;
+}
+
+// physical block of logical block `b` of request r, or -1 (past the table, or an
+// id outside the pool)
+__device__ __forceinline__ int attn_phys(const AttnArgs &a, int r, int b) {
+  if (b < 0 || b >= a.max_blocks) return -1;
+  const int64_t p = a.bt[(int64_t)r * a.bt_sr + b];
+  return (p >= 0 && p < a.num_blocks) ? (int)p : -1;
+}
+
+// ------------------------------------------------------------------ MFMA path
+template <int NW> struct AttnShape {
+  static constexpr int ST = NW >= 4 ? 16 * NW : 32;  // tokens per stage
+  static constexpr int GS = ST / 32;                  // 32-token slices per stage
+  static constexpr int CPT = ST * 16 / (NW * 64);     // 16-byte chunks per thread per stage (K and V each)
+  static constexpr int KROW = 272;                    // padded K row (bytes)
+  static constexpr int VROW = ST * 2 + 8;             // padded V^T row: ST tokens of one dim
+  static constexpr int KSTAGE = ST * KROW, VSTAGE = 128 * VROW;
+};
+
+template <typename T, typename V8, int G, int NW, bool CAUSAL>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 2 ? 2 : 1, NW >= 2 ? 2 : 1)))
+attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
+  using SH = AttnShape<NW>;
+  constexpr int ST = SH::ST, GS = SH::GS, CPT = SH::CPT, KROW = SH::KROW, VROW = SH::VROW;
+  constexpr int KS = 8;
+  __shared__ __attribute__((aligned(16))) unsigned char kbuf[2][SH::KSTAGE];
+  __shared__ __attribute__((aligned(16))) unsigned char vbuf[2][SH::VSTAGE];
+
+  // XCD-aware mapping: the row groups of one (layer, request, head) pair share an
+  // XCD, so the second group's K/V reads hit that XCD's L2.
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7, jj = bid >> 3;
+  const int p = (jj / ngroups) * 8 + xcd;
+  const int grp = jj % ngroups;
+  if (p >= pairs) return;
+  const int h = p % a.Hkv;
+  const int r = (p / a.Hkv) % a.R;
+  const int l = p / (a.Hkv * a.R);
+  const int nq = attn_nq(a, r);
+  if (grp * NW * 32 >= nq * G) return;
+  const int S = attn_seq_len(a, r);
+  const int BS = a.BS;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lcol = lane & 31, lh = lane >> 5;
+
+  // ---- this lane's query row: B operands of S^T = K . Q^T, causal limit
+  const int row = (grp * NW + wave) * 32 + lcol;
+  const int n = row / G, g = row % G;
+  const bool valid = n < nq;
+  const int lim = valid ? attn_lim(a, r, n, S) : 0;
+  V8 qf[KS];
+  {
+    const T *qp = (const T *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr +
+                  (int64_t)(valid ? n : 0) * a.q_sn + (int64_t)(h * G + g) * a.q_sh + lh * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const V8 *)(qp + ks * 16);
+    if (!valid) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qf[ks] = V8{};
+    }
+  }
+
+  // ---- stage loads: chunk q = tid + k*NW*64 of a stage is row q/16, 16-byte chunk q%16
+  const T *kplane = (const T *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh;
+  const T *vplane = kplane + a.kv_sv;
+  const int nst = (S + ST - 1) / ST;
+  int phys[CPT];  // physical blocks of this thread's rows of the next stage to load
+  auto stage_phys = [&](int (&ph)[CPT], int g0) {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int t = g0 * ST + ((tid + k * NW * 64) >> 4);
+      ph[k] = t < S ? attn_phys(a, r, t >> bs_shift) : -1;
+    }
+  };
+  uint4 kreg[CPT], vreg[CPT];
+  auto load_stage = [&](const int (&ph)[CPT], int g0) {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int q = tid + k * NW * 64;
+      const int t = g0 * ST + (q >> 4), c = q & 15;
+      const bool ok = ph[k] >= 0;  // token below S in a valid block
+      const int64_t off = ok ? (int64_t)ph[k] * a.kv_sb + (int64_t)(t & (BS - 1)) * a.kv_ss + c * 8 : 0;
+      kreg[k] = *(const uint4 *)(kplane + off);
+      vreg[k] = *(const uint4 *)(vplane + off);
+      if (!ok) { kreg[k] = make_uint4(0, 0, 0, 0); vreg[k] = make_uint4(0, 0, 0, 0); }
+    }
+  };
+  // K rows as they are (padded rows); V transposed: vbuf[dim][token]
+  auto store_stage = [&](int slot) {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int q = tid + k * NW * 64;
+      const int tr = q >> 4, c = q & 15;
+      *(uint4 *)(&kbuf[slot][tr * KROW + c * 16]) = kreg[k];
+      const uint32_t w[4] = {vreg[k].x, vreg[k].y, vreg[k].z, vreg[k].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint16_t v16 = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+        *(uint16_t *)(&vbuf[slot][(c * 8 + e) * VROW + tr * 2]) = v16;
+      }
+    }
+  };
+
+  const float c2 = a.scale * 1.4426950408889634f;  // logits in log2 units
+  float m2 = -INFINITY, lsum = 0.f;
+  f32x16 oacc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) oacc[dt][e] = 0.f;
+
+  if (nst > 0) {
+    stage_phys(phys, 0);
+    load_stage(phys, 0);
+    stage_phys(phys, 1);
+    store_stage(0);
+  }
+  __syncthreads();
+  for (int gs = 0; gs < nst; ++gs) {
+    const int slot = gs & 1;
+    // stage gs+1 into registers (past the end: zero rows, never stored for use)
+    load_stage(phys, gs + 1);
+    stage_phys(phys, gs + 2);
+#pragma unroll
+    for (int b = 0; b < GS; ++b) {
+      const int t0 = gs * ST + 32 * b;
+      // S^T tile: 32 tokens x 32 query rows
+      V8 kf[KS];
+      const unsigned char *kr = &kbuf[slot][(32 * b + lcol) * KROW + lh * 16];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kf[ks] = *(const V8 *)(kr + ks * 32);
+      f32x16 st = {};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        if constexpr (__is_same(T, __bf16))
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], st, 0, 0, 0);
+        else
+          st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks], qf[ks], st, 0, 0, 0);
+      }
+      // online softmax of the lane's query row over the slice
+      float x[16];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int t = t0 + 8 * (e >> 2) + 4 * lh + (e & 3);
+        x[e] = t < lim ? st[e] * c2 : -INFINITY;
+        mx = fmaxf(mx, x[e]);
+      }
+      {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+        mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      }
+      const float m_new = fmaxf(m2, mx);
+      const float msafe = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m2 - msafe);
+      float ps = 0.f;
+      V8 pb[2];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float pe = __builtin_amdgcn_exp2f(x[e] - msafe);
+        ps += pe;
+        pb[e >> 3][e & 7] = (T)pe;
+      }
+      {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ps), __float_as_uint(ps), false, false);
+        ps = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      }
+      lsum = lsum * alpha + ps;
+      m2 = m_new;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[dt][e] *= alpha;
+      // O^T += V^T . P^T: A = V^T[32dt + lcol][tau(kb, lh, 0..7)]
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const unsigned char *vr = &vbuf[slot][(32 * dt + lcol) * VROW + (32 * b + 16 * kb + 4 * lh) * 2];
+          const uint2 lo = *(const uint2 *)vr, hi = *(const uint2 *)(vr + 16);
+          const uint4 u = make_uint4(lo.x, lo.y, hi.x, hi.y);
+          const V8 va = __builtin_bit_cast(V8, u);
+          if constexpr (__is_same(T, __bf16))
+            oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kb], oacc[dt], 0, 0, 0);
+          else
+            oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[kb], oacc[dt], 0, 0, 0);
+        }
+      }
+    }
+    if (gs + 1 < nst) store_stage(slot ^ 1);
+    __syncthreads();
+  }
+
+  // ---- out[dim] = O^T[dim][row] / lsum, lse = ln 2 * (m2 + log2 lsum)
+  if (valid) {
+    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+    float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * G + g) * a.o_sh;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d0 = 32 * dt + 8 * i + 4 * lh;
+        f32x4 v;
+        v[0] = oacc[dt][4 * i] * inv; v[1] = oacc[dt][4 * i + 1] * inv;
+        v[2] = oacc[dt][4 * i + 2] * inv; v[3] = oacc[dt][4 * i + 3] * inv;
+        *(f32x4 *)(op + d0) = v;
+      }
+    if (lh == 0)
+      a.lse[(int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * G + g] =
+          lsum > 0.f ? (m2 + __log2f(lsum)) * 0.6931471805599453f : -INFINITY;
+  }
+}
+
+// ------------------------------------------------------------------ generic path
+// grid L*R*N*Hq, 256 threads: one query row per workgroup.
+template <typename QT, typename KT>
+__global__ void __launch_bounds__(256) attn_generic_kernel(AttnArgs a) {
+  extern __shared__ float sm[];  // q [D], then p [256]
+  float *qs = sm, *ps = sm + a.D;
+  __shared__ float red_m[4], red_l[4];
+  const int64_t id = blockIdx.x;
+  const int hq = (int)(id % a.Hq);
+  const int n = (int)((id / a.Hq) % a.N);
+  const int r = (int)((id / ((int64_t)a.Hq * a.N)) % a.R);
+  const int l = (int)(id / ((int64_t)a.Hq * a.N * a.R));
+  if (n >= attn_nq(a, r)) return;
+  const int S = attn_seq_len(a, r);
+  const int lim = attn_lim(a, r, n, S);
+  const int h = hq / a.G, D = a.D, tid = threadIdx.x;
+  const QT *qp = (const QT *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr + (int64_t)n * a.q_sn + (int64_t)hq * a.q_sh;
+  for (int d = tid; d < D; d += 256) qs[d] = (float)qp[d];
+  __syncthreads();
+  const KT *kplane = (const KT *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh;
+  const KT *vplane = kplane + a.kv_sv;
+  auto row_off = [&](int t) -> int64_t {
+    const int ph = attn_phys(a, r, t / a.BS);
+    return ph < 0 ? -1 : (int64_t)ph * a.kv_sb + (int64_t)(t % a.BS) * a.kv_ss;
+  };
+  auto logit = [&](int t) -> float {
+    const int64_t off = row_off(t);
+    if (off < 0) return -INFINITY;  // a token in a block the table marks invalid
+    float s = 0.f;
+    for (int d = 0; d < D; ++d) s = fmaf(qs[d], (float)kplane[off + d], s);
+    return s * a.scale;
+  };
+  // pass 1: online max / sum per thread, then over the workgroup
+  float m = -INFINITY, sum = 0.f;
+  for (int t = tid; t < lim; t += 256) {
+    const float x = logit(t);
+    if (x == -INFINITY) continue;
+    if (x > m) { sum = sum * expf(m - x) + 1.f; m = x; }
+    else sum += expf(x - m);
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float mo = __shfl_xor(m, o, 64), so = __shfl_xor(sum, o, 64);
+    const float mn = fmaxf(m, mo);
+    sum = (m == -INFINITY ? 0.f : sum * expf(m - mn)) + (mo == -INFINITY ? 0.f : so * expf(mo - mn));
+    m = mn;
+  }
+  if ((tid & 63) == 0) { red_m[tid >> 6] = m; red_l[tid >> 6] = sum; }
+  __syncthreads();
+  float M = -INFINITY;
+  for (int w = 0; w < 4; ++w) M = fmaxf(M, red_m[w]);
+  float Lsum = 0.f;
+  for (int w = 0; w < 4; ++w) Lsum += red_m[w] == -INFINITY ? 0.f : red_l[w] * expf(red_m[w] - M);
+  // pass 2: out = sum_t p_t v_t / Lsum, 256 tokens at a time through LDS
+  float acc0 = 0.f, acc1 = 0.f;  // dims tid and tid + 256 (D <= 512)
+  for (int t0 = 0; t0 < lim; t0 += 256) {
+    __syncthreads();
+    const int t = t0 + tid;
+    float pt = 0.f;
+    if (t < lim) {
+      const float x = logit(t);
+      pt = x == -INFINITY ? 0.f : expf(x - M);
+    }
+    ps[tid] = pt;
+    __syncthreads();
+    const int cnt = min(256, lim - t0);
+    for (int j = 0; j < cnt; ++j) {
+      const float pj = ps[j];
+      if (pj == 0.f) continue;
+      const int64_t off = row_off(t0 + j);
+      if (tid < D) acc0 = fmaf(pj, (float)vplane[off + tid], acc0);
+      if (tid + 256 < D) acc1 = fmaf(pj, (float)vplane[off + tid + 256], acc1);
+    }
+  }
+  float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)hq * a.o_sh;
+  const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
+  if (tid < D) op[tid] = acc0 * inv;
+  if (tid + 256 < D) op[tid + 256] = acc1 * inv;
+  if (tid == 0)
+    a.lse[(int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + hq] =
+        Lsum > 0.f ? M + logf(Lsum) : -INFINITY;
+}
+
+template <typename T, typename V8, int G>
+static int launch_attn_mfma(const AttnArgs &a, int bs_shift, hipStream_t st) {
+  const int pairs = a.L * a.R * a.Hkv;
+  const int rtiles = (a.N * a.G + 31) / 32;
+  const bool causal = a.kv_len != nullptr;
+#define ACTKV_ATTN(NWV)                                                                            \
+  do {                                                                                             \
+    const int ngroups = (rtiles + NWV - 1) / NWV;                                                  \
+    const int grid = ((pairs + 7) / 8) * 8 * ngroups;                                              \
+    if (causal)                                                                                    \
+      hipLaunchKernelGGL((attn_mfma_kernel<T, V8, G, NWV, true>), dim3(grid), dim3(NWV * 64), 0,   \
+                         st, a, pairs, ngroups, bs_shift);                                         \
+    else                                                                                           \
+      hipLaunchKernelGGL((attn_mfma_kernel<T, V8, G, NWV, false>), dim3(grid), dim3(NWV * 64), 0,  \
+                         st, a, pairs, ngroups, bs_shift);                                         \
+  } while (0)
+  if (rtiles <= 1) ACTKV_ATTN(1);
+  else if (rtiles <= 2) ACTKV_ATTN(2);
+  else if (rtiles <= 4) ACTKV_ATTN(4);
+  else ACTKV_ATTN(8);
+#undef ACTKV_ATTN
+  return actkv_check_launch();
+}
+
+template <typename QT, typename KT>
+static int launch_attn_generic(const AttnArgs &a, hipStream_t st) {
+  const int64_t rows = (int64_t)a.L * a.R * a.N * a.Hq;
+  if (rows > 0x7fffffffLL) return ACTKV_ERR_UNSUPPORTED;
+  const size_t shm = (size_t)(a.D + 256) * sizeof(float);
+  hipLaunchKernelGGL((attn_generic_kernel<QT, KT>), dim3((unsigned)rows), dim3(256), shm, st, a);
+  return actkv_check_launch();
+}
+
+template <typename QT>
+static int dispatch_attn_generic(const AttnArgs &a, int kv_dtype, hipStream_t st) {
+  switch (kv_dtype) {
+    case ACTKV_F32: return launch_attn_generic<QT, float>(a, st);
+    case ACTKV_F16: return launch_attn_generic<QT, _Float16>(a, st);
+    case ACTKV_BF16: return launch_attn_generic<QT, __bf16>(a, st);
+  }
+  return ACTKV_ERR_INVALID_ARG;
+}
+
+static bool attn_aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace actkv
+
+using namespace actkv;
+
+extern "C" int actkv_paged_attention(
+    const void *q, int q_dtype, int64_t q_sl, int64_t q_sr, int64_t q_sn, int64_t q_sh,
+    const void *kv, int kv_dtype, int64_t kv_sl, int64_t kv_sv, int64_t kv_sb, int64_t kv_ss,
+    int64_t kv_sh, int64_t num_blocks, const int32_t *block_table, int64_t bt_sr, int max_blocks,
+    const int32_t *seq_used, const int32_t *n_valid, const int32_t *kv_len, float *out,
+    int64_t o_sl, int64_t o_sr, int64_t o_sn, int64_t o_sh, float *lse, int64_t lse_sl,
+    int64_t lse_sr, int64_t lse_sn, int L, int R, int N, int Hq, int Hkv, int D, int block_size,
+    float scale, void *stream) {
+  if (!q || !kv || !block_table || !seq_used || !out || !lse) return ACTKV_ERR_INVALID_ARG;
+  if (L < 1 || R < 1 || N < 0 || Hq < 1 || Hkv < 1 || D < 1 || block_size < 1 || max_blocks < 1 ||
+      num_blocks < 1)
+    return ACTKV_ERR_INVALID_ARG;
+  if (Hq % Hkv != 0 || !(scale > 0.f)) return ACTKV_ERR_INVALID_ARG;
+  if (dtype_size(q_dtype) == 0 || dtype_size(kv_dtype) == 0) return ACTKV_ERR_INVALID_ARG;
+  if ((int64_t)max_blocks * block_size > 0x7fffffffLL || D > 512) return ACTKV_ERR_UNSUPPORTED;
+  if (N == 0) return ACTKV_OK;
+  hipStream_t st = (hipStream_t)stream;
+  AttnArgs a;
+  a.q = q; a.q_sl = q_sl; a.q_sr = q_sr; a.q_sn = q_sn; a.q_sh = q_sh;
+  a.kv = kv; a.kv_sl = kv_sl; a.kv_sv = kv_sv; a.kv_sb = kv_sb; a.kv_ss = kv_ss; a.kv_sh = kv_sh;
+  a.num_blocks = num_blocks;
+  a.bt = block_table; a.bt_sr = bt_sr; a.max_blocks = max_blocks;
+  a.seq_used = seq_used; a.n_valid = n_valid; a.kv_len = kv_len;
+  a.out = out; a.o_sl = o_sl; a.o_sr = o_sr; a.o_sn = o_sn; a.o_sh = o_sh;
+  a.lse = lse; a.lse_sl = lse_sl; a.lse_sr = lse_sr; a.lse_sn = lse_sn;
+  a.L = L; a.R = R; a.N = N; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.G = Hq / Hkv; a.BS = block_size;
+  a.scale = scale;
+  const int G = a.G;
+  int bs_shift = -1;
+  for (int sh = 4; sh < 31; ++sh)
+    if (block_size == (1 << sh)) bs_shift = sh;
+  const bool vec_ok = attn_aligned16(q) && attn_aligned16(kv) && attn_aligned16(out) &&
+                      q_sl % 8 == 0 && q_sr % 8 == 0 && q_sn % 8 == 0 && q_sh % 8 == 0 &&
+                      kv_sl % 8 == 0 && kv_sv % 8 == 0 && kv_sb % 8 == 0 && kv_ss % 8 == 0 &&
+                      kv_sh % 8 == 0 && o_sl % 4 == 0 && o_sr % 4 == 0 && o_sn % 4 == 0 && o_sh % 4 == 0;
+  const bool mfma_ok = q_dtype == kv_dtype && (kv_dtype == ACTKV_BF16 || kv_dtype == ACTKV_F16) &&
+                       D == 128 && (G == 1 || G == 2 || G == 4) && vec_ok && bs_shift >= 0;
+  if (mfma_ok) {
+    if (kv_dtype == ACTKV_BF16)
+      return G == 4 ? launch_attn_mfma<__bf16, bf16x8, 4>(a, bs_shift, st)
+           : G == 2 ? launch_attn_mfma<__bf16, bf16x8, 2>(a, bs_shift, st)
+                    : launch_attn_mfma<__bf16, bf16x8, 1>(a, bs_shift, st);
+    return G == 4 ? launch_attn_mfma<_Float16, f16x8, 4>(a, bs_shift, st)
+         : G == 2 ? launch_attn_mfma<_Float16, f16x8, 2>(a, bs_shift, st)
+                  : launch_attn_mfma<_Float16, f16x8, 1>(a, bs_shift, st);
+  }
+  switch (q_dtype) {
+    case ACTKV_F32: return dispatch_attn_generic<float>(a, kv_dtype, st);
+    case ACTKV_F16: return dispatch_attn_generic<_Float16>(a, kv_dtype, st);
+    default: return dispatch_attn_generic<__bf16>(a, kv_dtype, st);
+  }
+}

@@ -242,6 +242,46 @@ int actkv_lrfu_update(const float *scores, int64_t s_sl, int64_t s_sr, int64_t s
 /* Workspace bytes for actkv_lrfu_update (one float per layer, request and token). */
 size_t actkv_lrfu_workspace_size(int L, int R, int max_seq);
 
+/*
+ * actkv_paged_attention -- paged attention with the log-sum-exp by-product (the
+ * lse producer that actkv_action_scores consumes).
+ *
+ * Replaces actkv/kernels/lse_attn.py:42-60 (`paged_decode_attention_ref`, the
+ * stand-in for a paged FlashAttention backend) and actkv/paged.py:115-118
+ * (`decode_attention`).  The reference takes one query per request; this entry
+ * point takes N queries per request and L layers.  For layer l, request r,
+ * query n < nq (nq = n_valid ? n_valid[r] : N), query head hq (KV head hq / G):
+ *
+ *   s_t = scale * q[l,r,n,hq,:] . k[l,t,hq/G,:]   for t < lim
+ *   lse[l,r,n,hq]   = logsumexp_t s_t
+ *   out[l,r,n,hq,:] = sum_t softmax(s)_t v[l,t,hq/G,:]
+ *
+ * lim = seq_used[r], or min(kv_len[r*N + n], seq_used[r]) when kv_len is
+ * non-NULL (causal limits).  A query with lim = 0 gets lse = -inf, out = 0.
+ * Rows n >= nq are not written.
+ *
+ * q   : dtype q_dtype, [L, R, N, Hq, D], strides q_sl q_sr q_sn q_sh, unit last
+ * kv  : dtype kv_dtype; K plane of layer l at kv + l*kv_sl, V plane at
+ *       kv + l*kv_sl + kv_sv; block stride kv_sb, slot stride kv_ss, head
+ *       stride kv_sh, unit last.  num_blocks bounds every physical id read from
+ *       block_table (ids outside the pool are skipped).
+ * out : float32 [L, R, N, Hq, D], strides o_sl o_sr o_sn o_sh, unit last
+ * lse : float32 [L, R, N, Hq], strides lse_sl lse_sr lse_sn, unit last
+ * bf16/fp16 with D = 128 and Hq/Hkv in {1, 2, 4} run on the matrix cores
+ * (probabilities rounded to the cache dtype for the P.V product, float32
+ * accumulation); every other case uses float32 dot products.  D <= 512.
+ */
+int actkv_paged_attention(
+    const void *q, int q_dtype, int64_t q_sl, int64_t q_sr, int64_t q_sn, int64_t q_sh,
+    const void *kv, int kv_dtype, int64_t kv_sl, int64_t kv_sv, int64_t kv_sb, int64_t kv_ss,
+    int64_t kv_sh, int64_t num_blocks,
+    const int32_t *block_table, int64_t bt_sr, int max_blocks,
+    const int32_t *seq_used, const int32_t *n_valid, const int32_t *kv_len,
+    float *out, int64_t o_sl, int64_t o_sr, int64_t o_sn, int64_t o_sh,
+    float *lse, int64_t lse_sl, int64_t lse_sr, int64_t lse_sn,
+    int L, int R, int N, int Hq, int Hkv, int D, int block_size,
+    float scale, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -40,6 +40,46 @@ def decode_lse(q: torch.Tensor, kv_layer: torch.Tensor, table, seq_used, scale=N
     return lse
 
 
+def gather_v(kv_layer: torch.Tensor, table_row, seq_used: int) -> torch.Tensor:
+    """V rows [S, Hkv, D] of one request in logical order (lse_attn.py:32-40)."""
+    bs = kv_layer.shape[2]
+    nblk = -(-seq_used // bs)
+    blocks = torch.as_tensor(np.asarray(table_row[:nblk], dtype=np.int64))
+    return kv_layer[1].index_select(0, blocks).reshape(-1, kv_layer.shape[3], kv_layer.shape[4])[:seq_used]
+
+
+def paged_attention(q: torch.Tensor, kv_layer: torch.Tensor, table, seq_used, scale=None, kv_len=None,
+                    n_valid=None, dtype=torch.float64):
+    """(out [R, N, Hq, D], lse [R, N, Hq]) float32 of paged attention, accumulated in `dtype`.
+
+    Restates paged_decode_attention_ref (lse_attn.py:42-60): per request, gather K and V, repeat
+    the KV heads over the GQA group, logits = scale * q . k, lse = logsumexp(logits), out =
+    softmax(logits) @ v.  Additive, as the device entry point: N queries per request (q
+    [R, N, Hq, D]), kv_len [R, N] (query n sees tokens t < kv_len[r][n], clamped to seq_used) and
+    n_valid [R] (rows n >= n_valid[r] stay 0).  A query that sees no token gets lse = -inf and
+    out = 0 (torch's logsumexp and softmax-einsum over an empty set)."""
+    r_n, n_q, hq, d = q.shape
+    hkv = kv_layer.shape[3]
+    g = hq // hkv
+    scale = d ** -0.5 if scale is None else scale
+    out = torch.zeros(r_n, n_q, hq, d, dtype=torch.float32)
+    lse = torch.zeros(r_n, n_q, hq, dtype=torch.float32)
+    for r in range(r_n):
+        s = int(seq_used[r])
+        k = gather_k(kv_layer, table[r], s).to(dtype).repeat_interleave(g, dim=1)   # [S, Hq, D]
+        v = gather_v(kv_layer, table[r], s).to(dtype).repeat_interleave(g, dim=1)
+        nv = n_q if n_valid is None else min(max(int(n_valid[r]), 0), n_q)
+        for n in range(nv):
+            lim = s if kv_len is None else min(max(int(kv_len[r][n]), 0), s)
+            if lim == 0:
+                lse[r, n] = -math.inf
+                continue
+            logits = torch.einsum("hd,shd->hs", q[r, n].to(dtype), k[:lim]) * scale     # [Hq, lim]
+            lse[r, n] = torch.logsumexp(logits, -1).float()
+            out[r, n] = torch.einsum("hs,shd->hd", torch.softmax(logits, -1), v[:lim]).float()
+    return out, lse
+
+
 def _group_probs(q_r: torch.Tensor, k: torch.Tensor, lse_r: torch.Tensor, scale: float) -> torch.Tensor:
     """max over the GQA group of exp(scale * q.k - lse): q_r [Hq, D], k [S, Hkv, D] -> [Hkv, S]
     (lse_attn.py:68-72: max over the group first, float32)."""

@@ -1,0 +1,153 @@
+"""Paged attention with the LSE by-product (actkv_paged_attention through
+actkv.kernels.lse_attn.paged_decode_attention and PagedKVCache.decode_attention) against the
+oracle's float64 restatement of lse_attn.py:42-60.
+
+Tolerances:
+- lse: absolute 1e-4. The logits are float32 MFMA dot products; the oracle is float64.
+- out, matrix-core path: the probabilities are rounded to the cache dtype for the P.V
+  product, a relative error of at most 2^-9 (bf16) or 2^-12 (fp16) per term. So out is within
+  that fraction of max|v|: atol 1e-2 (bf16) and 2e-3 (fp16).
+- out, float32 path: 1e-4.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from actkv.kernels.lse_attn import paged_decode_attention
+from actkv.paged import PagedKVCache
+from oracle import reference as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _cache(lens, layers=1, hkv=8, d=128, bs=16, dtype=torch.bfloat16, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    nb = sum(math.ceil(n / bs) for n in lens) + 5
+    cache = PagedKVCache(nb, bs, hkv, d, n_layers=layers, dtype=dtype, device="cuda")
+    cache.free = torch.randperm(nb, generator=g).tolist()
+    for r, n in enumerate(lens):
+        k = torch.randn(layers, n, hkv, d, generator=g).to(dtype)
+        v = torch.randn(layers, n, hkv, d, generator=g).to(dtype)
+        cache.append(r, k.cuda(), v.cuda())
+    return cache
+
+
+def _oracle(cache, reqs, q, layer, kv_len=None, n_valid=None):
+    """q [R, N, Hq, D] (CPU) -> oracle (out, lse) for one layer."""
+    kvl = cache.kv[layer].cpu()
+    tables = [cache.tables[r] for r in reqs]
+    seqs = [cache.seq_used[r] for r in reqs]
+    return ref.paged_attention(q.float(), kvl.float(), tables, seqs, kv_len=kv_len, n_valid=n_valid)
+
+
+def _atol(dtype):
+    return {torch.bfloat16: 1e-2, torch.float16: 2e-3, torch.float32: 1e-4}[dtype]
+
+
+@pytest.mark.parametrize("lens,hq,hkv,n_q,dtype,causal", [
+    ([700, 1500], 32, 8, 1, torch.bfloat16, False),      # decode: one 32-row tile, 4 real rows
+    ([2000, 1337], 32, 8, 64, torch.bfloat16, True),     # action region: 256 rows, causal limits
+    ([900], 16, 8, 40, torch.float16, False),            # GQA 2, 80 rows (3 tiles)
+    ([1100, 64], 8, 8, 100, torch.bfloat16, True),       # GQA 1, 100 rows, a short request
+    ([640], 32, 8, 200, torch.bfloat16, True),           # 800 rows: four groups of 8 tiles
+])
+def test_matrix_core_path_matches_the_oracle(lens, hq, hkv, n_q, dtype, causal):
+    cache = _cache(lens, hkv=hkv, dtype=dtype, seed=len(lens) * 100 + n_q)
+    reqs = list(range(len(lens)))
+    g = torch.Generator().manual_seed(n_q)
+    q = torch.randn(len(lens), n_q, hq, 128, generator=g).to(dtype)
+    kv_len = None
+    if causal:
+        kv_len = torch.stack([torch.randint(0, S + 8, (n_q,), generator=g) for S in lens]).to(torch.int32)
+        kv_len[0, 0] = 0                                           # a query that sees nothing
+    out, lse = cache.decode_attention(reqs, q.cuda(), kv_len=None if kv_len is None else kv_len.cuda())
+    want_out, want_lse = _oracle(cache, reqs, q, 0, kv_len=None if kv_len is None else kv_len.tolist())
+    torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
+    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=_atol(dtype))
+    if causal:
+        assert float(lse[0, 0, 0]) == -math.inf and torch.equal(out[0, 0].cpu(), torch.zeros(hq, 128))
+
+
+def test_reference_signature_one_query_per_request():
+    """q [R, Hq, D] -> out [R, Hq, D], lse [R, Hq], as paged_decode_attention_ref."""
+    cache = _cache([333, 1024, 17], seed=5)
+    q = torch.randn(3, 32, 128, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    out, lse = cache.decode_attention([0, 1, 2], q.cuda())
+    assert tuple(out.shape) == (3, 32, 128) and tuple(lse.shape) == (3, 32)
+    want_out, want_lse = _oracle(cache, [0, 1, 2], q.unsqueeze(1), 0)
+    torch.testing.assert_close(lse.cpu(), want_lse[:, 0], rtol=0, atol=1e-4)
+    torch.testing.assert_close(out.cpu(), want_out[:, 0], rtol=0, atol=1e-2)
+
+
+def test_all_layers_with_ragged_query_counts():
+    """layer=None: q [L, R, N, Hq, D]; n_valid leaves the unused rows at zero."""
+    layers = 3
+    cache = _cache([500, 260], layers=layers, seed=7)
+    g = torch.Generator().manual_seed(8)
+    n_q = 24
+    q = torch.randn(layers, 2, n_q, 32, 128, generator=g).to(torch.bfloat16)
+    n_valid = torch.tensor([24, 9], dtype=torch.int32)
+    out, lse = cache.decode_attention([0, 1], q.cuda(), layer=None, n_valid=n_valid.cuda())
+    assert tuple(out.shape) == (layers, 2, n_q, 32, 128)
+    for l in range(layers):
+        want_out, want_lse = _oracle(cache, [0, 1], q[l], l, n_valid=n_valid.tolist())
+        torch.testing.assert_close(lse[l].cpu(), want_lse, rtol=0, atol=1e-4)
+        torch.testing.assert_close(out[l].cpu(), want_out, rtol=0, atol=1e-2)
+    assert torch.equal(out[:, 1, 9:].cpu(), torch.zeros(layers, n_q - 9, 32, 128))
+
+
+def test_empty_sequence_gives_minus_inf_and_zero():
+    cache = _cache([40, 0], seed=9)
+    assert cache.seq_used[1] == 0
+    q = torch.randn(2, 2, 32, 128).to(torch.bfloat16)
+    out, lse = cache.decode_attention([0, 1], q.cuda())
+    assert torch.isinf(lse[1]).all() and (lse[1] < 0).all()
+    assert torch.equal(out[1].cpu(), torch.zeros(2, 32, 128))
+    want_out, want_lse = _oracle(cache, [0], q[:1], 0)
+    torch.testing.assert_close(lse[:1].cpu(), want_lse, rtol=0, atol=1e-4)
+
+
+@pytest.mark.parametrize("d,hq,hkv,bs,dtype", [
+    (64, 8, 2, 16, torch.bfloat16),      # head_dim 64
+    (32, 4, 2, 16, torch.float32),       # float32 cache
+    (128, 12, 4, 12, torch.float16),     # GQA 3, block size 12
+])
+def test_float32_path_matches_the_oracle(d, hq, hkv, bs, dtype):
+    cache = _cache([150, 77], hkv=hkv, d=d, bs=bs, dtype=dtype, seed=d + hq)
+    g = torch.Generator().manual_seed(bs)
+    q = torch.randn(2, 5, hq, d, generator=g).to(dtype)
+    kv_len = torch.tensor([[150, 3, 0, 90, 151], [1, 77, 40, 2, 60]], dtype=torch.int32)
+    out, lse = cache.decode_attention([0, 1], q.cuda(), kv_len=kv_len.cuda())
+    want_out, want_lse = _oracle(cache, [0, 1], q, 0, kv_len=kv_len.tolist())
+    torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
+    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-4)
+
+
+def test_device_lse_drives_action_scoring():
+    """Algorithm 3 end to end on the device: the attention kernel's lse, fed to cal_attn, gives
+    the oracle's scores computed with the oracle's lse (within the scoring tolerance)."""
+    cache = _cache([1200, 800], seed=11)
+    g = torch.Generator().manual_seed(12)
+    n_q = 32
+    q = torch.randn(2, n_q, 32, 128, generator=g).to(torch.bfloat16)
+    S = [1200, 800]
+    kv_len = torch.stack([torch.arange(s - n_q + 1, s + 1) for s in S]).to(torch.int32)
+    _, lse = cache.decode_attention([0, 1], q.cuda(), kv_len=kv_len.cuda())
+    width = max(len(cache.tables[r]) for r in (0, 1)) * 16
+    out = torch.zeros(2, 8, width, device="cuda")
+    n_seen = torch.zeros(2, dtype=torch.int32, device="cuda")
+    cache.cal_attn([0, 1], q.cuda(), lse, out, n_seen, layer=0, kv_len=kv_len.cuda())
+    _, lse_o = _oracle(cache, [0, 1], q, 0, kv_len=kv_len.tolist())
+    want = torch.zeros(2, 8, width)
+    kvl = cache.kv[0].cpu()
+    for r in range(2):
+        s = cache.seq_used[r]
+        k = ref.gather_k(kvl, cache.tables[r], s).double().repeat_interleave(4, dim=1)
+        for n in range(n_q):
+            lim = int(kv_len[r, n])
+            logits = torch.einsum("hd,shd->hs", q[r, n].double(), k[:lim]) * 128 ** -0.5
+            p = torch.exp(logits - lse_o[r, n].double().unsqueeze(-1)).view(8, 4, lim).amax(1)
+            want[r, :, :lim] += p.float() / n_q
+    torch.testing.assert_close(out.cpu(), want, rtol=1e-3, atol=1e-6)

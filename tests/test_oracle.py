@@ -437,3 +437,66 @@ def test_top_p_mask_total_orders_agree_away_from_the_boundary():
             lo, hi = min(float(thr_a), float(thr_b)), max(float(thr_a), float(thr_b))
             assert bool(((csum >= lo) & (csum <= hi)).any())
     assert differ <= 30
+
+
+# ---------------------------------------------------------------- paged attention (lse producer)
+
+def _v_row(kv, table, bs, t, h):
+    return kv[1, table[t // bs], t % bs, h].double().tolist()
+
+
+def test_paged_attention_matches_the_definition():
+    """out and lse from float64 loops over the definition (lse_attn.py:42-60): GQA 2, two
+    queries per request, causal limits, ragged requests."""
+    bs, hkv, d = 4, 2, 8
+    kv, tables = _cache([11, 6], bs=bs, hkv=hkv, d=d, seed=21)
+    g = torch.Generator().manual_seed(22)
+    q = torch.randn(2, 2, 4, d, generator=g)
+    kv_len = [[5, 11], [6, 3]]
+    out, lse = ref.paged_attention(q, kv, tables, [11, 6], kv_len=kv_len)
+    scale = d ** -0.5
+    for r, S in enumerate([11, 6]):
+        for n in range(2):
+            lim = min(kv_len[r][n], S)
+            for hh in range(4):
+                logits = [scale * sum(a * b for a, b in zip(q[r, n, hh].tolist(), _k_row(kv, tables[r], bs, t, hh // 2)))
+                          for t in range(lim)]
+                m = max(logits)
+                w = [math.exp(x - m) for x in logits]
+                z = sum(w)
+                assert abs(float(lse[r, n, hh]) - (m + math.log(z))) < 1e-5
+                want = [sum(w[t] * _v_row(kv, tables[r], bs, t, hh // 2)[j] for t in range(lim)) / z for j in range(d)]
+                assert max(abs(a - b) for a, b in zip(out[r, n, hh].tolist(), want)) < 1e-5
+
+
+def test_paged_attention_known_answers():
+    """Equal keys give a uniform softmax: out = mean of the V rows, lse = logit + log S; one
+    token gives out = v_0; no token gives lse = -inf, out = 0; rows past n_valid stay 0."""
+    bs, hkv, d = 4, 1, 8
+    kv, tables = _cache([7], bs=bs, hkv=hkv, d=d, seed=23)
+    kv[0] = 0.5                                                    # every key equal
+    q = torch.ones(1, 3, 1, d)
+    out, lse = ref.paged_attention(q, kv, tables, [7], kv_len=[[7, 1, 0]])
+    logit = d ** -0.5 * 0.5 * d
+    vs = torch.stack([torch.tensor(_v_row(kv, tables[0], bs, t, 0), dtype=torch.float64) for t in range(7)])
+    assert abs(float(lse[0, 0, 0]) - (logit + math.log(7))) < 1e-5
+    torch.testing.assert_close(out[0, 0, 0].double(), vs.mean(0), rtol=1e-6, atol=1e-6)
+    assert abs(float(lse[0, 1, 0]) - logit) < 1e-6
+    torch.testing.assert_close(out[0, 1, 0].double(), vs[0], rtol=1e-6, atol=1e-6)
+    assert float(lse[0, 2, 0]) == -math.inf and torch.equal(out[0, 2, 0], torch.zeros(d))
+    out2, lse2 = ref.paged_attention(q, kv, tables, [7], n_valid=[2])
+    assert torch.equal(out2[0, 2], torch.zeros(1, d)) and float(lse2[0, 2, 0]) == 0.0
+
+
+def test_paged_attention_lse_is_decode_lse_and_normalises():
+    """One query per request without limits: lse equals decode_lse (pinned above), and the
+    recovered probabilities exp(s - lse) sum to 1 over the tokens."""
+    kv, tables = _cache([13, 30], bs=4, hkv=2, d=16, seed=24)
+    q = torch.randn(2, 1, 8, 16, generator=torch.Generator().manual_seed(25))
+    out, lse = ref.paged_attention(q, kv, tables, [13, 30])
+    torch.testing.assert_close(lse[:, 0], ref.decode_lse(q[:, 0], kv, tables, [13, 30]), rtol=0, atol=1e-6)
+    for r, S in enumerate([13, 30]):
+        k = ref.gather_k(kv, tables[r], S).double().repeat_interleave(4, dim=1)
+        s = torch.einsum("hd,shd->hs", q[r, 0].double(), k) * 16 ** -0.5
+        tot = torch.exp(s - lse[r, 0].double().unsqueeze(-1)).sum(-1)
+        torch.testing.assert_close(tot, torch.ones(8, dtype=torch.float64), rtol=0, atol=1e-6)

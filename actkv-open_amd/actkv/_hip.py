@@ -74,7 +74,8 @@ _SIGNATURES = {
         _c_p, _c_i64, _c_i64, _c_i64, _c_i64,                    # out, strides
         _c_p, _c_i64, _c_i64, _c_i64,                            # lse, strides
         _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,  # L R N Hq Hkv D bs
-        _c_f, _c_p]),
+        _c_f, _c_p, _c_sz, _c_p]),                               # scale workspace bytes stream
+    "actkv_paged_attention_workspace_size": (_c_sz, [_c_i32] * 8),
 }
 
 _lib = None

@@ -223,7 +223,10 @@ def paged_decode_attention(q, kv, block_table, seq_used, scale=None, *, n_valid=
     alloc = torch.empty if nv is None else torch.zeros
     out = alloc(L, r_n, n_q, hq, d, dtype=torch.float32, device=dev)
     lse = alloc(L, r_n, n_q, hq, dtype=torch.float32, device=dev)
-    rc = _hip.lib().actkv_paged_attention(
+    lib = _hip.lib()
+    nbytes = int(lib.actkv_paged_attention_workspace_size(L, r_n, n_q, hq, hkv, d, bt.shape[1], bs))
+    ws = _hip.scratch(dev, "attention", nbytes) if nbytes else None
+    rc = lib.actkv_paged_attention(
         q5.data_ptr(), _hip.dtype_code(q5.dtype), q5.stride(0), q5.stride(1), q5.stride(2), q5.stride(3),
         kv_k.data_ptr(), _hip.dtype_code(kv.dtype), kv_sl, kv_sv, kv_k.stride(-4), kv_k.stride(-3),
         kv_k.stride(-2), nb,
@@ -231,7 +234,8 @@ def paged_decode_attention(q, kv, block_table, seq_used, scale=None, *, n_valid=
         seq.data_ptr(), _hip.ptr(nv), _hip.ptr(kl),
         out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), out.stride(3),
         lse.data_ptr(), lse.stride(0), lse.stride(1), lse.stride(2),
-        L, r_n, n_q, hq, hkv, d, bs, float(scale), _hip.stream(dev))
+        L, r_n, n_q, hq, hkv, d, bs, float(scale), _hip.ptr(ws), 0 if ws is None else ws.numel(),
+        _hip.stream(dev))
     _hip.check(rc, "actkv_paged_attention")
     for dim in reversed(squeeze):
         out, lse = out.squeeze(dim), lse.squeeze(dim)

@@ -51,6 +51,11 @@ struct AttnArgs {
   int64_t lse_sl, lse_sr, lse_sn;
   int L, R, N, Hq, Hkv, D, G, BS;
   float scale;
+  // token-range split (flash-decoding): chunks per sequence, tokens per chunk, and
+  // the partial results of each chunk (row-major [pair][row][chunk])
+  int nchunk, tpc, rows_pad;
+  float *ws_o;   // [pairs][rows_pad][nchunk][128]: unnormalised sum p v
+  float *ws_ml;  // [pairs][rows_pad][nchunk][2]: running max (log2 units), sum p
 };
 
 __device__ __forceinline__ int attn_seq_len(const AttnArgs &a, int r) {
@@ -89,6 +94,7 @@ template <int NW> struct AttnShape {
 template <typename T, typename V8, int G, int NW, bool CAUSAL>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 2 ? 2 : 1, NW >= 2 ? 2 : 1)))
 attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
+  // work item = (pair, row group, token chunk)
   using SH = AttnShape<NW>;
   constexpr int ST = SH::ST, GS = SH::GS, CPT = SH::CPT, KROW = SH::KROW, VROW = SH::VROW;
   constexpr int KS = 8;
@@ -99,15 +105,21 @@ attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
   // XCD, so the second group's K/V reads hit that XCD's L2.
   const int bid = blockIdx.x;
   const int xcd = bid & 7, jj = bid >> 3;
-  const int p = (jj / ngroups) * 8 + xcd;
-  const int grp = jj % ngroups;
+  const int per_pair = ngroups * a.nchunk;
+  const int p = (jj / per_pair) * 8 + xcd;
+  const int grp = (jj % per_pair) / a.nchunk, chunk = jj % a.nchunk;
   if (p >= pairs) return;
   const int h = p % a.Hkv;
   const int r = (p / a.Hkv) % a.R;
   const int l = p / (a.Hkv * a.R);
   const int nq = attn_nq(a, r);
   if (grp * NW * 32 >= nq * G) return;
-  const int S = attn_seq_len(a, r);
+  const int S_all = attn_seq_len(a, r);
+  // chunks past the sequence hold nothing the combine step reads
+  if (a.nchunk > 1 && chunk * a.tpc >= S_all) return;
+  const int c_begin = min(chunk * a.tpc, S_all);
+  // this chunk's tokens are [c_begin, c_begin + S); token indices below are relative
+  const int S = min(S_all - c_begin, a.tpc);
   const int BS = a.BS;
 
   const int tid = threadIdx.x;
@@ -118,7 +130,8 @@ attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
   const int row = (grp * NW + wave) * 32 + lcol;
   const int n = row / G, g = row % G;
   const bool valid = n < nq;
-  const int lim = valid ? attn_lim(a, r, n, S) : 0;
+  // tokens of this chunk the row sees: [0, lim) relative to the chunk
+  const int lim = valid ? min(max(attn_lim(a, r, n, S_all) - c_begin, 0), S) : 0;
   V8 qf[KS];
   {
     const T *qp = (const T *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr +
@@ -140,7 +153,7 @@ attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int t = g0 * ST + ((tid + k * NW * 64) >> 4);
-      ph[k] = t < S ? attn_phys(a, r, t >> bs_shift) : -1;
+      ph[k] = t < S ? attn_phys(a, r, (c_begin + t) >> bs_shift) : -1;
     }
   };
   uint4 kreg[CPT], vreg[CPT];
@@ -150,7 +163,7 @@ attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
       const int q = tid + k * NW * 64;
       const int t = g0 * ST + (q >> 4), c = q & 15;
       const bool ok = ph[k] >= 0;  // token below S in a valid block
-      const int64_t off = ok ? (int64_t)ph[k] * a.kv_sb + (int64_t)(t & (BS - 1)) * a.kv_ss + c * 8 : 0;
+      const int64_t off = ok ? (int64_t)ph[k] * a.kv_sb + (int64_t)((c_begin + t) & (BS - 1)) * a.kv_ss + c * 8 : 0;
       kreg[k] = *(const uint4 *)(kplane + off);
       vreg[k] = *(const uint4 *)(vplane + off);
       if (!ok) { kreg[k] = make_uint4(0, 0, 0, 0); vreg[k] = make_uint4(0, 0, 0, 0); }
@@ -238,10 +251,14 @@ attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
       }
       lsum = lsum * alpha + ps;
       m2 = m_new;
+      // O is rescaled only when some row of the wave raised its max (alpha < 1); the
+      // running max settles after the first slices, so most slices skip the 64 multiplies
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0ull) {
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+        for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) oacc[dt][e] *= alpha;
+          for (int e = 0; e < 16; ++e) oacc[dt][e] *= alpha;
+      }
       // O^T += V^T . P^T: A = V^T[32dt + lcol][tau(kb, lh, 0..7)]
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
@@ -262,6 +279,23 @@ attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
     __syncthreads();
   }
 
+  // ---- split: the chunk's partial (unnormalised O, max, sum) for the combine kernel
+  if (a.nchunk > 1) {
+    if (valid) {
+      const int64_t pr = ((int64_t)p * a.rows_pad + row) * a.nchunk + chunk;
+      float *wo = a.ws_o + pr * 128;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f32x4 v;
+          v[0] = oacc[dt][4 * i]; v[1] = oacc[dt][4 * i + 1]; v[2] = oacc[dt][4 * i + 2]; v[3] = oacc[dt][4 * i + 3];
+          *(f32x4 *)(wo + 32 * dt + 8 * i + 4 * lh) = v;
+        }
+      if (lh == 0) { a.ws_ml[pr * 2] = m2; a.ws_ml[pr * 2 + 1] = lsum; }
+    }
+    return;
+  }
   // ---- out[dim] = O^T[dim][row] / lsum, lse = ln 2 * (m2 + log2 lsum)
   if (valid) {
     const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
@@ -280,6 +314,44 @@ attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
       a.lse[(int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * G + g] =
           lsum > 0.f ? (m2 + __log2f(lsum)) * 0.6931471805599453f : -INFINITY;
   }
+}
+
+// ------------------------------------------------------------------ split combine
+// grid ceil(pairs*rows_pad/4), 256 threads: one wave per (pair, row), two dims per lane.
+//   M = max_c m_c, w_c = 2^(m_c - M), out = sum_c w_c O_c / sum_c w_c l_c,
+//   lse = ln 2 * (M + log2 sum_c w_c l_c)
+__global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int pairs) {
+  const int64_t id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (id >= (int64_t)pairs * a.rows_pad) return;
+  const int lane = threadIdx.x & 63;
+  const int p = (int)(id / a.rows_pad), row = (int)(id % a.rows_pad);
+  const int h = p % a.Hkv;
+  const int r = (p / a.Hkv) % a.R;
+  const int l = p / (a.Hkv * a.R);
+  const int n = row / a.G, g = row % a.G;
+  if (n >= attn_nq(a, r)) return;
+  const float *ml = a.ws_ml + id * a.nchunk * 2;
+  const float *wo = a.ws_o + id * a.nchunk * 128;
+  // chunks past the sequence were never written: they hold no token of this row
+  const int S_all = attn_seq_len(a, r);
+  const int nc = min(a.nchunk, (S_all + a.tpc - 1) / a.tpc);
+  float M = -INFINITY;
+  for (int c = 0; c < nc; ++c) M = fmaxf(M, ml[2 * c]);
+  const float Ms = M == -INFINITY ? 0.f : M;
+  float Lsum = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int c = 0; c < nc; ++c) {
+    const float w = __builtin_amdgcn_exp2f(ml[2 * c] - Ms);
+    Lsum += w * ml[2 * c + 1];
+    o0 += w * wo[c * 128 + lane];
+    o1 += w * wo[c * 128 + 64 + lane];
+  }
+  const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
+  float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * a.G + g) * a.o_sh;
+  op[lane] = o0 * inv;
+  op[64 + lane] = o1 * inv;
+  if (lane == 0)
+    a.lse[(int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * a.G + g] =
+        Lsum > 0.f ? (M + __log2f(Lsum)) * 0.6931471805599453f : -INFINITY;
 }
 
 // ------------------------------------------------------------------ generic path
@@ -364,27 +436,72 @@ __global__ void __launch_bounds__(256) attn_generic_kernel(AttnArgs a) {
         Lsum > 0.f ? M + logf(Lsum) : -INFINITY;
 }
 
+// Waves per workgroup for a launch: enough 32-row tiles for the pair's query rows, at most 8.
+static int attn_waves(int rtiles) { return rtiles <= 1 ? 1 : rtiles <= 2 ? 2 : rtiles <= 4 ? 4 : 8; }
+
+// Token-range split: enough (pair, row group, chunk) work items for about four rounds of
+// resident workgroups (1 per CU at 8 waves, 2 at 4, 4 at 1-2 waves: the LDS stage
+// buffers), chunks of at least 256 tokens, a whole number of stages each.
+struct AttnSplit { int nchunk, tpc, rows_pad, ngroups; };
+static AttnSplit attn_split(int pairs, int N, int G, int span) {
+  AttnSplit sp;
+  const int rtiles = (N * G + 31) / 32;
+  const int nw = attn_waves(rtiles);
+  const int st = nw >= 4 ? 16 * nw : 32;
+  sp.ngroups = (rtiles + nw - 1) / nw;
+  sp.rows_pad = sp.ngroups * nw * 32;
+  const int per_cu = nw == 8 ? 1 : nw == 4 ? 2 : 4;
+  const int64_t items = (int64_t)pairs * sp.ngroups;
+  const int64_t want = 4LL * 256 * per_cu;
+  int nchunk = (int)std::min<int64_t>(std::max<int64_t>(1, (want + items - 1) / items), std::max(1, span / 256));
+  int tpc = ((span + nchunk - 1) / nchunk + st - 1) / st * st;
+  tpc = std::max(tpc, st);
+  sp.nchunk = (span + tpc - 1) / tpc;
+  sp.tpc = tpc;
+  if (sp.nchunk <= 1) { sp.nchunk = 1; sp.tpc = std::max(span, 1); }
+  return sp;
+}
+
+static size_t attn_ws_bytes(int pairs, const AttnSplit &sp) {
+  if (sp.nchunk <= 1) return 0;
+  return (size_t)pairs * sp.rows_pad * sp.nchunk * (128 + 2) * sizeof(float);
+}
+
 template <typename T, typename V8, int G>
-static int launch_attn_mfma(const AttnArgs &a, int bs_shift, hipStream_t st) {
+static int launch_attn_mfma(AttnArgs a, int bs_shift, void *ws, size_t ws_bytes, hipStream_t st) {
   const int pairs = a.L * a.R * a.Hkv;
   const int rtiles = (a.N * a.G + 31) / 32;
   const bool causal = a.kv_len != nullptr;
+  AttnSplit sp = attn_split(pairs, a.N, a.G, a.max_blocks * a.BS);
+  const size_t need = attn_ws_bytes(pairs, sp);
+  if (sp.nchunk > 1 && (!ws || ws_bytes < need)) {  // no (large enough) workspace: no split
+    sp.nchunk = 1;
+    sp.tpc = std::max(a.max_blocks * a.BS, 1);
+  }
+  a.nchunk = sp.nchunk; a.tpc = sp.tpc; a.rows_pad = sp.rows_pad;
+  a.ws_o = sp.nchunk > 1 ? (float *)ws : nullptr;
+  a.ws_ml = sp.nchunk > 1 ? (float *)((char *)ws + (size_t)pairs * sp.rows_pad * sp.nchunk * 128 * sizeof(float)) : nullptr;
 #define ACTKV_ATTN(NWV)                                                                            \
   do {                                                                                             \
-    const int ngroups = (rtiles + NWV - 1) / NWV;                                                  \
-    const int grid = ((pairs + 7) / 8) * 8 * ngroups;                                              \
+    const int grid = ((pairs + 7) / 8) * 8 * sp.ngroups * sp.nchunk;                               \
     if (causal)                                                                                    \
       hipLaunchKernelGGL((attn_mfma_kernel<T, V8, G, NWV, true>), dim3(grid), dim3(NWV * 64), 0,   \
-                         st, a, pairs, ngroups, bs_shift);                                         \
+                         st, a, pairs, sp.ngroups, bs_shift);                                      \
     else                                                                                           \
       hipLaunchKernelGGL((attn_mfma_kernel<T, V8, G, NWV, false>), dim3(grid), dim3(NWV * 64), 0,  \
-                         st, a, pairs, ngroups, bs_shift);                                         \
+                         st, a, pairs, sp.ngroups, bs_shift);                                      \
   } while (0)
-  if (rtiles <= 1) ACTKV_ATTN(1);
-  else if (rtiles <= 2) ACTKV_ATTN(2);
-  else if (rtiles <= 4) ACTKV_ATTN(4);
-  else ACTKV_ATTN(8);
+  switch (attn_waves(rtiles)) {
+    case 1: ACTKV_ATTN(1); break;
+    case 2: ACTKV_ATTN(2); break;
+    case 4: ACTKV_ATTN(4); break;
+    default: ACTKV_ATTN(8); break;
+  }
 #undef ACTKV_ATTN
+  int rc = actkv_check_launch();
+  if (rc || sp.nchunk <= 1) return rc;
+  const int64_t waves = (int64_t)pairs * sp.rows_pad;
+  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a, pairs);
   return actkv_check_launch();
 }
 
@@ -420,7 +537,7 @@ extern "C" int actkv_paged_attention(
     const int32_t *seq_used, const int32_t *n_valid, const int32_t *kv_len, float *out,
     int64_t o_sl, int64_t o_sr, int64_t o_sn, int64_t o_sh, float *lse, int64_t lse_sl,
     int64_t lse_sr, int64_t lse_sn, int L, int R, int N, int Hq, int Hkv, int D, int block_size,
-    float scale, void *stream) {
+    float scale, void *workspace, size_t workspace_bytes, void *stream) {
   if (!q || !kv || !block_table || !seq_used || !out || !lse) return ACTKV_ERR_INVALID_ARG;
   if (L < 1 || R < 1 || N < 0 || Hq < 1 || Hkv < 1 || D < 1 || block_size < 1 || max_blocks < 1 ||
       num_blocks < 1)
@@ -440,6 +557,7 @@ extern "C" int actkv_paged_attention(
   a.lse = lse; a.lse_sl = lse_sl; a.lse_sr = lse_sr; a.lse_sn = lse_sn;
   a.L = L; a.R = R; a.N = N; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.G = Hq / Hkv; a.BS = block_size;
   a.scale = scale;
+  a.nchunk = 1; a.tpc = max_blocks * block_size; a.rows_pad = 0; a.ws_o = nullptr; a.ws_ml = nullptr;
   const int G = a.G;
   int bs_shift = -1;
   for (int sh = 4; sh < 31; ++sh)
@@ -451,17 +569,29 @@ extern "C" int actkv_paged_attention(
   const bool mfma_ok = q_dtype == kv_dtype && (kv_dtype == ACTKV_BF16 || kv_dtype == ACTKV_F16) &&
                        D == 128 && (G == 1 || G == 2 || G == 4) && vec_ok && bs_shift >= 0;
   if (mfma_ok) {
+    void *ws = workspace;
+    const size_t wb = workspace_bytes;
     if (kv_dtype == ACTKV_BF16)
-      return G == 4 ? launch_attn_mfma<__bf16, bf16x8, 4>(a, bs_shift, st)
-           : G == 2 ? launch_attn_mfma<__bf16, bf16x8, 2>(a, bs_shift, st)
-                    : launch_attn_mfma<__bf16, bf16x8, 1>(a, bs_shift, st);
-    return G == 4 ? launch_attn_mfma<_Float16, f16x8, 4>(a, bs_shift, st)
-         : G == 2 ? launch_attn_mfma<_Float16, f16x8, 2>(a, bs_shift, st)
-                  : launch_attn_mfma<_Float16, f16x8, 1>(a, bs_shift, st);
+      return G == 4 ? launch_attn_mfma<__bf16, bf16x8, 4>(a, bs_shift, ws, wb, st)
+           : G == 2 ? launch_attn_mfma<__bf16, bf16x8, 2>(a, bs_shift, ws, wb, st)
+                    : launch_attn_mfma<__bf16, bf16x8, 1>(a, bs_shift, ws, wb, st);
+    return G == 4 ? launch_attn_mfma<_Float16, f16x8, 4>(a, bs_shift, ws, wb, st)
+         : G == 2 ? launch_attn_mfma<_Float16, f16x8, 2>(a, bs_shift, ws, wb, st)
+                  : launch_attn_mfma<_Float16, f16x8, 1>(a, bs_shift, ws, wb, st);
   }
   switch (q_dtype) {
     case ACTKV_F32: return dispatch_attn_generic<float>(a, kv_dtype, st);
     case ACTKV_F16: return dispatch_attn_generic<_Float16>(a, kv_dtype, st);
     default: return dispatch_attn_generic<__bf16>(a, kv_dtype, st);
   }
+}
+
+extern "C" size_t actkv_paged_attention_workspace_size(int L, int R, int N, int Hq, int Hkv, int D,
+                                                       int max_blocks, int block_size) {
+  if (L < 1 || R < 1 || N < 1 || Hkv < 1 || Hq % Hkv != 0 || max_blocks < 1 || block_size < 1) return 0;
+  const int G = Hq / Hkv;
+  if (D != 128 || !(G == 1 || G == 2 || G == 4)) return 0;  // the float32 path does not split
+  if ((int64_t)max_blocks * block_size > 0x7fffffffLL) return 0;
+  const int pairs = L * R * Hkv;
+  return attn_ws_bytes(pairs, attn_split(pairs, N, G, max_blocks * block_size));
 }

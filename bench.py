@@ -71,6 +71,9 @@ def parse(argv=None):
                     help="run the agent-loop workload instead (rounds of append + causal action scoring + "
                          "LRFU keep + compaction on a 36-layer batch of 4) and print its own JSON line")
     ap.add_argument("--ora-rounds", type=int, default=50)
+    ap.add_argument("--attn", action="store_true",
+                    help="measure the paged attention kernel (the lse producer) instead: the 36-layer "
+                         "32k-token cache with 128 queries, plain and causal, and a batch-8 decode step")
     return ap.parse_args(argv)
 
 
@@ -280,6 +283,92 @@ def load_traffic(path):
         return None
 
 
+def run_attn(args, dev):
+    """Paged attention with the LSE by-product on the main workload's cache shape.
+
+    - queries: 128 action queries per request attending to the whole 32k-token request, every
+      layer in one call (the lse producer of the scoring step), then the same with causal limits
+      (query n sees the first S - 127 + n tokens);
+    - decode: one query per request for a batch of 8 requests of 4k..32k tokens, every layer.
+    Time per call from HIP events around back-to-back calls on the launch stream; FLOPs are
+    4 * N * Hq * S * D per layer (q.k and p.v), bytes are the K and V rows read."""
+    import torch
+    from actkv.kernels.lse_attn import paged_decode_attention, paged_decode_attention_ref
+    from actkv.paged import PagedKVCache
+
+    L, hq, hkv, d, bs = args.layers, args.q_heads, args.kv_heads, args.head_dim, args.block_size
+    gdev = torch.Generator(device=dev).manual_seed(args.seed)
+
+    def make_cache(lens):
+        nb = sum(-(-n // bs) for n in lens) + 16
+        cache = PagedKVCache(nb, bs, hkv, d, n_layers=L, dtype=torch.bfloat16, device=dev)
+        cache.free = torch.randperm(nb, generator=torch.Generator().manual_seed(args.seed)).tolist()
+        for r, n in enumerate(lens):
+            cache._ensure(r, n)
+            cache.seq_used[r] = n
+        cache.kv.normal_(generator=gdev)
+        return cache
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(reps):
+            fn()
+        ev1.record()
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) * 1e3 / reps
+
+    res = {"metric": "paged attention with lse (the lse producer), time per call", "unit": "us",
+           "n_gpus": 1, "higher_is_better": False, "dtype": "bf16", "data": "synthetic"}
+    # 128 queries x 32k tokens, all layers
+    S, N = args.seq, args.queries
+    cache = make_cache([S])
+    seq, bt = cache._device_tables([0])
+    q = torch.randn(L, 1, N, hq, d, generator=gdev, device=dev, dtype=torch.bfloat16)
+    kv_len = torch.arange(S - N + 1, S + 1, device=dev, dtype=torch.int32).view(1, N)
+    flops = 4.0 * N * hq * S * d * L
+    rows = {}
+    for name, kl in (("queries", None), ("queries_causal", kv_len)):
+        us = timed(lambda: paged_decode_attention(q, cache.kv, bt, seq, kv_len=kl), max(args.steps // 4, 3))
+        rows[name] = {"us": round(us, 1), "TFLOPs": round(flops / (us * 1e-6) / 1e12, 1),
+                      "frac_of_bf16_peak": round(flops / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+        log(f"attention {name}: {us:.1f} us, {rows[name]['TFLOPs']} TFLOP/s")
+    res["queries"] = {"workload": f"{L} layers x 1 request x {S} tokens, {N} queries, Hq {hq} / Hkv {hkv}, "
+                                  f"head_dim {d}, block {bs}, bf16", **rows["queries"],
+                      "causal": rows["queries_causal"]}
+    del cache, q
+    torch.cuda.empty_cache()
+    # decode: batch 8, one query each
+    lens = [int(x) for x in np.random.default_rng(args.seed).integers(4096, 32769, 8)]
+    cache = make_cache(lens)
+    reqs = list(range(8))
+    seq, bt = cache._device_tables(reqs)
+    q1 = torch.randn(L, 8, 1, hq, d, generator=gdev, device=dev, dtype=torch.bfloat16)
+    us = timed(lambda: paged_decode_attention(q1, cache.kv, bt, seq), max(args.steps, 5))
+    nbytes = 2.0 * sum(lens) * hkv * d * 2 * L
+    dec = {"workload": f"{L} layers x 8 requests ({min(lens)}..{max(lens)} tokens), 1 query each, bf16",
+           "us": round(us, 1), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+           "frac_of_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    # the reference's stand-in (torch gather + einsum, lse_attn.py:42-60) on the same GPU, one layer
+    q0 = q1[0, :, 0].contiguous()
+    t_ref = timed(lambda: paged_decode_attention_ref(q0, cache.kv[0], bt, seq), 3)
+    t_one = timed(lambda: paged_decode_attention(q0, cache.kv[0], bt, seq), 10)
+    dec["one_layer_us"] = round(t_one, 1)
+    dec["torch_reference_one_layer_us"] = round(t_ref, 1)
+    res["decode"] = dec
+    res["value"] = rows["queries"]["us"]
+    res["config"] = {"workload": res["queries"]["workload"], "parallelism": "single-gpu"}
+    res["gpu"] = torch.cuda.get_device_name(dev)
+    line = json.dumps(res)
+    print(line)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(line + "\n")
+    return 0
+
+
 def run_ora(args, dev):
     """Agent-loop workload: 50 rounds on a Qwen3-8B-shaped 36-layer cache holding 4 sequences.
     Each round appends, per sequence, U[512, 2048] observation + U[128, 512] reasoning +
@@ -397,6 +486,8 @@ def main(argv=None):
     torch.cuda.set_device(dev)
     if args.ora:
         return run_ora(args, dev)
+    if args.attn:
+        return run_attn(args, dev)
 
     log(f"building the {args.layers}-layer workload")
     w = Workload(args, args.layers, dev)

@@ -270,6 +270,10 @@ size_t actkv_lrfu_workspace_size(int L, int R, int max_seq);
  * bf16/fp16 with D = 128 and Hq/Hkv in {1, 2, 4} run on the matrix cores
  * (probabilities rounded to the cache dtype for the P.V product, float32
  * accumulation); every other case uses float32 dot products.  D <= 512.
+ * workspace: optional, actkv_paged_attention_workspace_size(...) bytes, any
+ * contents.  With it, long sequences are split into token chunks attended in
+ * parallel and merged by a second launch (flash-decoding); without it (NULL or
+ * smaller), every sequence is attended by one workgroup per row group.
  */
 int actkv_paged_attention(
     const void *q, int q_dtype, int64_t q_sl, int64_t q_sr, int64_t q_sn, int64_t q_sh,
@@ -280,7 +284,12 @@ int actkv_paged_attention(
     float *out, int64_t o_sl, int64_t o_sr, int64_t o_sn, int64_t o_sh,
     float *lse, int64_t lse_sl, int64_t lse_sr, int64_t lse_sn,
     int L, int R, int N, int Hq, int Hkv, int D, int block_size,
-    float scale, void *stream);
+    float scale, void *workspace, size_t workspace_bytes, void *stream);
+
+/* Workspace bytes that let actkv_paged_attention split long sequences (0: it
+ * does not split this shape). */
+size_t actkv_paged_attention_workspace_size(int L, int R, int N, int Hq, int Hkv, int D,
+                                            int max_blocks, int block_size);
 
 #ifdef __cplusplus
 }

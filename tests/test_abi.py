@@ -87,6 +87,22 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     # compact: both a pinned mask and a pinned count
     cp[17], cp[18] = fake, fake
     assert lib.actkv_compact(*cp) == 1
+    # paged_attention: null q, GQA mismatch, non-positive scale, head_dim past 512, N = 0
+    pa = [None, 2, 0, 0, 0, 0, fake, 2, 0, 0, 0, 0, 0, 10, fake, 0, 1, fake, None, None,
+          fake, 0, 0, 0, 0, fake, 0, 0, 0, 1, 1, 1, 32, 8, 128, 16, 0.1, None, 0, None]
+    assert lib.actkv_paged_attention(*pa) == 1
+    pa[0] = fake
+    pa[32], pa[33] = 30, 8                               # Hq % Hkv != 0
+    assert lib.actkv_paged_attention(*pa) == 1
+    pa[32] = 32
+    pa[36] = 0.0                                         # scale must be positive
+    assert lib.actkv_paged_attention(*pa) == 1
+    pa[36] = 0.1
+    pa[34] = 1024                                        # head_dim beyond the kernels
+    assert lib.actkv_paged_attention(*pa) == 2
+    pa[34] = 128
+    pa[31] = 0                                           # no queries: nothing to do
+    assert lib.actkv_paged_attention(*pa) == 0
 
 
 @pytest.mark.parametrize("bad", ["missing"])

@@ -151,3 +151,22 @@ def test_device_lse_drives_action_scoring():
             p = torch.exp(logits - lse_o[r, n].double().unsqueeze(-1)).view(8, 4, lim).amax(1)
             want[r, :, :lim] += p.float() / n_q
     torch.testing.assert_close(out.cpu(), want, rtol=1e-3, atol=1e-6)
+
+
+def test_token_split_and_single_pass_agree(monkeypatch):
+    """With a workspace, long sequences are split into token chunks and merged by the combine
+    launch; without one, one workgroup attends the whole sequence. Both match the oracle."""
+    from actkv import _hip
+    cache = _cache([4000, 2500], seed=13)
+    g = torch.Generator().manual_seed(14)
+    q = torch.randn(2, 16, 32, 128, generator=g).to(torch.bfloat16)
+    kv_len = torch.stack([torch.randint(1, S + 1, (16,), generator=g) for S in (4000, 2500)]).to(torch.int32)
+    lib = _hip.lib()
+    assert lib.actkv_paged_attention_workspace_size(1, 2, 16, 32, 8, 128, len(cache.tables[0]), 16) > 0
+    split_out, split_lse = cache.decode_attention([0, 1], q.cuda(), kv_len=kv_len.cuda())
+    monkeypatch.setattr(lib, "actkv_paged_attention_workspace_size", lambda *a: 0)
+    one_out, one_lse = cache.decode_attention([0, 1], q.cuda(), kv_len=kv_len.cuda())
+    want_out, want_lse = _oracle(cache, [0, 1], q, 0, kv_len=kv_len.tolist())
+    for out, lse in ((split_out, split_lse), (one_out, one_lse)):
+        torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
+        torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-2)

@@ -85,10 +85,12 @@ __device__ __forceinline__ int attn_phys(const AttnArgs &a, int r, int b) {
 template <int NW> struct AttnShape {
   static constexpr int ST = NW >= 4 ? 16 * NW : 32;  // tokens per stage
   static constexpr int GS = ST / 32;                  // 32-token slices per stage
-  static constexpr int CPT = ST * 16 / (NW * 64);     // 16-byte chunks per thread per stage (K and V each)
+  // a thread stages (4-token group, 16-byte chunk) pairs: 4 K rows and 4 V rows of one chunk
+  static constexpr int PPT = (ST / 4) * 16 / (NW * 64);
   static constexpr int KROW = 272;                    // padded K row (bytes)
-  static constexpr int VROW = ST * 2 + 8;             // padded V^T row: ST tokens of one dim
-  static constexpr int KSTAGE = ST * KROW, VSTAGE = 128 * VROW;
+  // V stage: [token group][dim][4 tokens], 8 bytes per (group, dim)
+  static constexpr int KSTAGE = ST * KROW, VSTAGE = ST * 128 * 2;
+  static_assert(PPT >= 1 && (ST / 4) * 16 % (NW * 64) == 0, "whole pairs per thread");
 };
 
 template <typename T, typename V8, int G, int NW, bool CAUSAL>
@@ -96,7 +98,7 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW
 attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
   // work item = (pair, row group, token chunk)
   using SH = AttnShape<NW>;
-  constexpr int ST = SH::ST, GS = SH::GS, CPT = SH::CPT, KROW = SH::KROW, VROW = SH::VROW;
+  constexpr int ST = SH::ST, GS = SH::GS, PPT = SH::PPT, KROW = SH::KROW;
   constexpr int KS = 8;
   __shared__ __attribute__((aligned(16))) unsigned char kbuf[2][SH::KSTAGE];
   __shared__ __attribute__((aligned(16))) unsigned char vbuf[2][SH::VSTAGE];
@@ -132,6 +134,8 @@ attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
   const bool valid = n < nq;
   // tokens of this chunk the row sees: [0, lim) relative to the chunk
   const int lim = valid ? min(max(attn_lim(a, r, n, S_all) - c_begin, 0), S) : 0;
+  // the masking limit: padding rows (never written) see everything, so they never force it
+  const int lim_m = valid ? lim : 0x7fffffff;
   V8 qf[KS];
   {
     const T *qp = (const T *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr +
@@ -144,43 +148,58 @@ attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
     }
   }
 
-  // ---- stage loads: chunk q = tid + k*NW*64 of a stage is row q/16, 16-byte chunk q%16
+  // ---- stage loads: pair q = tid + k*NW*64 of a stage is token group q/16 (tokens
+  // 4(q/16) .. +3, one block: groups never straddle a block of >= 16 tokens) and 16-byte
+  // chunk q%16 (dims 8(q%16) .. +7)
   const T *kplane = (const T *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh;
   const T *vplane = kplane + a.kv_sv;
   const int nst = (S + ST - 1) / ST;
-  int phys[CPT];  // physical blocks of this thread's rows of the next stage to load
-  auto stage_phys = [&](int (&ph)[CPT], int g0) {
+  int phys[PPT];  // physical block of each of this thread's token groups of the next stage
+  auto stage_phys = [&](int (&ph)[PPT], int g0) {
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
-      const int t = g0 * ST + ((tid + k * NW * 64) >> 4);
+    for (int k = 0; k < PPT; ++k) {
+      const int t = g0 * ST + 4 * ((tid + k * NW * 64) >> 4);
       ph[k] = t < S ? attn_phys(a, r, (c_begin + t) >> bs_shift) : -1;
     }
   };
-  uint4 kreg[CPT], vreg[CPT];
-  auto load_stage = [&](const int (&ph)[CPT], int g0) {
+  uint4 kreg[PPT][4], vreg[PPT][4];
+  auto load_stage = [&](const int (&ph)[PPT], int g0) {
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
+    for (int k = 0; k < PPT; ++k) {
       const int q = tid + k * NW * 64;
-      const int t = g0 * ST + (q >> 4), c = q & 15;
-      const bool ok = ph[k] >= 0;  // token below S in a valid block
-      const int64_t off = ok ? (int64_t)ph[k] * a.kv_sb + (int64_t)((c_begin + t) & (BS - 1)) * a.kv_ss + c * 8 : 0;
-      kreg[k] = *(const uint4 *)(kplane + off);
-      vreg[k] = *(const uint4 *)(vplane + off);
-      if (!ok) { kreg[k] = make_uint4(0, 0, 0, 0); vreg[k] = make_uint4(0, 0, 0, 0); }
+      const int t4 = g0 * ST + 4 * (q >> 4), c = q & 15;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t4 + i;
+        const bool ok = ph[k] >= 0 && t < S;  // a token of the chunk in a valid block
+        const int64_t off = ok ? (int64_t)ph[k] * a.kv_sb + (int64_t)((c_begin + t) & (BS - 1)) * a.kv_ss + c * 8 : 0;
+        kreg[k][i] = *(const uint4 *)(kplane + off);
+        vreg[k][i] = *(const uint4 *)(vplane + off);
+        if (!ok) { kreg[k][i] = make_uint4(0, 0, 0, 0); vreg[k][i] = make_uint4(0, 0, 0, 0); }
+      }
     }
   };
-  // K rows as they are (padded rows); V transposed: vbuf[dim][token]
+  // K rows as they are (padded rows); V as [group][dim][4 tokens]: the 4x8 block of 16-bit
+  // values is transposed in registers and written as four 16-byte stores
   auto store_stage = [&](int slot) {
 #pragma unroll
-    for (int k = 0; k < CPT; ++k) {
+    for (int k = 0; k < PPT; ++k) {
       const int q = tid + k * NW * 64;
-      const int tr = q >> 4, c = q & 15;
-      *(uint4 *)(&kbuf[slot][tr * KROW + c * 16]) = kreg[k];
-      const uint32_t w[4] = {vreg[k].x, vreg[k].y, vreg[k].z, vreg[k].w};
+      const int tg = q >> 4, c = q & 15;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint16_t v16 = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
-        *(uint16_t *)(&vbuf[slot][(c * 8 + e) * VROW + tr * 2]) = v16;
+      for (int i = 0; i < 4; ++i) *(uint4 *)(&kbuf[slot][(4 * tg + i) * KROW + c * 16]) = kreg[k][i];
+      unsigned char *vd = &vbuf[slot][(tg * 128 + 8 * c) * 8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {  // dims 8c + 2j and 8c + 2j + 1
+        auto word = [j](const uint4 &v) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; };
+        const uint32_t w0 = word(vreg[k][0]), w1 = word(vreg[k][1]);
+        const uint32_t w2 = word(vreg[k][2]), w3 = word(vreg[k][3]);
+        uint4 o;
+        o.x = (w0 & 0xffffu) | (w1 << 16);          // dim 2j: tokens 0, 1
+        o.y = (w2 & 0xffffu) | (w3 << 16);          //         tokens 2, 3
+        o.z = (w0 >> 16) | (w1 & 0xffff0000u);      // dim 2j+1: tokens 0, 1
+        o.w = (w2 >> 16) | (w3 & 0xffff0000u);      //           tokens 2, 3
+        *(uint4 *)(vd + 16 * j) = o;
       }
     }
   };
@@ -205,10 +224,8 @@ attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
     // stage gs+1 into registers (past the end: zero rows, never stored for use)
     load_stage(phys, gs + 1);
     stage_phys(phys, gs + 2);
-#pragma unroll
-    for (int b = 0; b < GS; ++b) {
-      const int t0 = gs * ST + 32 * b;
-      // S^T tile: 32 tokens x 32 query rows
+    // S^T of slice b of this stage: 32 tokens x 32 query rows (dot products, unscaled)
+    auto qk = [&](int b) {
       V8 kf[KS];
       const unsigned char *kr = &kbuf[slot][(32 * b + lcol) * KROW + lh * 16];
 #pragma unroll
@@ -221,27 +238,34 @@ attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
         else
           st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks], qf[ks], st, 0, 0, 0);
       }
-      // online softmax of the lane's query row over the slice
-      float x[16];
-      float mx = -INFINITY;
+      return st;
+    };
+    // online softmax of the lane's query row over slice b, then O^T += V^T . P^T
+    auto softmax_pv = [&](f32x16 st, int b) {
+      const int t0 = gs * ST + 32 * b;
+      // tokens at or past a row's limit are masked; slices every row sees whole skip this
+      if (__builtin_amdgcn_ballot_w64(lim_m < t0 + 32) != 0ull) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int t = t0 + 8 * (e >> 2) + 4 * lh + (e & 3);
-        x[e] = t < lim ? st[e] * c2 : -INFINITY;
-        mx = fmaxf(mx, x[e]);
+        for (int e = 0; e < 16; ++e) {
+          const int t = t0 + 8 * (e >> 2) + 4 * lh + (e & 3);
+          st[e] = t < lim_m ? st[e] : -INFINITY;
+        }
       }
+      float mx = st[0];
+#pragma unroll
+      for (int e = 1; e < 16; ++e) mx = fmaxf(mx, st[e]);
       {
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
         mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
       }
-      const float m_new = fmaxf(m2, mx);
+      const float m_new = fmaxf(m2, mx * c2);  // log2 units (c2 > 0)
       const float msafe = m_new == -INFINITY ? 0.f : m_new;
       const float alpha = __builtin_amdgcn_exp2f(m2 - msafe);
       float ps = 0.f;
       V8 pb[2];
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const float pe = __builtin_amdgcn_exp2f(x[e] - msafe);
+        const float pe = __builtin_amdgcn_exp2f(fmaf(st[e], c2, -msafe));
         ps += pe;
         pb[e >> 3][e & 7] = (T)pe;
       }
@@ -264,8 +288,10 @@ attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
-          const unsigned char *vr = &vbuf[slot][(32 * dt + lcol) * VROW + (32 * b + 16 * kb + 4 * lh) * 2];
-          const uint2 lo = *(const uint2 *)vr, hi = *(const uint2 *)(vr + 16);
+          // tokens 32b + 16kb + 4lh + 0..3 (group g1) and + 8 .. + 11 (group g1 + 2)
+          const int g1 = 8 * b + 4 * kb + lh;
+          const unsigned char *vr = &vbuf[slot][(g1 * 128 + 32 * dt + lcol) * 8];
+          const uint2 lo = *(const uint2 *)vr, hi = *(const uint2 *)(vr + 2 * 128 * 8);
           const uint4 u = make_uint4(lo.x, lo.y, hi.x, hi.y);
           const V8 va = __builtin_bit_cast(V8, u);
           if constexpr (__is_same(T, __bf16))
@@ -274,6 +300,16 @@ attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
             oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[kb], oacc[dt], 0, 0, 0);
         }
       }
+    };
+    // the next slice's S^T chain is issued before this slice's softmax, so the matrix
+    // core works while the VALU does the exp/max/sum
+    f32x16 st_cur = qk(0);
+#pragma unroll
+    for (int b = 0; b < GS; ++b) {
+      f32x16 st_next = {};
+      if (b + 1 < GS) st_next = qk(b + 1);
+      softmax_pv(st_cur, b);
+      st_cur = st_next;
     }
     if (gs + 1 < nst) store_stage(slot ^ 1);
     __syncthreads();

@@ -12,6 +12,7 @@ from __future__ import annotations
 import ctypes
 import os
 
+import numpy as np
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libactkv_hip.so")
@@ -147,13 +148,62 @@ def stream(device: torch.device) -> int:
 _workspaces: dict = {}
 
 
+class _PinnedRing:
+    """Host-to-device int32 uploads through a ring of pinned staging buffers.
+
+    Allocating pinned memory per call (torch's pin_memory) can stall the host for tens of
+    milliseconds when a new size is first needed; the ring allocates a few buffers, grown
+    geometrically, and reuses each one once the copy that last read it has completed (an event
+    recorded after the copy; with 8 buffers it has completed long before)."""
+
+    SLOTS = 8
+
+    def __init__(self):
+        self.bufs = [None] * self.SLOTS
+        self.events = [None] * self.SLOTS
+        self.i = 0
+
+    def upload_i32(self, values, device: torch.device) -> torch.Tensor:
+        arr = np.asarray(values, dtype=np.int32).reshape(-1)
+        n = arr.size
+        k = self.i % self.SLOTS
+        self.i += 1
+        if self.events[k] is not None:
+            self.events[k].synchronize()
+        buf = self.bufs[k]
+        if buf is None or buf.numel() < n:
+            old = 0 if buf is None else buf.numel()
+            buf = torch.empty(max(n, 2 * old, 1 << 14), dtype=torch.int32, pin_memory=True)
+            self.bufs[k] = buf
+        buf.numpy()[:n] = arr
+        out = buf[:n].to(device, non_blocking=True)
+        if self.events[k] is None:
+            self.events[k] = torch.cuda.Event()
+        self.events[k].record()
+        return out
+
+
+_rings: dict = {}
+
+
+def upload_i32(values, device: torch.device) -> torch.Tensor:
+    """Host ints -> a new device int32 tensor, asynchronously on the current stream."""
+    ring = _rings.get(device)
+    if ring is None:
+        ring = _rings[device] = _PinnedRing()
+    return ring.upload_i32(values, device)
+
+
 def scratch(device: torch.device, key, nbytes: int) -> torch.Tensor:
     """A cached uint8 device buffer of at least nbytes for `key`, grown on demand (contents
     undefined).  Calls sharing it are ordered on the current stream."""
     full = (device, key)
     buf = _workspaces.get(full)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(int(nbytes), 1 << 16), dtype=torch.uint8, device=device)
+        # grown geometrically: a workload whose sizes creep up reallocates a few times, not
+        # on every call (a device allocation can cost milliseconds)
+        old = 0 if buf is None else buf.numel()
+        buf = torch.empty(max(int(nbytes), 2 * old, 1 << 16), dtype=torch.uint8, device=device)
         _workspaces[full] = buf
     return buf
 
@@ -165,6 +215,7 @@ def workspace(device: torch.device, kind: int, r: int, max_seq: int) -> torch.Te
     key = (device, kind)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < need:
-        ws = torch.empty(max(need, 1 << 16), dtype=torch.uint8, device=device)
+        old = 0 if ws is None else ws.numel()
+        ws = torch.empty(max(need, 2 * old, 1 << 16), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws

@@ -39,9 +39,9 @@ class CompactionPlan:
 
 
 def upload_i32(values, device) -> torch.Tensor:
-    """Host ints -> device int32 through pinned memory, without synchronising the stream."""
-    host = torch.tensor(values, dtype=torch.int32).pin_memory()
-    return host.to(device, non_blocking=True)
+    """Host ints -> device int32 through reused pinned staging memory, without synchronising
+    the stream."""
+    return _hip.upload_i32(values, device)
 
 
 def keep_words(seq_used: int, block_size: int) -> int:

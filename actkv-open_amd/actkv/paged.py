@@ -236,9 +236,7 @@ class PagedKVCache:
     def _upload(self, host: np.ndarray) -> torch.Tensor:
         if torch.device(self.device).type != "cuda":
             return torch.from_numpy(host.copy()).to(self.device)
-        pinned = torch.empty(host.size, dtype=torch.int32, pin_memory=True)
-        pinned.numpy()[:] = host
-        return pinned.to(self.device, non_blocking=True)
+        return _hip.upload_i32(host, torch.device(self.device))
 
     def _device_tables(self, reqs, ys=None):
         """(seq_used [R], block_table [R, MB]) int32 on the device, reused while the requests'

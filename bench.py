@@ -373,8 +373,9 @@ def run_ora(args, dev):
     """Agent-loop workload: 50 rounds on a Qwen3-8B-shaped 36-layer cache holding 4 sequences.
     Each round appends, per sequence, U[512, 2048] observation + U[128, 512] reasoning +
     U[32, 64] action tokens (bf16 K/V ~ N(0,1), seeded), scores the action tokens against the
-    cache with causal limits (action token j sees the prefix and action tokens <= j, exact
-    lse), updates the LRFU keep scores (decay 0.5, top-p 0.9), keeps 4 sinks plus the top
+    cache with causal limits (action token j sees the prefix and action tokens <= j; their lse
+    comes from the paged attention kernel, untimed, as from the model's forward pass), updates
+    the LRFU keep scores (decay 0.5, top-p 0.9), keeps 4 sinks plus the top
     `budget` tokens by the layer-average keep score (budget rising linearly 4096 -> 16384) and
     compacts.  Timed per round with HIP events: scoring + LRFU update + keep + compaction."""
     import torch
@@ -410,22 +411,13 @@ def run_ora(args, dev):
         nmax = max(n_act)
         q = torch.randn(L, R, nmax, hq, d, generator=gdev, device=dev, dtype=torch.bfloat16)
         kv_len = torch.zeros(R, nmax, dtype=torch.int32, device=dev)
-        lse = torch.zeros(L, R, nmax, hq, device=dev)
-        g = hq // hkv
         for j, r in enumerate(reqs):
             S = cache.seq_used[r]
             kv_len[j, : n_act[j]] = torch.arange(S - n_act[j] + 1, S + 1, device=dev, dtype=torch.int32)
-            slots = cache.slot_map(r)
-            pos = torch.arange(S, device=dev)
-            mask = pos[None, :] < kv_len[j, : n_act[j], None].long()              # [a, S]
-            for l in range(L):
-                kf = cache.kv[l, 0].reshape(-1, hkv, d)[slots].float()           # [S, Hkv, D]
-                for h in range(hkv):
-                    qh = q[l, j, : n_act[j], h * g:(h + 1) * g].float()           # [a, G, D]
-                    lg = (qh @ kf[:, h].t().contiguous()) * scale                 # [a, G, S]
-                    lg = lg.masked_fill(~mask[:, None, :], float("-inf"))
-                    lse[l, j, : n_act[j], h * g:(h + 1) * g] = torch.logsumexp(lg, -1)
         n_valid = torch.tensor(n_act, dtype=torch.int32, device=dev)
+        # the action tokens' attention and its lse (causal), as the model's forward pass
+        # produces them; outside the timed region
+        _, lse = cache.decode_attention(reqs, q, layer=None, scale=scale, n_valid=n_valid, kv_len=kv_len)
         tokens_before = sum(cache.seq_used[r] for r in reqs)
         free_before = len(cache.free)
         lr.begin_round()
@@ -434,14 +426,17 @@ def run_ora(args, dev):
         # kernel ends on this runtime, so the round is not split
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
         ev[0].record()
+        h0 = time.perf_counter()
         cache.cal_attn(reqs, q, lse, lr.scores, lr.n_seen, layer=None, n_valid=n_valid, kv_len=kv_len)
         lr.evict(budget, protected=sinks, n_action=n_act)
+        h1 = time.perf_counter()
         ev[1].record()
         torch.cuda.synchronize()
         per_round.append({"round": rnd, "budget": budget, "tokens_before": tokens_before,
                           "tokens_after": sum(cache.seq_used[r] for r in reqs),
                           "blocks_reclaimed": len(cache.free) - free_before,
-                          "evict_us": ev[0].elapsed_time(ev[1]) * 1e3})
+                          "evict_us": ev[0].elapsed_time(ev[1]) * 1e3,
+                          "host_us": (h1 - h0) * 1e6})
         if rnd % 10 == 0 or rnd == rounds - 1:
             pr = per_round[-1]
             log(f"round {rnd}: {pr['tokens_before']} -> {pr['tokens_after']} tokens, "

@@ -77,6 +77,14 @@ _SIGNATURES = {
         _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,  # L R N Hq Hkv D bs
         _c_f, _c_p, _c_sz, _c_p]),                               # scale workspace bytes stream
     "actkv_paged_attention_workspace_size": (_c_sz, [_c_i32] * 8),
+    "actkv_append": (_c_i32, [
+        _c_p, _c_i32, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,  # kv, sl sv sb ss sh, num_blocks
+        _c_p, _c_p, _c_i32,                                            # k v src_dtype
+        _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,                # k strides, v strides
+        _c_i32, _c_i32, _c_i32, _c_i32,                                # L Hkv D R
+        _c_p, _c_p, _c_p, _c_i64,                                      # starts counts src_off total
+        _c_p, _c_i64, _c_i32, _c_i32, _c_p, _c_p]),                    # table bt_sr mb bs bad stream
+    "actkv_slot_map": (_c_i32, [_c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p]),
 }
 
 _lib = None

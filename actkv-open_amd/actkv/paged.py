@@ -195,15 +195,90 @@ class PagedKVCache:
                 table.extend(ids)
 
     def append(self, req: int, k: torch.Tensor, v: torch.Tensor) -> None:
-        """k, v: [n_layers, n, Hkv, D] new tokens for request `req`."""
+        """k, v: [n_layers, n, Hkv, D] new tokens for request `req`.
+
+        On a GPU cache one actkv_append launch writes every layer's K and V rows (converted to
+        the cache dtype); the blocks come from the host free stack first, as in the reference.
+        Reference: actkv/paged.py:76-84."""
         n = k.shape[1]
         start = self.seq_used.get(req, 0)
         self._ensure(req, start + n)
-        slots = self.slot_map(req, start + n)[start:]
-        flat = self.kv.view(self.n_layers, 2, -1, self.n_kv_heads, self.head_dim)
-        flat[:, 0, slots] = k.to(device=self.kv.device, dtype=self.kv.dtype)
-        flat[:, 1, slots] = v.to(device=self.kv.device, dtype=self.kv.dtype)
+        if self.kv.device.type == "cuda":
+            self._append_device([req], [start], [n], k, v)
+        else:
+            # a CPU-resident cache (host-side allocator use): the same copy in torch
+            slots = self.slot_map(req, start + n)[start:]
+            flat = self.kv.view(self.n_layers, 2, -1, self.n_kv_heads, self.head_dim)
+            flat[:, 0, slots] = k.to(device=self.kv.device, dtype=self.kv.dtype)
+            flat[:, 1, slots] = v.to(device=self.kv.device, dtype=self.kv.dtype)
         self.seq_used[req] = start + n
+
+    def append_batch(self, reqs, k: torch.Tensor, v: torch.Tensor, counts=None) -> None:
+        """Append to several requests in one launch: k, v [n_layers, sum(counts), Hkv, D] hold
+        the requests' new tokens back to back (counts defaults to one token each, a decode
+        step).  Blocks are allocated request by request in the order given, so the free stack
+        ends exactly as after the same append() calls in a loop.  GPU caches only."""
+        reqs = list(reqs)
+        counts = [1] * len(reqs) if counts is None else [int(c) for c in counts]
+        if len(counts) != len(reqs) or len(set(reqs)) != len(reqs):
+            raise ValueError("append_batch: one count per request, each request once")
+        if sum(counts) != k.shape[1] or v.shape[1] != k.shape[1]:
+            raise ValueError(f"append_batch: k/v hold {k.shape[1]} tokens, counts sum to {sum(counts)}")
+        _hip.require_gpu("PagedKVCache.append_batch", self.kv)
+        starts = []
+        for r, c in zip(reqs, counts):
+            start = self.seq_used.get(r, 0)
+            self._ensure(r, start + c)
+            starts.append(start)
+        self._append_device(reqs, starts, counts, k, v)
+        for r, s0, c in zip(reqs, starts, counts):
+            self.seq_used[r] = s0 + c
+
+    def _append_src(self, x: torch.Tensor, total: int) -> torch.Tensor:
+        """A source operand as [L, total, Hkv, D] on the cache's device with a unit last stride
+        (broadcasting like the reference's indexed assignment); dtypes the kernel does not read
+        are converted to the cache dtype first, which is the reference's own conversion."""
+        x = x.to(device=self.kv.device)
+        if x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            x = x.to(self.kv.dtype)
+        x = torch.broadcast_to(x, (self.n_layers, total, self.n_kv_heads, self.head_dim))
+        return x if x.stride(-1) == 1 else x.contiguous()
+
+    def _append_device(self, reqs, starts, counts, k, v) -> None:
+        total = sum(counts)
+        if total == 0:
+            return
+        if k.dtype != v.dtype:
+            # one source dtype per launch: convert both as the reference does, straight to the
+            # cache dtype (through the other source dtype could round twice)
+            k, v = k.to(self.kv.dtype), v.to(self.kv.dtype)
+        k = self._append_src(k, total)
+        v = self._append_src(v, total)
+        r_n = len(reqs)
+        tabs = [_as_i32(self.tables[r]) for r in reqs]
+        mb = max(max(t.size for t in tabs), 1)
+        # one upload: src_off (int64, as lo/hi int32 pairs), starts, counts, block tables
+        host = np.zeros(4 * r_n + r_n * mb, dtype=np.int32)
+        off = np.concatenate([[0], np.cumsum(counts[:-1])]).astype(np.int64)
+        host[: 2 * r_n] = off.view(np.int32)
+        host[2 * r_n: 3 * r_n] = starts
+        host[3 * r_n: 4 * r_n] = counts
+        grid = host[4 * r_n:].reshape(r_n, mb)
+        for i, t in enumerate(tabs):
+            grid[i, : t.size] = t
+        dev = self._upload(host)
+        kv = self.kv
+        if kv.stride(-1) != 1:
+            raise RuntimeError("PagedKVCache.kv must have a unit last stride")
+        rc = _hip.lib().actkv_append(
+            kv.data_ptr(), _hip.dtype_code(kv.dtype), kv.stride(0), kv.stride(1), kv.stride(2),
+            kv.stride(3), kv.stride(4), self.num_blocks,
+            k.data_ptr(), v.data_ptr(), _hip.dtype_code(k.dtype),
+            k.stride(0), k.stride(1), k.stride(2), v.stride(0), v.stride(1), v.stride(2),
+            self.n_layers, self.n_kv_heads, self.head_dim, r_n,
+            dev[2 * r_n:].data_ptr(), dev[3 * r_n:].data_ptr(), dev.data_ptr(), total,
+            dev[4 * r_n:].data_ptr(), mb, mb, self.block_size, None, _hip.stream(kv.device))
+        _hip.check(rc, "actkv_append")
 
     def release(self, req: int) -> None:
         self.free.extend(reversed(self.tables.pop(req, [])))
@@ -213,10 +288,25 @@ class PagedKVCache:
 
     # ---------------------------------------------------------------- views
     def slot_map(self, req: int, n: int | None = None) -> torch.Tensor:
+        """Physical slot of each of the first n logical positions (int64 [n]); on a GPU cache
+        computed by actkv_slot_map from the request's device block table.
+        Reference: actkv/paged.py:93-97."""
         n = self.seq_used[req] if n is None else n
-        table = torch.tensor(self.tables[req], dtype=torch.long, device=self.device)
-        pos = torch.arange(n, device=self.device)
-        return table[pos // self.block_size] * self.block_size + pos % self.block_size
+        if self.kv.device.type != "cuda":
+            table = torch.tensor(self.tables[req], dtype=torch.long, device=self.device)
+            pos = torch.arange(n, device=self.device)
+            return table[pos // self.block_size] * self.block_size + pos % self.block_size
+        table = self.tables[req]
+        if n < 0 or n > len(table) * self.block_size:
+            raise IndexError(f"slot_map: {n} positions, the table covers {len(table) * self.block_size}")
+        out = torch.empty(n, dtype=torch.long, device=self.kv.device)
+        if n == 0:
+            return out
+        _, bt = self._device_tables([req])
+        rc = _hip.lib().actkv_slot_map(bt.data_ptr(), bt.shape[1], 0, n, self.block_size, out.data_ptr(),
+                                       _hip.stream(self.kv.device))
+        _hip.check(rc, "actkv_slot_map")
+        return out
 
     def _host_tables(self, reqs, ys=None):
         """[len(reqs) + R*MB] int32 host array: seq_used values, then the block tables (first

@@ -25,6 +25,7 @@ of the same workload on this host) and checks of the step's results.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -71,6 +72,9 @@ def parse(argv=None):
                     help="run the agent-loop workload instead (rounds of append + causal action scoring + "
                          "LRFU keep + compaction on a 36-layer batch of 4) and print its own JSON line")
     ap.add_argument("--ora-rounds", type=int, default=50)
+    ap.add_argument("--no-gc-freeze", action="store_true",
+                    help="agent loop: leave the startup heap in the collected generations (by default it "
+                         "is frozen after setup, as a serving process does after loading)")
     ap.add_argument("--attn", action="store_true",
                     help="measure the paged attention kernel (the lse producer) instead: the 36-layer "
                          "32k-token cache with 128 queries, plain and causal, and a batch-8 decode step")
@@ -369,10 +373,24 @@ def run_attn(args, dev):
     return 0
 
 
+def _append_summary(per_round, L, hkv, d):
+    """Append launches of the agent loop: bf16 source rows read and cache rows written, K and
+    V planes of every layer (algorithmic bytes 2 planes x 2 (read + write) x L x Hkv x D x 2 B
+    per token)."""
+    us = [p["append_us"] for p in per_round]
+    gbs = [p["appended"] * 2 * 2 * L * hkv * d * 2 / (p["append_us"] * 1e-6) / 1e9 for p in per_round]
+    return {"tokens_per_round_median": int(statistics.median(p["appended"] for p in per_round)),
+            "us_median": round(statistics.median(us), 1),
+            "GBps_median": round(statistics.median(gbs), 1),
+            "pct_of_hbm_peak": round(100 * statistics.median(gbs) / HBM_PEAK_GBS, 1),
+            "host_us_median": round(statistics.median(p["append_host_us"] for p in per_round), 1)}
+
+
 def run_ora(args, dev):
     """Agent-loop workload: 50 rounds on a Qwen3-8B-shaped 36-layer cache holding 4 sequences.
     Each round appends, per sequence, U[512, 2048] observation + U[128, 512] reasoning +
-    U[32, 64] action tokens (bf16 K/V ~ N(0,1), seeded), scores the action tokens against the
+    U[32, 64] action tokens (bf16 K/V ~ N(0,1), seeded; one batched append launch, timed on
+    its own and reported beside the eviction), scores the action tokens against the
     cache with causal limits (action token j sees the prefix and action tokens <= j; their lse
     comes from the paged attention kernel, untimed, as from the model's forward pass), updates
     the LRFU keep scores (decay 0.5, top-p 0.9), keeps 4 sinks plus the top
@@ -396,18 +414,43 @@ def run_ora(args, dev):
     lr = PagedLRFU(cache, reqs, cap, LRFUConfig(decay=0.5, top_p=0.9))
     scale = d ** -0.5
     per_round = []
+    # Python's collector: a full collection walks every tracked object of the process
+    # (torch's import alone leaves hundreds of thousands) and stalls the host for tens of
+    # milliseconds when it lands inside a round; time spent collecting is recorded per round
+    gc_ms = [0.0, 0.0]
+
+    def _gc_clock(phase, info):
+        if phase == "start":
+            gc_ms[1] = time.perf_counter()
+        else:
+            gc_ms[0] += (time.perf_counter() - gc_ms[1]) * 1e3
+
+    gc.callbacks.append(_gc_clock)
+    if not args.no_gc_freeze:
+        gc.collect()
+        gc.freeze()
     log(f"agent loop: {rounds} rounds, {R} sequences, {L} layers")
     for rnd in range(rounds):
         budget = int(round(b_lo + (b_hi - b_lo) * rnd / max(rounds - 1, 1)))
-        n_act = []
+        n_act, counts = [], []
         for r in reqs:
             n_new = int(rng.integers(512, 2049)) + int(rng.integers(128, 513))
             a = int(rng.integers(32, 65))
             n_act.append(a)
-            k = torch.randn(L, n_new + a, hkv, d, generator=gdev, device=dev, dtype=torch.bfloat16)
-            v = torch.randn(L, n_new + a, hkv, d, generator=gdev, device=dev, dtype=torch.bfloat16)
-            cache.append(r, k, v)
-            del k, v
+            counts.append(n_new + a)
+        k = torch.randn(L, sum(counts), hkv, d, generator=gdev, device=dev, dtype=torch.bfloat16)
+        v = torch.randn(L, sum(counts), hkv, d, generator=gdev, device=dev, dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        # the round's new tokens of all sequences, every layer, in one append launch
+        ea = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ea[0].record()
+        gc_ms[0] = 0.0
+        ha0 = time.perf_counter()
+        cache.append_batch(reqs, k, v, counts)
+        ha1 = time.perf_counter()
+        gc_append = gc_ms[0]
+        ea[1].record()
+        del k, v
         nmax = max(n_act)
         q = torch.randn(L, R, nmax, hq, d, generator=gdev, device=dev, dtype=torch.bfloat16)
         kv_len = torch.zeros(R, nmax, dtype=torch.int32, device=dev)
@@ -426,17 +469,24 @@ def run_ora(args, dev):
         # kernel ends on this runtime, so the round is not split
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
         ev[0].record()
+        gc_ms[0] = 0.0
         h0 = time.perf_counter()
         cache.cal_attn(reqs, q, lse, lr.scores, lr.n_seen, layer=None, n_valid=n_valid, kv_len=kv_len)
         lr.evict(budget, protected=sinks, n_action=n_act)
         h1 = time.perf_counter()
+        gc_round = gc_ms[0]
         ev[1].record()
         torch.cuda.synchronize()
         per_round.append({"round": rnd, "budget": budget, "tokens_before": tokens_before,
                           "tokens_after": sum(cache.seq_used[r] for r in reqs),
                           "blocks_reclaimed": len(cache.free) - free_before,
                           "evict_us": ev[0].elapsed_time(ev[1]) * 1e3,
-                          "host_us": (h1 - h0) * 1e6})
+                          "host_us": (h1 - h0) * 1e6,
+                          "gc_us": gc_round * 1e3,
+                          "appended": sum(counts),
+                          "append_us": ea[0].elapsed_time(ea[1]) * 1e3,
+                          "append_host_us": (ha1 - ha0) * 1e6,
+                          "append_gc_us": gc_append * 1e3})
         if rnd % 10 == 0 or rnd == rounds - 1:
             pr = per_round[-1]
             log(f"round {rnd}: {pr['tokens_before']} -> {pr['tokens_after']} tokens, "
@@ -453,6 +503,9 @@ def run_ora(args, dev):
         "evict_us": {"mean": round(statistics.mean(lat), 1), "median": round(statistics.median(lat), 1),
                      "p90": round(lat[int(0.9 * (len(lat) - 1))], 1), "max": round(lat[-1], 1)},
         "evict_us_per_layer_median": round(statistics.median(lat) / L, 2),
+        "append": _append_summary(per_round, L, hkv, d),
+        "gc_frozen": not args.no_gc_freeze,
+        "gc_us_max": round(max(p["gc_us"] for p in per_round), 1),
         "blocks_reclaimed_total": sum(p["blocks_reclaimed"] for p in per_round),
         "per_round": [{k: (round(v, 1) if isinstance(v, float) else v) for k, v in p.items()} for p in per_round],
         "gpu": torch.cuda.get_device_name(dev),

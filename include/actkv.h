@@ -291,6 +291,43 @@ int actkv_paged_attention(
 size_t actkv_paged_attention_workspace_size(int L, int R, int N, int Hq, int Hkv, int D,
                                             int max_blocks, int block_size);
 
+/*
+ * actkv_append -- write appended tokens into the paged cache, every layer and both
+ * planes, for R requests in one launch.
+ *
+ * Replaces the data movement of actkv/paged.py:76-84 (`PagedKVCache.append`):
+ *   kv[l, 0, slot(starts[r] + i)] = k[l, src_off[r] + i].to(kv dtype), same for V,
+ *   slot(t) = block_table[r, t / block_size] * block_size + t % block_size,
+ * for i < counts[r]; total = sum of counts.  The blocks must already be in the
+ * table: allocation (paged.py:67-74, the free-block stack) is the caller's, as in
+ * the reference.  Conversions round to nearest even (torch's .to()).
+ * kv : dtype kv_dtype; K plane of layer l at kv + l*kv_sl, V plane + kv_sv; block,
+ *      slot and head strides kv_sb kv_ss kv_sh, unit last (elements).
+ * k, v : dtype src_dtype, [L, >=total, Hkv, D]; strides (k_sl, k_sn, k_sh) and
+ *      (v_sl, v_sn, v_sh), unit last.
+ * starts, counts : int32 [R]; src_off : int64 [R]; block_table int32 [R, bt_sr].
+ * bad (optional): set to 1 if a destination block is missing from the table or
+ *      outside the pool (that token is skipped).
+ * Rows that are 16-byte aligned with D a multiple of 8 move 8 elements per thread;
+ * any other layout one element per thread.  Strides may be 0 (broadcast sources).
+ */
+int actkv_append(void *kv, int kv_dtype, int64_t kv_sl, int64_t kv_sv, int64_t kv_sb,
+                 int64_t kv_ss, int64_t kv_sh, int64_t num_blocks,
+                 const void *k, const void *v, int src_dtype,
+                 int64_t k_sl, int64_t k_sn, int64_t k_sh, int64_t v_sl, int64_t v_sn, int64_t v_sh,
+                 int L, int Hkv, int D, int R, const int32_t *starts, const int32_t *counts,
+                 const int64_t *src_off, int64_t total,
+                 const int32_t *block_table, int64_t bt_sr, int max_blocks, int block_size,
+                 int32_t *bad, void *stream);
+
+/*
+ * actkv_slot_map -- out[i] = table_row[t / block_size] * block_size + t % block_size
+ * for t = start + i, i < n (int64; -1 past the table's nblocks entries).
+ * Replaces actkv/paged.py:93-97 (`slot_map`, which is the start = 0 case).
+ */
+int actkv_slot_map(const int32_t *table_row, int nblocks, int start, int n, int block_size,
+                   int64_t *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -103,6 +103,21 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     pa[34] = 128
     pa[31] = 0                                           # no queries: nothing to do
     assert lib.actkv_paged_attention(*pa) == 0
+    # append: null cache, unknown dtype, no tokens; slot_map: null table, nothing to map
+    ap = [None, 2, 0, 0, 0, 0, 0, 4, fake, fake, 2, 0, 0, 0, 0, 0, 0, 1, 1, 8, 1, fake, fake, fake, 3,
+          fake, 1, 1, 16, None, None]
+    assert lib.actkv_append(*ap) == 1
+    ap[0] = fake
+    ap[10] = 9
+    assert lib.actkv_append(*ap) == 1
+    ap[10] = 2
+    ap[24] = 0
+    assert lib.actkv_append(*ap) == 0
+    ap[28] = 0                                           # block_size must be positive
+    assert lib.actkv_append(*ap) == 1
+    assert lib.actkv_slot_map(None, 1, 0, 4, 16, fake, None) == 1
+    assert lib.actkv_slot_map(fake, 1, 0, 0, 16, fake, None) == 0
+    assert lib.actkv_slot_map(fake, 1, -1, 4, 16, fake, None) == 1
 
 
 @pytest.mark.parametrize("bad", ["missing"])

@@ -359,6 +359,26 @@ def test_model_free_list_is_a_stack():
     assert m.free == [5, 4, 3, 1, 0]
 
 
+def test_model_append_and_slot_map_known_answer():
+    """Blocks are popped from the end of the free stack as each append needs them and token
+    t lives at table[t // bs] * bs + t % bs (paged.py:67-84, :93-97)."""
+    m = ref.PagedCacheModel(6, 2, 1, 1, 2, np_dtype=np.float32)
+    m.free = [3, 0, 5, 1, 4, 2]
+    tok = np.arange(1, 8, dtype=np.float32).reshape(1, 7, 1, 1)
+    m.append(7, np.concatenate([tok[:, :3]] * 2), -np.concatenate([tok[:, :3]] * 2))
+    assert m.tables[7] == [2, 4] and m.free == [3, 0, 5, 1]
+    m.append(7, np.concatenate([tok[:, 3:]] * 2), -np.concatenate([tok[:, 3:]] * 2))
+    assert m.tables[7] == [2, 4, 1, 5] and m.free == [3, 0] and m.seq_used[7] == 7
+    assert m.slot_map(7).tolist() == [4, 5, 8, 9, 2, 3, 10]
+    flat = m.kv.reshape(2, 2, 12)
+    for layer in range(2):
+        assert flat[layer, 0, [4, 5, 8, 9, 2, 3, 10]].tolist() == list(range(1, 8))
+        assert flat[layer, 1, [4, 5, 8, 9, 2, 3, 10]].tolist() == [-t for t in range(1, 8)]
+    assert flat[:, :, [0, 1, 6, 7, 11]].sum() == 0
+    k, v = m.gather(7, layer=1)
+    assert k.ravel().tolist() == list(range(1, 8)) and v.ravel().tolist() == [-t for t in range(1, 8)]
+
+
 # ---------------------------------------------------------------- LRFU keep score
 
 def test_top_p_mask_known_answer():

@@ -1,0 +1,299 @@
+"""A paged-cache backend for Hugging Face transformers models, and an ActKV session on it.
+
+The reference runs models only through a contiguous DynamicCache (actkv/hf/session.py):
+- scores come from `output_attentions` on eager attention (session.py:150-156);
+- compression is an `index_select` of every layer's keys and values (session.py:195-206).
+It names a paged backend that scores with the LSE-recovery kernel as the missing piece
+(session.py:12-14; README.md:153, "no model runs on it").  This module is that backend:
+
+  PagedHFCache     a transformers `Cache` over a PagedKVCache for a batch of requests.  A
+                   forward's first layer allocates the new tokens' blocks from the host free
+                   stack (once per step); every layer's `update` then writes its K/V rows
+                   with one actkv_append launch.
+  paged_attention_forward
+                   the attention function, registered as "actkv_paged": actkv_paged_attention
+                   over the layer's paged K/V, causal within the step's new tokens, returning
+                   the output and keeping q and the LSE of action tokens for scoring.
+  PagedSession     prefill / decode / rounds for a batch of sequences.  Action tokens' q and
+                   LSE are kept as they are decoded; `end_round` scores them all in one
+                   cal_attn launch (Algorithm 3, each with its causal limit: the cache does not
+                   change inside a round, so this equals scoring at every step) and compresses
+                   with the device LRFU policy (Algorithm 1) and the paged compaction.
+
+Positions follow the reference's two counters (session.py:4-10): RoPE uses each sequence's
+logical position (`seen`), while the paged cache holds the physical tokens; masks are not
+built (the kernels apply causality from the cache's lengths).
+"""
+from __future__ import annotations
+
+import threading
+
+import numpy as np
+import torch
+
+from .. import _hip
+from ..kernels.lrfu import LRFUConfig, PagedLRFU
+from ..kernels.lse_attn import paged_decode_attention
+from ..paged import PagedKVCache
+
+try:  # transformers is optional for the rest of the package
+    from transformers import AttentionInterface
+    from transformers.cache_utils import Cache, CacheLayerMixin
+    from transformers.masking_utils import AttentionMaskInterface
+except ImportError as e:  # pragma: no cover
+    raise ImportError("actkv.hf needs transformers") from e
+
+ATTN_NAME = "actkv_paged"
+
+_tls = threading.local()   # the step being run by this thread's forward pass
+
+
+class _Step:
+    """One forward pass over the batch: n new tokens per request."""
+
+    __slots__ = ("cache", "n", "starts", "plan", "seq", "bt", "kv_len", "capture", "q", "lse", "written")
+
+    def __init__(self, cache, n, starts, plan, seq, bt, kv_len, capture):
+        self.cache, self.n, self.starts, self.plan = cache, n, starts, plan
+        self.seq, self.bt, self.kv_len, self.capture = seq, bt, kv_len, capture
+        self.q, self.lse = {}, {}
+        self.written = 0
+
+
+class _PagedLayer(CacheLayerMixin):
+    """One model layer's view of the paged cache (writes go through the owner)."""
+
+    is_sliding = False
+    is_compileable = False
+
+    def __init__(self, owner: "PagedHFCache", idx: int):
+        super().__init__()
+        self.owner, self.idx = owner, idx
+        self.is_initialized = True
+
+    def lazy_initialization(self, key_states, value_states) -> None:
+        pass
+
+    def update(self, key_states, value_states, *args, **kwargs):
+        self.owner._write(self.idx, key_states, value_states)
+        return key_states, value_states
+
+    def get_mask_sizes(self, query_length: int):
+        return self.owner.get_seq_length() + query_length, 0
+
+    def get_seq_length(self) -> int:
+        return self.owner.get_seq_length()
+
+    def get_max_length(self) -> int:
+        return -1
+
+    def reset(self) -> None:
+        raise NotImplementedError("release the requests of the PagedKVCache instead")
+
+    def reorder_cache(self, beam_idx) -> None:
+        raise NotImplementedError("beam reordering is not supported by the paged cache")
+
+
+class PagedHFCache(Cache):
+    """transformers Cache over `kv` (a PagedKVCache) for the requests `reqs`, batch row i being
+    request reqs[i].  Every layer of the model maps to the same layer of `kv`."""
+
+    def __init__(self, kv: PagedKVCache, reqs):
+        self.kv = kv
+        self.reqs = list(reqs)
+        super().__init__(layers=[_PagedLayer(self, i) for i in range(kv.n_layers)])
+        self.step: _Step | None = None
+        self.capture = False      # keep q and lse of the next steps (action tokens)
+
+    def get_seq_length(self, layer_idx: int = 0) -> int:
+        return max((self.kv.seq_used.get(r, 0) for r in self.reqs), default=0)
+
+    def begin_step(self, n: int) -> _Step:
+        """Allocate n new tokens per request (host free stack, request order, as n appends)
+        and prepare the device side once for all layers."""
+        kv = self.kv
+        starts = [kv.seq_used.get(r, 0) for r in self.reqs]
+        for r, s in zip(self.reqs, starts):
+            kv._ensure(r, s + n)
+        plan = kv._append_plan(self.reqs, starts, [n] * len(self.reqs))
+        for r, s in zip(self.reqs, starts):
+            kv.seq_used[r] = s + n
+        seq, bt = kv._device_tables(self.reqs)
+        kv_len = None
+        if n > 1:   # query j of the step sees the prefix and new tokens <= j
+            lim = np.asarray(starts, dtype=np.int32)[:, None] + np.arange(1, n + 1, dtype=np.int32)[None, :]
+            kv_len = kv._upload(lim.reshape(-1)).view(len(self.reqs), n)
+        self.step = _Step(self, n, starts, plan, seq, bt, kv_len, self.capture)
+        _tls.step = self.step
+        return self.step
+
+    def _write(self, layer: int, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        b, hkv, n, d = key_states.shape
+        if b != len(self.reqs):
+            raise ValueError(f"batch of {b} rows, the cache serves {len(self.reqs)} requests")
+        st = self.step
+        if layer == 0 or st is None or st.written >= self.kv.n_layers:
+            st = self.begin_step(n)
+        elif st.n != n:
+            raise RuntimeError("layers of one forward pass wrote different token counts")
+        _tls.step = st
+        if self.kv.kv.device.type != "cuda":
+            # a CPU-resident cache (host-side use): the same rows written with torch
+            flat = self.kv.kv[layer].view(2, -1, hkv, d)
+            for i, r in enumerate(self.reqs):
+                slots = self.kv.slot_map(r, st.starts[i] + n)[st.starts[i]:]
+                flat[0, slots] = key_states[i].transpose(0, 1).to(flat.dtype)
+                flat[1, slots] = value_states[i].transpose(0, 1).to(flat.dtype)
+            st.written += 1
+            return
+        # [B, Hkv, n, D] -> [1, B*n, Hkv, D]: request r's tokens are rows r*n .. r*n + n - 1
+        k = key_states.transpose(1, 2)
+        v = value_states.transpose(1, 2)
+        k = (k if k.is_contiguous() else k.contiguous()).view(1, b * n, hkv, d)
+        v = (v if v.is_contiguous() else v.contiguous()).view(1, b * n, hkv, d)
+        self.kv._append_launch(st.plan, k, v, layer=layer)
+        st.written += 1
+
+
+def paged_attention_forward(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
+    """Attention of `query` [B, Hq, n, D] over the layer's paged K/V (the step's new tokens
+    included, causal among them).  Returns ([B, n, Hq, D] in the query dtype, None)."""
+    st = getattr(_tls, "step", None)
+    if st is None:
+        raise RuntimeError("actkv_paged attention runs with a PagedHFCache as past_key_values")
+    layer = module.layer_idx
+    kv = st.cache.kv
+    q = query.transpose(1, 2)                       # [B, n, Hq, D] view, unit last stride
+    out, lse = paged_decode_attention(q, kv.kv[layer], st.bt, st.seq, scaling, kv_len=st.kv_len)
+    if st.capture:
+        st.q[layer], st.lse[layer] = q, lse
+    return out.to(query.dtype), None
+
+
+def _no_mask(*args, **kwargs):
+    return None
+
+
+def register() -> str:
+    """Register the attention function (and a no-op mask builder) under "actkv_paged"."""
+    AttentionInterface.register(ATTN_NAME, paged_attention_forward)
+    AttentionMaskInterface.register(ATTN_NAME, _no_mask)
+    return ATTN_NAME
+
+
+class PagedSession:
+    """A batch of sequences served by `model` on a paged cache, compressed with ActKV.
+
+    prefill(ids [B, n], protected)   prompt tokens; protected ones are never evicted
+    decode(ids [B], in_action [B])   one token per sequence; action tokens are kept for scoring
+    begin_round()                    a new observation-reasoning-action round (Algorithm 1)
+    end_round(budget)                score the round's action tokens (one launch over every
+                                     layer), update the LRFU keep scores, keep the protected
+                                     tokens plus the top `budget`, compact
+    Returns logits of each sequence's last position.  Reference: actkv/hf/session.py:91-206
+    (prefill, generate, end_round, _compress), with the paged cache instead of DynamicCache."""
+
+    def __init__(self, model, batch: int, max_tokens: int, num_blocks: int | None = None,
+                 block_size: int = 16, lrfu: LRFUConfig | None = None):
+        cfg = model.config
+        types = set(getattr(cfg, "layer_types", None) or ["full_attention"])
+        if types != {"full_attention"}:
+            raise NotImplementedError(f"layer types {sorted(types)}: only full-attention layers are paged")
+        p = next(model.parameters())
+        dev, dtype = p.device, p.dtype
+        _hip.require_gpu("PagedSession", p)
+        self.model = model
+        self.n_layers = cfg.num_hidden_layers
+        self.n_kv = getattr(cfg, "num_key_value_heads", cfg.num_attention_heads)
+        self.n_q = cfg.num_attention_heads
+        self.head_dim = getattr(cfg, "head_dim", cfg.hidden_size // cfg.num_attention_heads)
+        if num_blocks is None:
+            num_blocks = batch * (-(-max_tokens // block_size) + 1)
+        self.kv = PagedKVCache(num_blocks, block_size, self.n_kv, self.head_dim, n_layers=self.n_layers,
+                               dtype=dtype, device=dev)
+        self.reqs = list(range(batch))
+        self.cache = PagedHFCache(self.kv, self.reqs)
+        self.lrfu = PagedLRFU(self.kv, self.reqs, max_tokens, lrfu or LRFUConfig())
+        self.seen = [0] * batch           # logical positions (RoPE)
+        self.protected = [0] * batch      # protected prefix length
+        self.n_action = [0] * batch       # action tokens kept this round
+        self._act = []                    # per decode step with action tokens: (q, lse, kv_len, mask)
+        model.set_attn_implementation(register())
+
+    # ------------------------------------------------------------------ forward
+    @torch.no_grad()
+    def _forward(self, ids: torch.Tensor, capture: bool):
+        b, n = ids.shape
+        dev = self.kv.kv.device
+        pos = torch.as_tensor(self.seen, device=dev)[:, None] + torch.arange(n, device=dev)[None, :]
+        self.cache.capture = capture
+        try:
+            out = self.model(input_ids=ids.to(dev), past_key_values=self.cache, position_ids=pos,
+                             attention_mask={"full_attention": None}, use_cache=True, logits_to_keep=1)
+        finally:
+            self.cache.capture = False
+        self.seen = [s + n for s in self.seen]
+        return out.logits[:, -1]
+
+    def prefill(self, ids: torch.Tensor, protected: bool = False) -> torch.Tensor:
+        """ids [B, n] (or [n] for one sequence).  Protected tokens are pinned at the first
+        compression (the reference's `protected` prefix, session.py:113-124)."""
+        ids = ids.view(len(self.reqs), -1)
+        if ids.shape[1] == 0:
+            raise ValueError("empty prefill")
+        logits = self._forward(ids, capture=False)
+        if protected:
+            self.protected = [self.kv.seq_used[r] for r in self.reqs]
+        return logits
+
+    def begin_round(self) -> None:
+        self.lrfu.begin_round()
+        self.n_action = [0] * len(self.reqs)
+        self._act = []
+
+    def decode(self, ids: torch.Tensor, in_action=None) -> torch.Tensor:
+        """ids [B]: one new token per sequence.  in_action [B] bools (or one bool): which of the
+        tokens belong to an action region and are scored at the round's end."""
+        b = len(self.reqs)
+        flags = [bool(in_action)] * b if in_action is None or isinstance(in_action, bool) else \
+            [bool(x) for x in in_action]
+        capture = any(flags)
+        logits = self._forward(ids.view(b, 1), capture)
+        if capture:
+            st = self.cache.step
+            q = torch.stack([st.q[l][:, 0] for l in range(self.n_layers)])          # [L, B, Hq, D]
+            lse = torch.stack([st.lse[l][:, 0] for l in range(self.n_layers)])      # [L, B, Hq]
+            lim = [self.kv.seq_used[r] for r in self.reqs]
+            self._act.append((q, lse, lim, flags))
+            self.n_action = [c + int(f) for c, f in zip(self.n_action, flags)]
+        return logits
+
+    def _score_round(self) -> None:
+        """One cal_attn launch over every layer for the round's action tokens, packed per
+        sequence in decode order, each with its causal limit."""
+        nmax = max(self.n_action)
+        if nmax == 0:
+            return
+        b, dev = len(self.reqs), self.kv.kv.device
+        steps = [[i for i, a in enumerate(self._act) if a[3][j]] for j in range(b)]
+        gidx = torch.tensor([s + [s[-1] if s else 0] * (nmax - len(s)) for s in steps], device=dev)  # [B, N]
+        qs = torch.stack([a[0] for a in self._act])         # [S, L, B, Hq, D]
+        ls = torch.stack([a[1] for a in self._act])         # [S, L, B, Hq]
+        rows = torch.arange(b, device=dev)[:, None]
+        q = qs[gidx, :, rows].permute(2, 0, 1, 3, 4).contiguous()     # [L, B, N, Hq, D]
+        lse = ls[gidx, :, rows].permute(2, 0, 1, 3).contiguous()      # [L, B, N, Hq]
+        lim = np.zeros((b, nmax), dtype=np.int32)
+        for j, s in enumerate(steps):
+            lim[j, : len(s)] = [self._act[i][2][j] for i in s]
+        kv_len = _hip.upload_i32(lim, dev).view(b, nmax)
+        n_valid = _hip.upload_i32(self.n_action, dev)
+        self.kv.cal_attn(self.reqs, q, lse, self.lrfu.scores, self.lrfu.n_seen, layer=None,
+                         n_valid=n_valid, kv_len=kv_len)
+
+    def end_round(self, budget) -> list:
+        """Algorithm 1 at the end of a round: score, update the keep scores, compress.
+        budget: an int or one per sequence (excluding the protected prefix)."""
+        self._score_round()
+        perms = self.lrfu.evict(budget, protected=self.protected, n_action=self.n_action)
+        self._act = []
+        return perms

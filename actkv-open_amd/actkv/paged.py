@@ -234,30 +234,30 @@ class PagedKVCache:
         for r, s0, c in zip(reqs, starts, counts):
             self.seq_used[r] = s0 + c
 
-    def _append_src(self, x: torch.Tensor, total: int) -> torch.Tensor:
+    def _append_src(self, x: torch.Tensor, total: int, n_layers: int | None = None) -> torch.Tensor:
         """A source operand as [L, total, Hkv, D] on the cache's device with a unit last stride
         (broadcasting like the reference's indexed assignment); dtypes the kernel does not read
         are converted to the cache dtype first, which is the reference's own conversion."""
         x = x.to(device=self.kv.device)
         if x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
             x = x.to(self.kv.dtype)
-        x = torch.broadcast_to(x, (self.n_layers, total, self.n_kv_heads, self.head_dim))
+        n_l = self.n_layers if n_layers is None else n_layers
+        x = torch.broadcast_to(x, (n_l, total, self.n_kv_heads, self.head_dim))
         return x if x.stride(-1) == 1 else x.contiguous()
 
     def _append_device(self, reqs, starts, counts, k, v) -> None:
         total = sum(counts)
         if total == 0:
             return
-        if k.dtype != v.dtype:
-            # one source dtype per launch: convert both as the reference does, straight to the
-            # cache dtype (through the other source dtype could round twice)
-            k, v = k.to(self.kv.dtype), v.to(self.kv.dtype)
-        k = self._append_src(k, total)
-        v = self._append_src(v, total)
+        self._append_launch(self._append_plan(reqs, starts, counts), k, v)
+
+    def _append_plan(self, reqs, starts, counts):
+        """The device side of an append whose blocks are allocated: one upload of the source
+        offsets (int64, as lo/hi int32 pairs), start positions, counts and block tables.
+        Reused by every launch of the same step (a model writes one layer at a time)."""
         r_n = len(reqs)
         tabs = [_as_i32(self.tables[r]) for r in reqs]
         mb = max(max(t.size for t in tabs), 1)
-        # one upload: src_off (int64, as lo/hi int32 pairs), starts, counts, block tables
         host = np.zeros(4 * r_n + r_n * mb, dtype=np.int32)
         off = np.concatenate([[0], np.cumsum(counts[:-1])]).astype(np.int64)
         host[: 2 * r_n] = off.view(np.int32)
@@ -266,8 +266,21 @@ class PagedKVCache:
         grid = host[4 * r_n:].reshape(r_n, mb)
         for i, t in enumerate(tabs):
             grid[i, : t.size] = t
-        dev = self._upload(host)
-        kv = self.kv
+        return self._upload(host), r_n, mb, int(sum(counts))
+
+    def _append_launch(self, plan, k, v, layer=None) -> None:
+        """k, v [L, total, Hkv, D] (or [1, total, Hkv, D] for one `layer`) -> the cache."""
+        dev, r_n, mb, total = plan
+        if total == 0:
+            return
+        if k.dtype != v.dtype:
+            # one source dtype per launch: convert both as the reference does, straight to the
+            # cache dtype (through the other source dtype could round twice)
+            k, v = k.to(self.kv.dtype), v.to(self.kv.dtype)
+        n_l = self.n_layers if layer is None else 1
+        k = self._append_src(k, total, n_l)
+        v = self._append_src(v, total, n_l)
+        kv = self.kv if layer is None else self.kv[layer:layer + 1]
         if kv.stride(-1) != 1:
             raise RuntimeError("PagedKVCache.kv must have a unit last stride")
         rc = _hip.lib().actkv_append(
@@ -275,7 +288,7 @@ class PagedKVCache:
             kv.stride(3), kv.stride(4), self.num_blocks,
             k.data_ptr(), v.data_ptr(), _hip.dtype_code(k.dtype),
             k.stride(0), k.stride(1), k.stride(2), v.stride(0), v.stride(1), v.stride(2),
-            self.n_layers, self.n_kv_heads, self.head_dim, r_n,
+            n_l, self.n_kv_heads, self.head_dim, r_n,
             dev[2 * r_n:].data_ptr(), dev[3 * r_n:].data_ptr(), dev.data_ptr(), total,
             dev[4 * r_n:].data_ptr(), mb, mb, self.block_size, None, _hip.stream(kv.device))
         _hip.check(rc, "actkv_append")

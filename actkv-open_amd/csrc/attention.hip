@@ -153,7 +153,18 @@ attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
   // chunk q%16 (dims 8(q%16) .. +7)
   const T *kplane = (const T *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh;
   const T *vplane = kplane + a.kv_sv;
-  const int nst = (S + ST - 1) / ST;
+  // stages up to the furthest token any row of the workgroup sees: a causal prefill's
+  // early row groups stop where their queries do instead of masking the rest
+  int s_end = S;
+  if constexpr (CAUSAL) {
+    __shared__ int wg_lim;
+    if (tid == 0) wg_lim = 0;
+    __syncthreads();
+    if (valid && lim > 0) atomicMax(&wg_lim, lim);
+    __syncthreads();
+    s_end = wg_lim;
+  }
+  const int nst = (s_end + ST - 1) / ST;
   int phys[PPT];  // physical block of each of this thread's token groups of the next stage
   auto stage_phys = [&](int (&ph)[PPT], int g0) {
 #pragma unroll

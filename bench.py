@@ -78,6 +78,16 @@ def parse(argv=None):
     ap.add_argument("--attn", action="store_true",
                     help="measure the paged attention kernel (the lse producer) instead: the 36-layer "
                          "32k-token cache with 128 queries, plain and causal, and a batch-8 decode step")
+    ap.add_argument("--serve", action="store_true",
+                    help="serve a Qwen3-8B-shaped model (random bf16 weights) on the paged cache through "
+                         "the transformers backend: batch prefill, decode rounds with action tokens, ActKV "
+                         "compression at each round's end; prints its own JSON line")
+    ap.add_argument("--serve-batch", type=int, default=4)
+    ap.add_argument("--serve-prompt", type=int, default=8192)
+    ap.add_argument("--serve-rounds", type=int, default=4)
+    ap.add_argument("--serve-steps", type=int, default=48, help="decode steps per round")
+    ap.add_argument("--serve-action", type=int, default=24, help="action tokens at the end of each round")
+    ap.add_argument("--serve-budget", type=int, default=4096)
     return ap.parse_args(argv)
 
 
@@ -518,6 +528,97 @@ def run_ora(args, dev):
     return 0
 
 
+def run_serve(args, dev):
+    """Serving on the paged cache: a Qwen3-8B-shaped transformers model (36 layers, hidden 4096,
+    Hq 32 / Hkv 8, head_dim 128, MLP 12288, vocab 151936; random bf16 weights, no checkpoint)
+    runs through PagedSession: the attention of every layer is the paged HIP kernel, new K/V
+    go in with the append kernel.  A batch of sequences prefills a prompt (the first 256 tokens
+    protected), then runs rounds of greedy decode steps whose last tokens are the action region;
+    each round ends with ActKV's compression (scoring of the action tokens from their lse, LRFU
+    update, keep, compaction) to the budget.  Reports prefill and decode throughput and the
+    end-of-round latency."""
+    import torch
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    from actkv.hf import PagedSession
+
+    B, P = args.serve_batch, args.serve_prompt
+    rounds, steps, n_act, budget = args.serve_rounds, args.serve_steps, args.serve_action, args.serve_budget
+    cfg = Qwen3Config(vocab_size=151936, hidden_size=4096, intermediate_size=12288, num_hidden_layers=36,
+                      num_attention_heads=32, num_key_value_heads=8, head_dim=128, max_position_embeddings=65536,
+                      rope_theta=1000000.0, tie_word_embeddings=False)
+    log(f"building a random-weight Qwen3-8B-shaped model (bf16)")
+    torch.manual_seed(args.seed)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            model = Qwen3ForCausalLM(cfg).eval()
+    finally:
+        torch.set_default_dtype(prev)
+    n_params = sum(p.numel() for p in model.parameters())
+    max_tokens = P + rounds * steps + 64
+    sess = PagedSession(model, B, max_tokens=max_tokens, block_size=args.block_size)
+    g = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    prompt = torch.randint(0, cfg.vocab_size, (B, P), generator=g, device=dev)
+    gc.collect()
+    gc.freeze()
+    torch.cuda.synchronize()
+    log(f"prefill {B} x {P} tokens ({n_params / 1e9:.2f}B parameters)")
+    t0 = time.perf_counter()
+    sess.prefill(prompt[:, :256], protected=True)
+    logits = sess.prefill(prompt[:, 256:])
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    tok = logits.argmax(-1)
+    per_round = []
+    for rnd in range(rounds):
+        sess.begin_round()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for j in range(steps):
+            logits = sess.decode(tok, in_action=j >= steps - n_act)
+            tok = logits.argmax(-1)
+        torch.cuda.synchronize()
+        dec_s = time.perf_counter() - t0
+        before = [sess.kv.seq_used[r] for r in sess.reqs]
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        ev[0].record()
+        h0 = time.perf_counter()
+        sess.end_round(budget)
+        h1 = time.perf_counter()
+        ev[1].record()
+        torch.cuda.synchronize()
+        per_round.append({"round": rnd, "tokens_before": before[0], "tokens_after": sess.kv.seq_used[0],
+                          "decode_ms_per_step": dec_s / steps * 1e3,
+                          "decode_tokens_per_s": B * steps / dec_s,
+                          "end_round_us": ev[0].elapsed_time(ev[1]) * 1e3, "end_round_host_us": (h1 - h0) * 1e6})
+        pr = per_round[-1]
+        log(f"round {rnd}: {pr['tokens_before']} -> {pr['tokens_after']} tokens per sequence, decode "
+            f"{pr['decode_ms_per_step']:.1f} ms/step, end of round {pr['end_round_us']:.0f} us")
+    dec = [p["decode_tokens_per_s"] for p in per_round]
+    result = {
+        "metric": "serving on the paged cache: decode tokens/s with ActKV compression each round",
+        "value": round(statistics.median(dec), 1), "unit": "tokens/s", "n_gpus": 1,
+        "higher_is_better": True, "dtype": "bf16", "data": "synthetic (random weights, random prompt ids)",
+        "config": {"workload": f"Qwen3-8B-shaped transformers model ({n_params / 1e9:.2f}B parameters, random "
+                               f"bf16 weights), batch {B}, prompt {P} (256 protected), {rounds} rounds x {steps} "
+                               f"greedy decode steps, last {n_act} of each round scored as the action region, "
+                               f"budget {budget}, LRFU decay 0.5 top-p 0.9, block {args.block_size}",
+                   "parallelism": "single-gpu"},
+        "prefill_tokens_per_s": round(B * P / prefill_s, 1),
+        "decode_ms_per_step_median": round(statistics.median(p["decode_ms_per_step"] for p in per_round), 2),
+        "end_round_us_median": round(statistics.median(p["end_round_us"] for p in per_round), 1),
+        "per_round": [{k: (round(v, 1) if isinstance(v, float) else v) for k, v in p.items()} for p in per_round],
+        "gpu": torch.cuda.get_device_name(dev),
+    }
+    line = json.dumps(result)
+    print(line)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(line + "\n")
+    return 0
+
+
 def main(argv=None):
     args = parse(argv)
     if args.gpus != 1:
@@ -536,6 +637,8 @@ def main(argv=None):
         return run_ora(args, dev)
     if args.attn:
         return run_attn(args, dev)
+    if args.serve:
+        return run_serve(args, dev)
 
     log(f"building the {args.layers}-layer workload")
     w = Workload(args, args.layers, dev)

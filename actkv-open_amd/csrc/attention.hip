@@ -10,7 +10,8 @@
 // out and lse are float32.  A row that sees no token gets lse = -inf, out = 0
 // (torch's logsumexp and softmax-einsum over an empty set).
 //
-// MFMA path (bf16/fp16, head_dim 128, GQA group 1/2/4): FlashAttention-style,
+// MFMA path (bf16/fp16, head_dim 128, GQA group 1/2/4, more than one 32-row tile of
+// query rows per pair): FlashAttention-style,
 // one workgroup per (layer, request, KV head, group of NW row tiles), NW waves,
 // each owning one 32-row tile of the pair's query rows (n, g) and streaming all
 // of the request's tokens.  The transposed products keep every per-query
@@ -25,6 +26,11 @@
 // g+1 into registers while stage g is multiplied, then writes K rows (padded to
 // 272 bytes: conflict-free B-operand reads) and V transposed (dim-major rows,
 // padded: conflict-free 8-byte reads), one barrier per stage.
+//
+// Decode path (the same dtypes and shapes when a pair's query rows fit one 32-row
+// tile, N*G <= 32): four waves per (pair, token chunk), each streaming its own
+// slices through a private LDS region without workgroup barriers; V comes back
+// transposed from LDS (ds_read_b64_tr_b16).  Described at attn_decode_kernel.
 //
 // Generic path (any other dtype / head_dim / group): one workgroup per query row,
 // float32 dot products, an online max/sum pass for lse and a second pass that
@@ -363,6 +369,270 @@ attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
   }
 }
 
+// ------------------------------------------------------------------ decode path
+// A pair whose query rows fit one 32-row tile (N*G <= 32: decode steps and short
+// action regions) gets a workgroup of DW waves per token chunk, each wave streaming
+// the chunk's 32-token slices w, w + DW, ... on its own.  The next slice's K and V
+// rows are loaded into registers (coalesced 16-byte loads, four token rows per
+// instruction) while the current slice is multiplied out of the wave's private LDS
+// region, so the loop has no workgroup barrier.  K rows sit in LDS with their 16-byte
+// chunks XOR-swizzled by token (conflict-free A-operand reads); V rows are stored the
+// same way and read back with ds_read_b64_tr_b16, which hands each lane four
+// consecutive tokens of one dim: the V^T operand with no register transpose.  The
+// waves' (max, sum, O) merge through LDS at the end.
+constexpr int DW = 4;                         // waves per decode workgroup
+constexpr int DREG = 2 * 32 * 256;            // LDS bytes per wave: K rows, then V rows
+
+// 16-byte chunk slot of chunk c of token t: distinct over 16 consecutive tokens (K
+// reads), and over the 8 chunks four consecutive tokens expose to a transposed V read
+__device__ __forceinline__ int dswz(int t) { return 2 * (t & 7) + ((t >> 3) & 1); }
+
+typedef short dv4s __attribute__((ext_vector_type(4)));
+
+template <typename T, typename V8, int G, bool CAUSAL>
+__global__ void __launch_bounds__(DW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
+  __shared__ __attribute__((aligned(16))) unsigned char reg_lds[DW][DREG];
+  __shared__ float mrg_ml[DW][32][2];
+  __shared__ int wg_lim;
+  const int p = blockIdx.x / a.nchunk, chunk = blockIdx.x % a.nchunk;
+  if (p >= pairs) return;
+  const int h = p % a.Hkv;
+  const int r = (p / a.Hkv) % a.R;
+  const int l = p / (a.Hkv * a.R);
+  const int nq = attn_nq(a, r);
+  if (nq * G <= 0) return;
+  const int S_all = attn_seq_len(a, r);
+  if (a.nchunk > 1 && chunk * a.tpc >= S_all) return;
+  const int c_begin = min(chunk * a.tpc, S_all);
+  const int S = min(S_all - c_begin, a.tpc);
+  const int BS = a.BS;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int lcol = lane & 31, lh = lane >> 5;
+  const int row = lcol;
+  const int n = row / G, g = row % G;
+  const bool valid = n < nq;
+  const int lim = valid ? min(max(attn_lim(a, r, n, S_all) - c_begin, 0), S) : 0;
+  const int lim_m = valid ? lim : 0x7fffffff;
+  int s_end = S;
+  if constexpr (CAUSAL) {
+    if (tid == 0) wg_lim = 0;
+    __syncthreads();
+    if (valid && lim > 0) atomicMax(&wg_lim, lim);
+    __syncthreads();
+    s_end = wg_lim;
+  }
+  const int nsl = (s_end + 31) / 32;  // slices of the chunk anyone needs
+
+  V8 qf[8];
+  {
+    const T *qp = (const T *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr +
+                  (int64_t)(valid ? n : 0) * a.q_sn + (int64_t)(h * G + g) * a.q_sh + lh * 8;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = *(const V8 *)(qp + ks * 16);
+    if (!valid) {
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) qf[ks] = V8{};
+    }
+  }
+  const T *kplane = (const T *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh;
+  const T *vplane = kplane + a.kv_sv;
+  unsigned char *kl = reg_lds[wave];
+  unsigned char *vl = kl + 32 * 256;
+
+  // block-table entry of token group i (tokens 4i..4i+3) of slice s: lane i < 8 holds it
+  auto slice_phys = [&](int s) {
+    const int t = s * 32 + 4 * (lane & 7);
+    return (s < nsl && t < S) ? attn_phys(a, r, (c_begin + t) >> bs_shift) : -1;
+  };
+  // lane: token rows 4i + lane/16 (i = 0..7), 16-byte chunk lane%16, of K and V
+  uint4 kr[8], vr[8];
+  auto load_slice = [&](int s, int ph) {
+    const int c = lane & 15;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int pb = __builtin_amdgcn_readlane(ph, i);
+      const int t = s * 32 + 4 * i + (lane >> 4);
+      const bool ok = pb >= 0 && t < S;
+      const int64_t off = ok ? (int64_t)pb * a.kv_sb + (int64_t)((c_begin + t) & (BS - 1)) * a.kv_ss + c * 8 : 0;
+      kr[i] = *(const uint4 *)(kplane + off);
+      vr[i] = *(const uint4 *)(vplane + off);
+      if (!ok) { kr[i] = make_uint4(0, 0, 0, 0); vr[i] = make_uint4(0, 0, 0, 0); }
+    }
+  };
+  auto store_slice = [&]() {
+    const int c = lane & 15;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int t = 4 * i + (lane >> 4);
+      const int o = t * 256 + ((c ^ dswz(t)) << 4);
+      *(uint4 *)(kl + o) = kr[i];
+      *(uint4 *)(vl + o) = vr[i];
+    }
+  };
+
+  const float c2 = a.scale * 1.4426950408889634f;
+  float m2 = -INFINITY, lsum = 0.f;
+  f32x16 oacc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) oacc[dt][e] = 0.f;
+
+  auto compute = [&](int s) {
+    // S^T = K . Q^T for the slice's 32 tokens (A: token lcol, dims 16ks + 8lh .. +7)
+    f32x16 st = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const int c = 2 * ks + lh;
+      const V8 kf = *(const V8 *)(kl + lcol * 256 + ((c ^ dswz(lcol)) << 4));
+      if constexpr (__is_same(T, __bf16))
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], st, 0, 0, 0);
+      else
+        st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], st, 0, 0, 0);
+    }
+    const int t0 = s * 32;
+    if (__builtin_amdgcn_ballot_w64(lim_m < t0 + 32) != 0ull) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int t = t0 + 8 * (e >> 2) + 4 * lh + (e & 3);
+        st[e] = t < lim_m ? st[e] : -INFINITY;
+      }
+    }
+    float mx = st[0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e) mx = fmaxf(mx, st[e]);
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
+    const float m_new = fmaxf(m2, mx * c2);
+    const float msafe = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m2 - msafe);
+    float ps = 0.f;
+    V8 pb[2];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float pe = __builtin_amdgcn_exp2f(fmaf(st[e], c2, -msafe));
+      ps += pe;
+      pb[e >> 3][e & 7] = (T)pe;
+    }
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ps), __float_as_uint(ps), false, false);
+      ps = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    lsum = lsum * alpha + ps;
+    m2 = m_new;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0ull) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[dt][e] *= alpha;
+    }
+    // O^T += V^T . P^T.  A = V^T[dim][tau(kb, lh, j)]: two transposed reads give tokens
+    // 16kb + 4lh + 0..3 and + 8..11 of dim 32dt + 16((lane/16)&1) + lane%16; lane
+    // 4j' + q' of each 16-lane group points at token j', dims 4q' .. 4q'+3
+    const int jj = (lane & 15) >> 2, qq = lane & 3;
+    const int dgrp = 16 * ((lane >> 4) & 1) + 4 * qq;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const int d = 32 * dt + dgrp;
+        const int cc = d >> 3, half = (d >> 2) & 1;
+        const int t_lo = 16 * kb + 4 * lh + jj, t_hi = t_lo + 8;
+        const dv4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (dv4s __attribute__((address_space(3))) *)(vl + t_lo * 256 + ((cc ^ dswz(t_lo)) << 4) + half * 8));
+        const dv4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (dv4s __attribute__((address_space(3))) *)(vl + t_hi * 256 + ((cc ^ dswz(t_hi)) << 4) + half * 8));
+        // whole-register casts: the 64-bit results become the operand's two halves
+        // (inserting the 16-bit elements one by one compiled to a wrong operand)
+        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+        const V8 va = __builtin_bit_cast(V8, make_uint4(l2.x, l2.y, h2.x, h2.y));
+        if constexpr (__is_same(T, __bf16))
+          oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kb], oacc[dt], 0, 0, 0);
+        else
+          oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[kb], oacc[dt], 0, 0, 0);
+      }
+    }
+  };
+
+  // ---- the wave's slices: wave, wave + DW, ...; table entries two slices ahead
+  int s = wave;
+  int ph_next = slice_phys(s + DW);
+  if (s < nsl) load_slice(s, slice_phys(s));
+  for (; s < nsl; s += DW) {
+    store_slice();
+    if (s + DW < nsl) load_slice(s + DW, ph_next);
+    ph_next = slice_phys(s + 2 * DW);
+    compute(s);
+  }
+
+  // ---- merge the waves' (max, sum, O) through LDS
+  __syncthreads();
+  {
+    float *om = (float *)reg_lds[wave];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) om[(dt * 16 + e) * 64 + lane] = oacc[dt][e];
+    if (lh == 0) { mrg_ml[wave][lcol][0] = m2; mrg_ml[wave][lcol][1] = lsum; }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < DW; ++w) M = fmaxf(M, mrg_ml[w][lcol][0]);
+  const float Ms = M == -INFINITY ? 0.f : M;
+  float Lsum = 0.f, wgt[DW];
+#pragma unroll
+  for (int w = 0; w < DW; ++w) {
+    wgt[w] = __builtin_amdgcn_exp2f(mrg_ml[w][lcol][0] - Ms);
+    Lsum += wgt[w] * mrg_ml[w][lcol][1];
+  }
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      float o = 0.f;
+#pragma unroll
+      for (int w = 0; w < DW; ++w) o += wgt[w] * ((const float *)reg_lds[w])[(dt * 16 + e) * 64 + lane];
+      oacc[dt][e] = o;
+    }
+  if (!valid) return;
+  if (a.nchunk > 1) {
+    const int64_t pr = ((int64_t)p * a.rows_pad + row) * a.nchunk + chunk;
+    float *wo = a.ws_o + pr * 128;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f32x4 v;
+        v[0] = oacc[dt][4 * i]; v[1] = oacc[dt][4 * i + 1]; v[2] = oacc[dt][4 * i + 2]; v[3] = oacc[dt][4 * i + 3];
+        *(f32x4 *)(wo + 32 * dt + 8 * i + 4 * lh) = v;
+      }
+    if (lh == 0) { a.ws_ml[pr * 2] = M; a.ws_ml[pr * 2 + 1] = Lsum; }
+    return;
+  }
+  const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
+  float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * G + g) * a.o_sh;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d0 = 32 * dt + 8 * i + 4 * lh;
+      f32x4 v;
+      v[0] = oacc[dt][4 * i] * inv; v[1] = oacc[dt][4 * i + 1] * inv;
+      v[2] = oacc[dt][4 * i + 2] * inv; v[3] = oacc[dt][4 * i + 3] * inv;
+      *(f32x4 *)(op + d0) = v;
+    }
+  if (lh == 0)
+    a.lse[(int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * G + g] =
+        Lsum > 0.f ? (M + __log2f(Lsum)) * 0.6931471805599453f : -INFINITY;
+}
+
 // ------------------------------------------------------------------ split combine
 // grid ceil(pairs*rows_pad/4), 256 threads: one wave per (pair, row), two dims per lane.
 //   M = max_c m_c, w_c = 2^(m_c - M), out = sum_c w_c O_c / sum_c w_c l_c,
@@ -493,6 +763,21 @@ struct AttnSplit { int nchunk, tpc, rows_pad, ngroups; };
 static AttnSplit attn_split(int pairs, int N, int G, int span) {
   AttnSplit sp;
   const int rtiles = (N * G + 31) / 32;
+  if (rtiles == 1) {
+    // decode kernel: DW waves per (pair, chunk), two workgroups per CU; about two rounds
+    // of them, each wave taking at least two 32-token slices of its chunk
+    sp.ngroups = 1;
+    sp.rows_pad = 32;
+    const int unit = DW * 32;
+    const int64_t want = 2LL * 2 * 256;
+    const int nchunk = (int)std::min<int64_t>(std::max<int64_t>(1, (want + pairs - 1) / pairs),
+                                              std::max(1, span / (2 * unit)));
+    const int tpc = ((span + nchunk - 1) / nchunk + unit - 1) / unit * unit;
+    sp.nchunk = (span + tpc - 1) / tpc;
+    sp.tpc = tpc;
+    if (sp.nchunk <= 1) { sp.nchunk = 1; sp.tpc = std::max(span, 1); }
+    return sp;
+  }
   const int nw = attn_waves(rtiles);
   const int st = nw >= 4 ? 16 * nw : 32;
   sp.ngroups = (rtiles + nw - 1) / nw;
@@ -528,6 +813,13 @@ static int launch_attn_mfma(AttnArgs a, int bs_shift, void *ws, size_t ws_bytes,
   a.nchunk = sp.nchunk; a.tpc = sp.tpc; a.rows_pad = sp.rows_pad;
   a.ws_o = sp.nchunk > 1 ? (float *)ws : nullptr;
   a.ws_ml = sp.nchunk > 1 ? (float *)((char *)ws + (size_t)pairs * sp.rows_pad * sp.nchunk * 128 * sizeof(float)) : nullptr;
+  if (rtiles == 1) {
+    const int grid = pairs * sp.nchunk;
+    if (causal)
+      hipLaunchKernelGGL((attn_decode_kernel<T, V8, G, true>), dim3(grid), dim3(DW * 64), 0, st, a, pairs, bs_shift);
+    else
+      hipLaunchKernelGGL((attn_decode_kernel<T, V8, G, false>), dim3(grid), dim3(DW * 64), 0, st, a, pairs, bs_shift);
+  } else {
 #define ACTKV_ATTN(NWV)                                                                            \
   do {                                                                                             \
     const int grid = ((pairs + 7) / 8) * 8 * sp.ngroups * sp.nchunk;                               \
@@ -539,12 +831,12 @@ static int launch_attn_mfma(AttnArgs a, int bs_shift, void *ws, size_t ws_bytes,
                          st, a, pairs, sp.ngroups, bs_shift);                                      \
   } while (0)
   switch (attn_waves(rtiles)) {
-    case 1: ACTKV_ATTN(1); break;
     case 2: ACTKV_ATTN(2); break;
     case 4: ACTKV_ATTN(4); break;
     default: ACTKV_ATTN(8); break;
   }
 #undef ACTKV_ATTN
+  }
   int rc = actkv_check_launch();
   if (rc || sp.nchunk <= 1) return rc;
   const int64_t waves = (int64_t)pairs * sp.rows_pad;

@@ -52,6 +52,9 @@ def _atol(dtype):
     ([900], 16, 8, 40, torch.float16, False),            # GQA 2, 80 rows (3 tiles)
     ([1100, 64], 8, 8, 100, torch.bfloat16, True),       # GQA 1, 100 rows, a short request
     ([640], 32, 8, 200, torch.bfloat16, True),           # 800 rows: four groups of 8 tiles
+    ([3000, 47], 32, 8, 8, torch.bfloat16, True),        # 32 rows: the one-tile decode kernel, causal
+    ([2100], 16, 8, 5, torch.float16, True),             # GQA 2, 10 rows, fp16, causal
+    ([5000, 1], 8, 8, 3, torch.bfloat16, False),         # GQA 1, 3 rows, a one-token request
 ])
 def test_matrix_core_path_matches_the_oracle(lens, hq, hkv, n_q, dtype, causal):
     cache = _cache(lens, hkv=hkv, dtype=dtype, seed=len(lens) * 100 + n_q)
@@ -153,16 +156,18 @@ def test_device_lse_drives_action_scoring():
     torch.testing.assert_close(out.cpu(), want, rtol=1e-3, atol=1e-6)
 
 
-def test_token_split_and_single_pass_agree(monkeypatch):
+@pytest.mark.parametrize("n_q", [16, 8, 1])
+def test_token_split_and_single_pass_agree(monkeypatch, n_q):
     """With a workspace, long sequences are split into token chunks and merged by the combine
-    launch; without one, one workgroup attends the whole sequence. Both match the oracle."""
+    launch; without one, one workgroup attends the whole sequence. Both match the oracle.
+    16 queries take the multi-tile kernel, 8 and 1 the one-tile decode kernel."""
     from actkv import _hip
     cache = _cache([4000, 2500], seed=13)
     g = torch.Generator().manual_seed(14)
-    q = torch.randn(2, 16, 32, 128, generator=g).to(torch.bfloat16)
-    kv_len = torch.stack([torch.randint(1, S + 1, (16,), generator=g) for S in (4000, 2500)]).to(torch.int32)
+    q = torch.randn(2, n_q, 32, 128, generator=g).to(torch.bfloat16)
+    kv_len = torch.stack([torch.randint(1, S + 1, (n_q,), generator=g) for S in (4000, 2500)]).to(torch.int32)
     lib = _hip.lib()
-    assert lib.actkv_paged_attention_workspace_size(1, 2, 16, 32, 8, 128, len(cache.tables[0]), 16) > 0
+    assert lib.actkv_paged_attention_workspace_size(1, 2, n_q, 32, 8, 128, len(cache.tables[0]), 16) > 0
     split_out, split_lse = cache.decode_attention([0, 1], q.cuda(), kv_len=kv_len.cuda())
     monkeypatch.setattr(lib, "actkv_paged_attention_workspace_size", lambda *a: 0)
     one_out, one_lse = cache.decode_attention([0, 1], q.cuda(), kv_len=kv_len.cuda())

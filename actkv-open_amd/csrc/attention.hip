@@ -22,10 +22,9 @@
 //   O^T += V^T . P^T (A = V^T from LDS, B = P^T: the lane's own 16 probabilities,
 //   taken in the token order tau(kb, lh, j) = 16kb + 8(j/4) + 4lh + j%4 that
 //   matches the S^T register layout, so no shuffle is needed).
-// K and V move through a two-slot LDS stage buffer: the workgroup loads stage
-// g+1 into registers while stage g is multiplied, then writes K rows (padded to
-// 272 bytes: conflict-free B-operand reads) and V transposed (dim-major rows,
-// padded: conflict-free 8-byte reads), one barrier per stage.
+// K and V stages go straight from HBM into an LDS ring (buffer loads with the LDS
+// bit, several stages ahead), rows XOR-swizzled; V is read back transposed
+// (ds_read_b64_tr_b16).  Described at attn_ring_kernel.
 //
 // Decode path (the same dtypes and shapes when a pair's query rows fit one 32-row
 // tile, N*G <= 32): four waves per (pair, token chunk), each streaming its own
@@ -88,287 +87,6 @@ __device__ __forceinline__ int attn_phys(const AttnArgs &a, int r, int b) {
 }
 
 // ------------------------------------------------------------------ MFMA path
-template <int NW> struct AttnShape {
-  static constexpr int ST = NW >= 4 ? 16 * NW : 32;  // tokens per stage
-  static constexpr int GS = ST / 32;                  // 32-token slices per stage
-  // a thread stages (4-token group, 16-byte chunk) pairs: 4 K rows and 4 V rows of one chunk
-  static constexpr int PPT = (ST / 4) * 16 / (NW * 64);
-  static constexpr int KROW = 272;                    // padded K row (bytes)
-  // V stage: [token group][dim][4 tokens], 8 bytes per (group, dim)
-  static constexpr int KSTAGE = ST * KROW, VSTAGE = ST * 128 * 2;
-  static_assert(PPT >= 1 && (ST / 4) * 16 % (NW * 64) == 0, "whole pairs per thread");
-};
-
-template <typename T, typename V8, int G, int NW, bool CAUSAL>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 2 ? 2 : 1, NW >= 2 ? 2 : 1)))
-attn_mfma_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
-  // work item = (pair, row group, token chunk)
-  using SH = AttnShape<NW>;
-  constexpr int ST = SH::ST, GS = SH::GS, PPT = SH::PPT, KROW = SH::KROW;
-  constexpr int KS = 8;
-  __shared__ __attribute__((aligned(16))) unsigned char kbuf[2][SH::KSTAGE];
-  __shared__ __attribute__((aligned(16))) unsigned char vbuf[2][SH::VSTAGE];
-
-  // XCD-aware mapping: the row groups of one (layer, request, head) pair share an
-  // XCD, so the second group's K/V reads hit that XCD's L2.
-  const int bid = blockIdx.x;
-  const int xcd = bid & 7, jj = bid >> 3;
-  const int per_pair = ngroups * a.nchunk;
-  const int p = (jj / per_pair) * 8 + xcd;
-  const int grp = (jj % per_pair) / a.nchunk, chunk = jj % a.nchunk;
-  if (p >= pairs) return;
-  const int h = p % a.Hkv;
-  const int r = (p / a.Hkv) % a.R;
-  const int l = p / (a.Hkv * a.R);
-  const int nq = attn_nq(a, r);
-  if (grp * NW * 32 >= nq * G) return;
-  const int S_all = attn_seq_len(a, r);
-  // chunks past the sequence hold nothing the combine step reads
-  if (a.nchunk > 1 && chunk * a.tpc >= S_all) return;
-  const int c_begin = min(chunk * a.tpc, S_all);
-  // this chunk's tokens are [c_begin, c_begin + S); token indices below are relative
-  const int S = min(S_all - c_begin, a.tpc);
-  const int BS = a.BS;
-
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int lcol = lane & 31, lh = lane >> 5;
-
-  // ---- this lane's query row: B operands of S^T = K . Q^T, causal limit
-  const int row = (grp * NW + wave) * 32 + lcol;
-  const int n = row / G, g = row % G;
-  const bool valid = n < nq;
-  // tokens of this chunk the row sees: [0, lim) relative to the chunk
-  const int lim = valid ? min(max(attn_lim(a, r, n, S_all) - c_begin, 0), S) : 0;
-  // the masking limit: padding rows (never written) see everything, so they never force it
-  const int lim_m = valid ? lim : 0x7fffffff;
-  V8 qf[KS];
-  {
-    const T *qp = (const T *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr +
-                  (int64_t)(valid ? n : 0) * a.q_sn + (int64_t)(h * G + g) * a.q_sh + lh * 8;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const V8 *)(qp + ks * 16);
-    if (!valid) {
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qf[ks] = V8{};
-    }
-  }
-
-  // ---- stage loads: pair q = tid + k*NW*64 of a stage is token group q/16 (tokens
-  // 4(q/16) .. +3, one block: groups never straddle a block of >= 16 tokens) and 16-byte
-  // chunk q%16 (dims 8(q%16) .. +7)
-  const T *kplane = (const T *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh;
-  const T *vplane = kplane + a.kv_sv;
-  // stages up to the furthest token any row of the workgroup sees: a causal prefill's
-  // early row groups stop where their queries do instead of masking the rest
-  int s_end = S;
-  if constexpr (CAUSAL) {
-    __shared__ int wg_lim;
-    if (tid == 0) wg_lim = 0;
-    __syncthreads();
-    if (valid && lim > 0) atomicMax(&wg_lim, lim);
-    __syncthreads();
-    s_end = wg_lim;
-  }
-  const int nst = (s_end + ST - 1) / ST;
-  int phys[PPT];  // physical block of each of this thread's token groups of the next stage
-  auto stage_phys = [&](int (&ph)[PPT], int g0) {
-#pragma unroll
-    for (int k = 0; k < PPT; ++k) {
-      const int t = g0 * ST + 4 * ((tid + k * NW * 64) >> 4);
-      ph[k] = t < S ? attn_phys(a, r, (c_begin + t) >> bs_shift) : -1;
-    }
-  };
-  uint4 kreg[PPT][4], vreg[PPT][4];
-  auto load_stage = [&](const int (&ph)[PPT], int g0) {
-#pragma unroll
-    for (int k = 0; k < PPT; ++k) {
-      const int q = tid + k * NW * 64;
-      const int t4 = g0 * ST + 4 * (q >> 4), c = q & 15;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = t4 + i;
-        const bool ok = ph[k] >= 0 && t < S;  // a token of the chunk in a valid block
-        const int64_t off = ok ? (int64_t)ph[k] * a.kv_sb + (int64_t)((c_begin + t) & (BS - 1)) * a.kv_ss + c * 8 : 0;
-        kreg[k][i] = *(const uint4 *)(kplane + off);
-        vreg[k][i] = *(const uint4 *)(vplane + off);
-        if (!ok) { kreg[k][i] = make_uint4(0, 0, 0, 0); vreg[k][i] = make_uint4(0, 0, 0, 0); }
-      }
-    }
-  };
-  // K rows as they are (padded rows); V as [group][dim][4 tokens]: the 4x8 block of 16-bit
-  // values is transposed in registers and written as four 16-byte stores
-  auto store_stage = [&](int slot) {
-#pragma unroll
-    for (int k = 0; k < PPT; ++k) {
-      const int q = tid + k * NW * 64;
-      const int tg = q >> 4, c = q & 15;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) *(uint4 *)(&kbuf[slot][(4 * tg + i) * KROW + c * 16]) = kreg[k][i];
-      unsigned char *vd = &vbuf[slot][(tg * 128 + 8 * c) * 8];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {  // dims 8c + 2j and 8c + 2j + 1
-        auto word = [j](const uint4 &v) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; };
-        const uint32_t w0 = word(vreg[k][0]), w1 = word(vreg[k][1]);
-        const uint32_t w2 = word(vreg[k][2]), w3 = word(vreg[k][3]);
-        uint4 o;
-        o.x = (w0 & 0xffffu) | (w1 << 16);          // dim 2j: tokens 0, 1
-        o.y = (w2 & 0xffffu) | (w3 << 16);          //         tokens 2, 3
-        o.z = (w0 >> 16) | (w1 & 0xffff0000u);      // dim 2j+1: tokens 0, 1
-        o.w = (w2 >> 16) | (w3 & 0xffff0000u);      //           tokens 2, 3
-        *(uint4 *)(vd + 16 * j) = o;
-      }
-    }
-  };
-
-  const float c2 = a.scale * 1.4426950408889634f;  // logits in log2 units
-  float m2 = -INFINITY, lsum = 0.f;
-  f32x16 oacc[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) oacc[dt][e] = 0.f;
-
-  if (nst > 0) {
-    stage_phys(phys, 0);
-    load_stage(phys, 0);
-    stage_phys(phys, 1);
-    store_stage(0);
-  }
-  __syncthreads();
-  for (int gs = 0; gs < nst; ++gs) {
-    const int slot = gs & 1;
-    // stage gs+1 into registers (past the end: zero rows, never stored for use)
-    load_stage(phys, gs + 1);
-    stage_phys(phys, gs + 2);
-    // S^T of slice b of this stage: 32 tokens x 32 query rows (dot products, unscaled)
-    auto qk = [&](int b) {
-      V8 kf[KS];
-      const unsigned char *kr = &kbuf[slot][(32 * b + lcol) * KROW + lh * 16];
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kf[ks] = *(const V8 *)(kr + ks * 32);
-      f32x16 st = {};
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        if constexpr (__is_same(T, __bf16))
-          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[ks], qf[ks], st, 0, 0, 0);
-        else
-          st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[ks], qf[ks], st, 0, 0, 0);
-      }
-      return st;
-    };
-    // online softmax of the lane's query row over slice b, then O^T += V^T . P^T
-    auto softmax_pv = [&](f32x16 st, int b) {
-      const int t0 = gs * ST + 32 * b;
-      // tokens at or past a row's limit are masked; slices every row sees whole skip this
-      if (__builtin_amdgcn_ballot_w64(lim_m < t0 + 32) != 0ull) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int t = t0 + 8 * (e >> 2) + 4 * lh + (e & 3);
-          st[e] = t < lim_m ? st[e] : -INFINITY;
-        }
-      }
-      float mx = st[0];
-#pragma unroll
-      for (int e = 1; e < 16; ++e) mx = fmaxf(mx, st[e]);
-      {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-        mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-      }
-      const float m_new = fmaxf(m2, mx * c2);  // log2 units (c2 > 0)
-      const float msafe = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m2 - msafe);
-      float ps = 0.f;
-      V8 pb[2];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float pe = __builtin_amdgcn_exp2f(fmaf(st[e], c2, -msafe));
-        ps += pe;
-        pb[e >> 3][e & 7] = (T)pe;
-      }
-      {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ps), __float_as_uint(ps), false, false);
-        ps = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-      }
-      lsum = lsum * alpha + ps;
-      m2 = m_new;
-      // O is rescaled only when some row of the wave raised its max (alpha < 1); the
-      // running max settles after the first slices, so most slices skip the 64 multiplies
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0ull) {
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) oacc[dt][e] *= alpha;
-      }
-      // O^T += V^T . P^T: A = V^T[32dt + lcol][tau(kb, lh, 0..7)]
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          // tokens 32b + 16kb + 4lh + 0..3 (group g1) and + 8 .. + 11 (group g1 + 2)
-          const int g1 = 8 * b + 4 * kb + lh;
-          const unsigned char *vr = &vbuf[slot][(g1 * 128 + 32 * dt + lcol) * 8];
-          const uint2 lo = *(const uint2 *)vr, hi = *(const uint2 *)(vr + 2 * 128 * 8);
-          const uint4 u = make_uint4(lo.x, lo.y, hi.x, hi.y);
-          const V8 va = __builtin_bit_cast(V8, u);
-          if constexpr (__is_same(T, __bf16))
-            oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kb], oacc[dt], 0, 0, 0);
-          else
-            oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[kb], oacc[dt], 0, 0, 0);
-        }
-      }
-    };
-    // the next slice's S^T chain is issued before this slice's softmax, so the matrix
-    // core works while the VALU does the exp/max/sum
-    f32x16 st_cur = qk(0);
-#pragma unroll
-    for (int b = 0; b < GS; ++b) {
-      f32x16 st_next = {};
-      if (b + 1 < GS) st_next = qk(b + 1);
-      softmax_pv(st_cur, b);
-      st_cur = st_next;
-    }
-    if (gs + 1 < nst) store_stage(slot ^ 1);
-    __syncthreads();
-  }
-
-  // ---- split: the chunk's partial (unnormalised O, max, sum) for the combine kernel
-  if (a.nchunk > 1) {
-    if (valid) {
-      const int64_t pr = ((int64_t)p * a.rows_pad + row) * a.nchunk + chunk;
-      float *wo = a.ws_o + pr * 128;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          f32x4 v;
-          v[0] = oacc[dt][4 * i]; v[1] = oacc[dt][4 * i + 1]; v[2] = oacc[dt][4 * i + 2]; v[3] = oacc[dt][4 * i + 3];
-          *(f32x4 *)(wo + 32 * dt + 8 * i + 4 * lh) = v;
-        }
-      if (lh == 0) { a.ws_ml[pr * 2] = m2; a.ws_ml[pr * 2 + 1] = lsum; }
-    }
-    return;
-  }
-  // ---- out[dim] = O^T[dim][row] / lsum, lse = ln 2 * (m2 + log2 lsum)
-  if (valid) {
-    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
-    float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * G + g) * a.o_sh;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d0 = 32 * dt + 8 * i + 4 * lh;
-        f32x4 v;
-        v[0] = oacc[dt][4 * i] * inv; v[1] = oacc[dt][4 * i + 1] * inv;
-        v[2] = oacc[dt][4 * i + 2] * inv; v[3] = oacc[dt][4 * i + 3] * inv;
-        *(f32x4 *)(op + d0) = v;
-      }
-    if (lh == 0)
-      a.lse[(int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * G + g] =
-          lsum > 0.f ? (m2 + __log2f(lsum)) * 0.6931471805599453f : -INFINITY;
-  }
-}
-
 // ------------------------------------------------------------------ decode path
 // A pair whose query rows fit one 32-row tile (N*G <= 32: decode steps and short
 // action regions) gets a workgroup of DW waves per token chunk, each wave streaming
@@ -633,6 +351,330 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
         Lsum > 0.f ? (M + __log2f(Lsum)) * 0.6931471805599453f : -INFINITY;
 }
 
+// ------------------------------------------------------------------ ring path
+// Pairs with more than one 32-row tile.  A workgroup of NW waves (one row tile each)
+// shares ST-token stages of K and V held in an NSTG-deep LDS ring.  The stages are
+// loaded straight into LDS with buffer_load_dwordx4 ... lds, NSTG - 1 stages ahead of
+// the one being multiplied: no register staging, one LDS barrier per stage, and the
+// wait for a stage is counted by hand (wait_stages).  Each load
+// instruction moves four token rows (1 KB) of one block, so the buffer resource is that
+// block (wave-uniform); its lanes pick the global 16-byte chunk that lands in their LDS
+// slot, which lays rows out with the decode path's XOR swizzle, and tokens past the
+// chunk (or in blocks the table marks invalid) are out of the resource's range, so the
+// hardware writes zeros.  V is read back transposed (ds_read_b64_tr_b16).  The block
+// table of the workgroup's token range sits in an LDS window, refilled (after a drain)
+// when the loads reach its end.
+
+// s_waitcnt with vmcnt <= N and the other counters unconstrained
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// workgroup barrier ordering LDS only (no drain of the loads in flight)
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Stage size and ring depth, from a sweep on 36 layers x 32k tokens x 128 queries and on
+// 4 requests x 8k tokens x 48 causal queries: with the loads issued ahead, depth matters
+// little (3 or 4 stages of 64 tokens and 2 of 128 are within 8%) and fewer, larger stages
+// (fewer barriers) win; 4- and 2-wave workgroups keep 64-token stages so that two fit
+// per CU.
+template <int NW> struct RingShape {
+  static constexpr int ST = NW >= 8 ? 128 : 64;               // tokens per stage
+  static constexpr int NSTG = 2;                              // ring depth
+  static constexpr int TBLW = NW >= 8 ? 4096 : 2048;          // block-table window (entries)
+  static constexpr int SBYTES = 2 * ST * 256;                 // K then V rows of a stage
+  static constexpr int IPP = ST / 4;                          // load instructions per plane
+  static constexpr int PER = 2 * IPP / NW;                    // per wave per stage
+  static_assert(ST % 32 == 0 && (2 * IPP) % NW == 0, "whole load instructions per wave");
+};
+
+// wait until at most `rem` stages' loads (PER instructions each) are outstanding
+template <int PER, int MAXR>
+__device__ __forceinline__ void wait_stages(int rem) {
+  if constexpr (MAXR >= 3) { if (rem >= 3) { wait_vmcnt<3 * PER>(); return; } }
+  if constexpr (MAXR >= 2) { if (rem >= 2) { wait_vmcnt<2 * PER>(); return; } }
+  if constexpr (MAXR >= 1) { if (rem >= 1) { wait_vmcnt<PER>(); return; } }
+  wait_vmcnt<0>();
+}
+
+typedef int ri32x4 __attribute__((ext_vector_type(4)));
+
+// 16 bytes from buffer `rsrc` at byte offset voff into LDS at lds_base + 16 * lane.
+// Inline assembly: the compiler's wait counting would otherwise drain every load in
+// flight before each LDS read of the ring; the kernel counts them itself.  M0 carries
+// the LDS base and is restored.
+__device__ __forceinline__ void buf_lds16(ri32x4 rsrc, unsigned voff, unsigned lds_base) {
+  unsigned saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved)
+               : "v"(voff), "s"(rsrc), "s"(lds_base)
+               : "memory");
+}
+
+template <typename T, typename V8, int G, int NW, bool CAUSAL>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 4 ? 2 : 1, 2)))
+attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
+  using SH = RingShape<NW>;
+  constexpr int ST = SH::ST, NSTG = SH::NSTG, TBLW = SH::TBLW, PER = SH::PER;
+  __shared__ __attribute__((aligned(1024))) unsigned char ring[NSTG][SH::SBYTES];
+  __shared__ int tbl[TBLW];
+  __shared__ int wg_lim;
+
+  // XCD-aware mapping: the row groups and chunks of one pair share an XCD
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7, jj = bid >> 3;
+  const int per_pair = ngroups * a.nchunk;
+  const int p = (jj / per_pair) * 8 + xcd;
+  const int grp = (jj % per_pair) / a.nchunk, chunk = jj % a.nchunk;
+  if (p >= pairs) return;
+  const int h = p % a.Hkv;
+  const int r = (p / a.Hkv) % a.R;
+  const int l = p / (a.Hkv * a.R);
+  const int nq = attn_nq(a, r);
+  if (grp * NW * 32 >= nq * G) return;
+  const int S_all = attn_seq_len(a, r);
+  if (a.nchunk > 1 && chunk * a.tpc >= S_all) return;
+  const int c_begin = min(chunk * a.tpc, S_all);
+  const int S = min(S_all - c_begin, a.tpc);
+  const int BS = a.BS;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int lcol = lane & 31, lh = lane >> 5;
+  const int row = (grp * NW + wave) * 32 + lcol;
+  const int n = row / G, g = row % G;
+  const bool valid = n < nq;
+  const int lim = valid ? min(max(attn_lim(a, r, n, S_all) - c_begin, 0), S) : 0;
+  const int lim_m = valid ? lim : 0x7fffffff;
+  int s_end = S;
+  if constexpr (CAUSAL) {
+    if (tid == 0) wg_lim = 0;
+    __syncthreads();
+    if (valid && lim > 0) atomicMax(&wg_lim, lim);
+    __syncthreads();
+    s_end = wg_lim;
+  }
+  const int nst = (s_end + ST - 1) / ST;
+
+  V8 qf[8];
+  {
+    const T *qp = (const T *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr +
+                  (int64_t)(valid ? n : 0) * a.q_sn + (int64_t)(h * G + g) * a.q_sh + lh * 8;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = *(const V8 *)(qp + ks * 16);
+    if (!valid) {
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) qf[ks] = V8{};
+    }
+  }
+
+  // the query loads complete here, before the first ring load: otherwise the compiler's
+  // wait for them lands inside the loop, where the hardware counter also holds the
+  // ring's loads and the wait would drain them every stage
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) asm volatile("" ::"v"(qf[ks]));
+  // ---- block table window: logical blocks [blk0 + wbase, blk0 + wbase + TBLW)
+  const int blk0 = c_begin >> bs_shift;
+  int wbase = 0;
+  auto load_window = [&]() {
+    for (int i = tid; i < TBLW; i += NW * 64) tbl[i] = attn_phys(a, r, blk0 + wbase + i);
+  };
+  load_window();
+  __syncthreads();
+  // before issuing stage gi: move the window when the stage's last block is past it (the
+  // workgroup calls this uniformly; a stage spans at most ST / BS + 1 blocks)
+  auto ensure_window = [&](int gi) {
+    const int lb = ((c_begin + gi * ST + ST - 1) >> bs_shift) - blk0;
+    if (lb - wbase >= TBLW) {
+      __syncthreads();
+      wbase = ((c_begin + gi * ST) >> bs_shift) - blk0;
+      load_window();
+      __syncthreads();
+    }
+  };
+
+  // ---- stage loads: instruction k (0..31) of a stage: plane k / 16, tokens 4(k%16) .. +3
+  const uint64_t kbase = (uint64_t)(uintptr_t)((const T *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh);
+  const uint64_t vbase = kbase + (uint64_t)a.kv_sv * sizeof(T);
+  const unsigned blk_bytes = (unsigned)(((int64_t)(BS - 1) * a.kv_ss + 128) * sizeof(T));
+  const unsigned ring_base = (unsigned)(uintptr_t)&ring[0][0];
+  auto issue = [&](int gi) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int k = wave * PER + i;
+      const int plane = k / SH::IPP, tg = k % SH::IPP;
+      const int t0 = gi * ST + 4 * tg;                       // chunk-relative first token
+      const int bi = ((c_begin + t0) >> bs_shift) - blk0 - wbase;
+      const int ph = __builtin_amdgcn_readfirstlane(tbl[bi]);
+      const uint64_t bb = (plane ? vbase : kbase) + (uint64_t)(ph < 0 ? 0 : ph) * (uint64_t)a.kv_sb * sizeof(T);
+      ri32x4 rs;
+      rs[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)bb);
+      rs[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(bb >> 32) & 0xffffu));
+      rs[2] = __builtin_amdgcn_readfirstlane(ph < 0 ? 0 : (int)blk_bytes);
+      rs[3] = 0x00020000;
+      const int tl = 4 * tg + (lane >> 4);                   // token within the stage
+      const int t = gi * ST + tl;
+      const int c = (lane & 15) ^ dswz(tl);                   // global chunk landing in slot lane%16
+      const unsigned voff = t < S ? (unsigned)((((c_begin + t) & (BS - 1)) * a.kv_ss + c * 8) * sizeof(T)) : 0xfffffff0u;
+      const unsigned dst = ring_base + (unsigned)((gi % NSTG) * SH::SBYTES + plane * ST * 256 + tg * 1024);
+      buf_lds16(rs, voff, __builtin_amdgcn_readfirstlane(dst));
+    }
+  };
+
+  const float c2 = a.scale * 1.4426950408889634f;
+  float m2 = -INFINITY, lsum = 0.f;
+  f32x16 oacc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) oacc[dt][e] = 0.f;
+
+  const int jq = (lane & 15) >> 2, qq = lane & 3;
+  const int dgrp = 16 * ((lane >> 4) & 1) + 4 * qq;
+  auto qk = [&](const unsigned char *kl) {
+    f32x16 st = {};
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const int c = 2 * ks + lh;
+      const V8 kf = *(const V8 *)(kl + lcol * 256 + ((c ^ dswz(lcol)) << 4));
+      if constexpr (__is_same(T, __bf16))
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], st, 0, 0, 0);
+      else
+        st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], st, 0, 0, 0);
+    }
+    return st;
+  };
+  auto softmax_pv = [&](f32x16 st, const unsigned char *vl, int t0) {
+    if (__builtin_amdgcn_ballot_w64(lim_m < t0 + 32) != 0ull) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int t = t0 + 8 * (e >> 2) + 4 * lh + (e & 3);
+        st[e] = t < lim_m ? st[e] : -INFINITY;
+      }
+    }
+    float mx = st[0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e) mx = fmaxf(mx, st[e]);
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
+    const float m_new = fmaxf(m2, mx * c2);
+    const float msafe = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m2 - msafe);
+    float ps = 0.f;
+    V8 pb[2];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float pe = __builtin_amdgcn_exp2f(fmaf(st[e], c2, -msafe));
+      ps += pe;
+      pb[e >> 3][e & 7] = (T)pe;
+    }
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ps), __float_as_uint(ps), false, false);
+      ps = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    lsum = lsum * alpha + ps;
+    m2 = m_new;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0ull) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) oacc[dt][e] *= alpha;
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const int d = 32 * dt + dgrp;
+        const int cc = d >> 3, half = (d >> 2) & 1;
+        const int t_lo = 16 * kb + 4 * lh + jq, t_hi = t_lo + 8;
+        const dv4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (dv4s __attribute__((address_space(3))) *)(vl + t_lo * 256 + ((cc ^ dswz(t_lo)) << 4) + half * 8));
+        const dv4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (dv4s __attribute__((address_space(3))) *)(vl + t_hi * 256 + ((cc ^ dswz(t_hi)) << 4) + half * 8));
+        const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+        const V8 va = __builtin_bit_cast(V8, make_uint4(l2.x, l2.y, h2.x, h2.y));
+        if constexpr (__is_same(T, __bf16))
+          oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kb], oacc[dt], 0, 0, 0);
+        else
+          oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[kb], oacc[dt], 0, 0, 0);
+      }
+    }
+  };
+
+  // ---- pipeline: stage g in ring slot g % NSTG, loads NSTG - 1 stages ahead
+#pragma unroll
+  for (int i = 0; i < NSTG - 1; ++i)
+    if (i < nst) {
+      ensure_window(i);
+      issue(i);
+    }
+  for (int gs = 0; gs < nst; ++gs) {
+    // stage gs has landed once at most rem younger stages' loads are outstanding
+    wait_stages<PER, NSTG - 2>(min(NSTG - 2, nst - 1 - gs));
+    lds_barrier();  // stage gs visible to all waves; stage gs - 1 is no longer read
+    const int gi = gs + NSTG - 1;
+    if (gi < nst) {
+      ensure_window(gi);
+      issue(gi);
+    }
+    const unsigned char *kl = ring[gs % NSTG];
+    const unsigned char *vl = kl + ST * 256;
+    // the next slice's S^T chain is issued before this slice's softmax, so the matrix
+    // core works while the VALU does the exp/max/sum
+    f32x16 st_cur = qk(kl);
+#pragma unroll
+    for (int b = 0; b < ST / 32; ++b) {
+      f32x16 st_next = {};
+      if (b + 1 < ST / 32) st_next = qk(kl + (b + 1) * 32 * 256);
+      softmax_pv(st_cur, vl + b * 32 * 256, gs * ST + 32 * b);
+      st_cur = st_next;
+    }
+  }
+
+  // ---- split: the chunk's partial (unnormalised O, max, sum) for the combine kernel
+  if (a.nchunk > 1) {
+    if (valid) {
+      const int64_t pr = ((int64_t)p * a.rows_pad + row) * a.nchunk + chunk;
+      float *wo = a.ws_o + pr * 128;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          f32x4 v;
+          v[0] = oacc[dt][4 * i]; v[1] = oacc[dt][4 * i + 1]; v[2] = oacc[dt][4 * i + 2]; v[3] = oacc[dt][4 * i + 3];
+          *(f32x4 *)(wo + 32 * dt + 8 * i + 4 * lh) = v;
+        }
+      if (lh == 0) { a.ws_ml[pr * 2] = m2; a.ws_ml[pr * 2 + 1] = lsum; }
+    }
+    return;
+  }
+  if (valid) {
+    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
+    float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * G + g) * a.o_sh;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d0 = 32 * dt + 8 * i + 4 * lh;
+        f32x4 v;
+        v[0] = oacc[dt][4 * i] * inv; v[1] = oacc[dt][4 * i + 1] * inv;
+        v[2] = oacc[dt][4 * i + 2] * inv; v[3] = oacc[dt][4 * i + 3] * inv;
+        *(f32x4 *)(op + d0) = v;
+      }
+    if (lh == 0)
+      a.lse[(int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * G + g] =
+          lsum > 0.f ? (m2 + __log2f(lsum)) * 0.6931471805599453f : -INFINITY;
+  }
+}
+
 // ------------------------------------------------------------------ split combine
 // grid ceil(pairs*rows_pad/4), 256 threads: one wave per (pair, row), two dims per lane.
 //   M = max_c m_c, w_c = 2^(m_c - M), out = sum_c w_c O_c / sum_c w_c l_c,
@@ -779,10 +821,10 @@ static AttnSplit attn_split(int pairs, int N, int G, int span) {
     return sp;
   }
   const int nw = attn_waves(rtiles);
-  const int st = nw >= 4 ? 16 * nw : 32;
+  const int st = nw >= 8 ? 128 : 64;  // ring stage (RingShape<nw>::ST)
   sp.ngroups = (rtiles + nw - 1) / nw;
   sp.rows_pad = sp.ngroups * nw * 32;
-  const int per_cu = nw == 8 ? 1 : nw == 4 ? 2 : 4;
+  const int per_cu = nw == 8 ? 1 : 2;  // resident ring workgroups per CU (LDS)
   const int64_t items = (int64_t)pairs * sp.ngroups;
   const int64_t want = 4LL * 256 * per_cu;
   int nchunk = (int)std::min<int64_t>(std::max<int64_t>(1, (want + items - 1) / items), std::max(1, span / 256));
@@ -824,10 +866,10 @@ static int launch_attn_mfma(AttnArgs a, int bs_shift, void *ws, size_t ws_bytes,
   do {                                                                                             \
     const int grid = ((pairs + 7) / 8) * 8 * sp.ngroups * sp.nchunk;                               \
     if (causal)                                                                                    \
-      hipLaunchKernelGGL((attn_mfma_kernel<T, V8, G, NWV, true>), dim3(grid), dim3(NWV * 64), 0,   \
+      hipLaunchKernelGGL((attn_ring_kernel<T, V8, G, NWV, true>), dim3(grid), dim3(NWV * 64), 0,   \
                          st, a, pairs, sp.ngroups, bs_shift);                                      \
     else                                                                                           \
-      hipLaunchKernelGGL((attn_mfma_kernel<T, V8, G, NWV, false>), dim3(grid), dim3(NWV * 64), 0,  \
+      hipLaunchKernelGGL((attn_ring_kernel<T, V8, G, NWV, false>), dim3(grid), dim3(NWV * 64), 0,  \
                          st, a, pairs, sp.ngroups, bs_shift);                                      \
   } while (0)
   switch (attn_waves(rtiles)) {

@@ -384,14 +384,13 @@ __device__ __forceinline__ void lds_barrier() {
 // little (3 or 4 stages of 64 tokens and 2 of 128 are within 8%) and fewer, larger stages
 // (fewer barriers) win; 4- and 2-wave workgroups keep 64-token stages so that two fit
 // per CU.
-template <int NW> struct RingShape {
-  static constexpr int ST = NW >= 8 ? 128 : 64;               // tokens per stage
+template <int TILES> struct RingShape {                      // TILES: row tiles per workgroup
+  static constexpr int ST = TILES >= 8 ? 128 : 64;            // tokens per stage
   static constexpr int NSTG = 2;                              // ring depth
-  static constexpr int TBLW = NW >= 8 ? 4096 : 2048;          // block-table window (entries)
+  static constexpr int TBLW = TILES >= 8 ? 4096 : 2048;       // block-table window (entries)
   static constexpr int SBYTES = 2 * ST * 256;                 // K then V rows of a stage
   static constexpr int IPP = ST / 4;                          // load instructions per plane
-  static constexpr int PER = 2 * IPP / NW;                    // per wave per stage
-  static_assert(ST % 32 == 0 && (2 * IPP) % NW == 0, "whole load instructions per wave");
+  static_assert(ST % 32 == 0, "whole slices per stage");
 };
 
 // wait until at most `rem` stages' loads (PER instructions each) are outstanding
@@ -417,11 +416,14 @@ __device__ __forceinline__ void buf_lds16(ri32x4 rsrc, unsigned voff, unsigned l
                : "memory");
 }
 
-template <typename T, typename V8, int G, int NW, bool CAUSAL>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW >= 4 ? 2 : 1, 2)))
+template <typename T, typename V8, int G, int NW, int RT, bool CAUSAL>
+__global__ void __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu(RT >= 2 ? 1 : (NW >= 4 ? 2 : 1), RT >= 2 ? 1 : 2)))
 attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
-  using SH = RingShape<NW>;
-  constexpr int ST = SH::ST, NSTG = SH::NSTG, TBLW = SH::TBLW, PER = SH::PER;
+  using SH = RingShape<NW * RT>;
+  constexpr int ST = SH::ST, NSTG = SH::NSTG, TBLW = SH::TBLW;
+  constexpr int PER = 2 * SH::IPP / NW;  // load instructions per wave per stage
+  static_assert((2 * SH::IPP) % NW == 0, "whole load instructions per wave");
   __shared__ __attribute__((aligned(1024))) unsigned char ring[NSTG][SH::SBYTES];
   __shared__ int tbl[TBLW];
   __shared__ int wg_lim;
@@ -437,7 +439,7 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
   const int r = (p / a.Hkv) % a.R;
   const int l = p / (a.Hkv * a.R);
   const int nq = attn_nq(a, r);
-  if (grp * NW * 32 >= nq * G) return;
+  if (grp * NW * RT * 32 >= nq * G) return;
   const int S_all = attn_seq_len(a, r);
   if (a.nchunk > 1 && chunk * a.tpc >= S_all) return;
   const int c_begin = min(chunk * a.tpc, S_all);
@@ -447,38 +449,51 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int lcol = lane & 31, lh = lane >> 5;
-  const int row = (grp * NW + wave) * 32 + lcol;
-  const int n = row / G, g = row % G;
-  const bool valid = n < nq;
-  const int lim = valid ? min(max(attn_lim(a, r, n, S_all) - c_begin, 0), S) : 0;
-  const int lim_m = valid ? lim : 0x7fffffff;
+  // the wave's RT row tiles: rows ((grp * NW + wave) * RT + rt) * 32 + lcol
+  int row[RT], n[RT], g[RT], lim_m[RT];
+  bool valid[RT];
+  int my_lim = 0;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    row[rt] = ((grp * NW + wave) * RT + rt) * 32 + lcol;
+    n[rt] = row[rt] / G;
+    g[rt] = row[rt] % G;
+    valid[rt] = n[rt] < nq;
+    const int lim = valid[rt] ? min(max(attn_lim(a, r, n[rt], S_all) - c_begin, 0), S) : 0;
+    // the masking limit: padding rows (never written) see everything, so they never force it
+    lim_m[rt] = valid[rt] ? lim : 0x7fffffff;
+    my_lim = max(my_lim, lim);
+  }
   int s_end = S;
   if constexpr (CAUSAL) {
     if (tid == 0) wg_lim = 0;
     __syncthreads();
-    if (valid && lim > 0) atomicMax(&wg_lim, lim);
+    if (my_lim > 0) atomicMax(&wg_lim, my_lim);
     __syncthreads();
     s_end = wg_lim;
   }
   const int nst = (s_end + ST - 1) / ST;
 
-  V8 qf[8];
-  {
+  V8 qf[RT][8];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
     const T *qp = (const T *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr +
-                  (int64_t)(valid ? n : 0) * a.q_sn + (int64_t)(h * G + g) * a.q_sh + lh * 8;
+                  (int64_t)(valid[rt] ? n[rt] : 0) * a.q_sn + (int64_t)(h * G + g[rt]) * a.q_sh + lh * 8;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qf[ks] = *(const V8 *)(qp + ks * 16);
-    if (!valid) {
+    for (int ks = 0; ks < 8; ++ks) qf[rt][ks] = *(const V8 *)(qp + ks * 16);
+    if (!valid[rt]) {
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) qf[ks] = V8{};
+      for (int ks = 0; ks < 8; ++ks) qf[rt][ks] = V8{};
     }
   }
-
   // the query loads complete here, before the first ring load: otherwise the compiler's
   // wait for them lands inside the loop, where the hardware counter also holds the
   // ring's loads and the wait would drain them every stage
 #pragma unroll
-  for (int ks = 0; ks < 8; ++ks) asm volatile("" ::"v"(qf[ks]));
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) asm volatile("" ::"v"(qf[rt][ks]));
+
   // ---- block table window: logical blocks [blk0 + wbase, blk0 + wbase + TBLW)
   const int blk0 = c_begin >> bs_shift;
   int wbase = 0;
@@ -499,7 +514,7 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
     }
   };
 
-  // ---- stage loads: instruction k (0..31) of a stage: plane k / 16, tokens 4(k%16) .. +3
+  // ---- stage loads: instruction k of a stage: plane k / IPP, tokens 4(k % IPP) .. +3
   const uint64_t kbase = (uint64_t)(uintptr_t)((const T *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh);
   const uint64_t vbase = kbase + (uint64_t)a.kv_sv * sizeof(T);
   const unsigned blk_bytes = (unsigned)(((int64_t)(BS - 1) * a.kv_ss + 128) * sizeof(T));
@@ -528,65 +543,84 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
   };
 
   const float c2 = a.scale * 1.4426950408889634f;
-  float m2 = -INFINITY, lsum = 0.f;
-  f32x16 oacc[4];
+  float m2[RT], lsum[RT];
+  f32x16 oacc[RT][4];
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int rt = 0; rt < RT; ++rt) {
+    m2[rt] = -INFINITY;
+    lsum[rt] = 0.f;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) oacc[dt][e] = 0.f;
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) oacc[rt][dt][e] = 0.f;
+  }
 
   const int jq = (lane & 15) >> 2, qq = lane & 3;
   const int dgrp = 16 * ((lane >> 4) & 1) + 4 * qq;
+  struct Tiles { f32x16 s[RT]; };
+  // S^T = K . Q^T of one 32-token slice for every row tile: each K fragment read once
   auto qk = [&](const unsigned char *kl) {
-    f32x16 st = {};
+    Tiles st;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) st.s[rt] = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
       const int c = 2 * ks + lh;
       const V8 kf = *(const V8 *)(kl + lcol * 256 + ((c ^ dswz(lcol)) << 4));
-      if constexpr (__is_same(T, __bf16))
-        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], st, 0, 0, 0);
-      else
-        st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], st, 0, 0, 0);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        if constexpr (__is_same(T, __bf16))
+          st.s[rt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[rt][ks], st.s[rt], 0, 0, 0);
+        else
+          st.s[rt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[rt][ks], st.s[rt], 0, 0, 0);
+      }
     }
     return st;
   };
-  auto softmax_pv = [&](f32x16 st, const unsigned char *vl, int t0) {
-    if (__builtin_amdgcn_ballot_w64(lim_m < t0 + 32) != 0ull) {
+  // online softmax of each tile's rows over the slice, then O^T += V^T . P^T with each V^T
+  // fragment read once for all tiles
+  auto softmax_pv = [&](Tiles &st, const unsigned char *vl, int t0) {
+    V8 pb[RT][2];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      f32x16 &x = st.s[rt];
+      if (__builtin_amdgcn_ballot_w64(lim_m[rt] < t0 + 32) != 0ull) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int t = t0 + 8 * (e >> 2) + 4 * lh + (e & 3);
+          x[e] = t < lim_m[rt] ? x[e] : -INFINITY;
+        }
+      }
+      float mx = x[0];
+#pragma unroll
+      for (int e = 1; e < 16; ++e) mx = fmaxf(mx, x[e]);
+      {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+        mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      }
+      const float m_new = fmaxf(m2[rt], mx * c2);
+      const float msafe = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m2[rt] - msafe);
+      float ps = 0.f;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        const int t = t0 + 8 * (e >> 2) + 4 * lh + (e & 3);
-        st[e] = t < lim_m ? st[e] : -INFINITY;
+        const float pe = __builtin_amdgcn_exp2f(fmaf(x[e], c2, -msafe));
+        ps += pe;
+        pb[rt][e >> 3][e & 7] = (T)pe;
       }
-    }
-    float mx = st[0];
+      {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ps), __float_as_uint(ps), false, false);
+        ps = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      }
+      lsum[rt] = lsum[rt] * alpha + ps;
+      m2[rt] = m_new;
+      // O is rescaled only when some row of the tile raised its max
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0ull) {
 #pragma unroll
-    for (int e = 1; e < 16; ++e) mx = fmaxf(mx, st[e]);
-    {
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-    }
-    const float m_new = fmaxf(m2, mx * c2);
-    const float msafe = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m2 - msafe);
-    float ps = 0.f;
-    V8 pb[2];
+        for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float pe = __builtin_amdgcn_exp2f(fmaf(st[e], c2, -msafe));
-      ps += pe;
-      pb[e >> 3][e & 7] = (T)pe;
-    }
-    {
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ps), __float_as_uint(ps), false, false);
-      ps = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-    }
-    lsum = lsum * alpha + ps;
-    m2 = m_new;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0ull) {
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) oacc[dt][e] *= alpha;
+          for (int e = 0; e < 16; ++e) oacc[rt][dt][e] *= alpha;
+      }
     }
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -601,10 +635,13 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
             (dv4s __attribute__((address_space(3))) *)(vl + t_hi * 256 + ((cc ^ dswz(t_hi)) << 4) + half * 8));
         const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
         const V8 va = __builtin_bit_cast(V8, make_uint4(l2.x, l2.y, h2.x, h2.y));
-        if constexpr (__is_same(T, __bf16))
-          oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kb], oacc[dt], 0, 0, 0);
-        else
-          oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[kb], oacc[dt], 0, 0, 0);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          if constexpr (__is_same(T, __bf16))
+            oacc[rt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[rt][kb], oacc[rt][dt], 0, 0, 0);
+          else
+            oacc[rt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[rt][kb], oacc[rt][dt], 0, 0, 0);
+        }
       }
     }
   };
@@ -629,49 +666,51 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
     const unsigned char *vl = kl + ST * 256;
     // the next slice's S^T chain is issued before this slice's softmax, so the matrix
     // core works while the VALU does the exp/max/sum
-    f32x16 st_cur = qk(kl);
+    Tiles st_cur = qk(kl);
 #pragma unroll
     for (int b = 0; b < ST / 32; ++b) {
-      f32x16 st_next = {};
+      Tiles st_next;
       if (b + 1 < ST / 32) st_next = qk(kl + (b + 1) * 32 * 256);
       softmax_pv(st_cur, vl + b * 32 * 256, gs * ST + 32 * b);
       st_cur = st_next;
     }
   }
 
-  // ---- split: the chunk's partial (unnormalised O, max, sum) for the combine kernel
-  if (a.nchunk > 1) {
-    if (valid) {
-      const int64_t pr = ((int64_t)p * a.rows_pad + row) * a.nchunk + chunk;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    if (!valid[rt]) continue;
+    // ---- split: the chunk's partial (unnormalised O, max, sum) for the combine kernel
+    if (a.nchunk > 1) {
+      const int64_t pr = ((int64_t)p * a.rows_pad + row[rt]) * a.nchunk + chunk;
       float *wo = a.ws_o + pr * 128;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           f32x4 v;
-          v[0] = oacc[dt][4 * i]; v[1] = oacc[dt][4 * i + 1]; v[2] = oacc[dt][4 * i + 2]; v[3] = oacc[dt][4 * i + 3];
+          v[0] = oacc[rt][dt][4 * i]; v[1] = oacc[rt][dt][4 * i + 1];
+          v[2] = oacc[rt][dt][4 * i + 2]; v[3] = oacc[rt][dt][4 * i + 3];
           *(f32x4 *)(wo + 32 * dt + 8 * i + 4 * lh) = v;
         }
-      if (lh == 0) { a.ws_ml[pr * 2] = m2; a.ws_ml[pr * 2 + 1] = lsum; }
+      if (lh == 0) { a.ws_ml[pr * 2] = m2[rt]; a.ws_ml[pr * 2 + 1] = lsum[rt]; }
+      continue;
     }
-    return;
-  }
-  if (valid) {
-    const float inv = lsum > 0.f ? 1.0f / lsum : 0.f;
-    float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * G + g) * a.o_sh;
+    const float inv = lsum[rt] > 0.f ? 1.0f / lsum[rt] : 0.f;
+    float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n[rt] * a.o_sn +
+                (int64_t)(h * G + g[rt]) * a.o_sh;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int d0 = 32 * dt + 8 * i + 4 * lh;
         f32x4 v;
-        v[0] = oacc[dt][4 * i] * inv; v[1] = oacc[dt][4 * i + 1] * inv;
-        v[2] = oacc[dt][4 * i + 2] * inv; v[3] = oacc[dt][4 * i + 3] * inv;
+        v[0] = oacc[rt][dt][4 * i] * inv; v[1] = oacc[rt][dt][4 * i + 1] * inv;
+        v[2] = oacc[rt][dt][4 * i + 2] * inv; v[3] = oacc[rt][dt][4 * i + 3] * inv;
         *(f32x4 *)(op + d0) = v;
       }
     if (lh == 0)
-      a.lse[(int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * G + g] =
-          lsum > 0.f ? (m2 + __log2f(lsum)) * 0.6931471805599453f : -INFINITY;
+      a.lse[(int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n[rt] * a.lse_sn + h * G + g[rt]] =
+          lsum[rt] > 0.f ? (m2[rt] + __log2f(lsum[rt])) * 0.6931471805599453f : -INFINITY;
   }
 }
 
@@ -795,8 +834,17 @@ __global__ void __launch_bounds__(256) attn_generic_kernel(AttnArgs a) {
         Lsum > 0.f ? M + logf(Lsum) : -INFINITY;
 }
 
-// Waves per workgroup for a launch: enough 32-row tiles for the pair's query rows, at most 8.
-static int attn_waves(int rtiles) { return rtiles <= 1 ? 1 : rtiles <= 2 ? 2 : rtiles <= 4 ? 4 : 8; }
+// Ring workgroup shape for a pair with rtiles 32-row tiles of query rows: waves and row
+// tiles per wave.  Two tiles per wave (each K and V^T fragment read once for 64 rows)
+// needs about 500 registers, one wave per SIMD, and measured 4.86 ms against 3.40 ms for
+// one tile per wave at two waves per SIMD (36 layers x 32k x 128 queries): the second
+// wave hides more than the halved LDS reads save.
+struct RingCfg { int nw, rt; };
+static RingCfg ring_cfg(int rtiles) {
+  if (rtiles <= 2) return {2, 1};
+  if (rtiles <= 4) return {4, 1};
+  return {8, 1};
+}
 
 // Token-range split: enough (pair, row group, chunk) work items for about four rounds of
 // resident workgroups (1 per CU at 8 waves, 2 at 4, 4 at 1-2 waves: the LDS stage
@@ -820,11 +868,12 @@ static AttnSplit attn_split(int pairs, int N, int G, int span) {
     if (sp.nchunk <= 1) { sp.nchunk = 1; sp.tpc = std::max(span, 1); }
     return sp;
   }
-  const int nw = attn_waves(rtiles);
-  const int st = nw >= 8 ? 128 : 64;  // ring stage (RingShape<nw>::ST)
-  sp.ngroups = (rtiles + nw - 1) / nw;
-  sp.rows_pad = sp.ngroups * nw * 32;
-  const int per_cu = nw == 8 ? 1 : 2;  // resident ring workgroups per CU (LDS)
+  const RingCfg cfg = ring_cfg(rtiles);
+  const int tiles = cfg.nw * cfg.rt;
+  const int st = tiles >= 8 ? 128 : 64;  // ring stage (RingShape<tiles>::ST)
+  sp.ngroups = (rtiles + tiles - 1) / tiles;
+  sp.rows_pad = sp.ngroups * tiles * 32;
+  const int per_cu = tiles >= 8 ? 1 : 2;  // resident ring workgroups per CU (LDS)
   const int64_t items = (int64_t)pairs * sp.ngroups;
   const int64_t want = 4LL * 256 * per_cu;
   int nchunk = (int)std::min<int64_t>(std::max<int64_t>(1, (want + items - 1) / items), std::max(1, span / 256));
@@ -862,21 +911,20 @@ static int launch_attn_mfma(AttnArgs a, int bs_shift, void *ws, size_t ws_bytes,
     else
       hipLaunchKernelGGL((attn_decode_kernel<T, V8, G, false>), dim3(grid), dim3(DW * 64), 0, st, a, pairs, bs_shift);
   } else {
-#define ACTKV_ATTN(NWV)                                                                            \
+#define ACTKV_ATTN(NWV, RTV)                                                                       \
   do {                                                                                             \
     const int grid = ((pairs + 7) / 8) * 8 * sp.ngroups * sp.nchunk;                               \
     if (causal)                                                                                    \
-      hipLaunchKernelGGL((attn_ring_kernel<T, V8, G, NWV, true>), dim3(grid), dim3(NWV * 64), 0,   \
-                         st, a, pairs, sp.ngroups, bs_shift);                                      \
+      hipLaunchKernelGGL((attn_ring_kernel<T, V8, G, NWV, RTV, true>), dim3(grid), dim3(NWV * 64), \
+                         0, st, a, pairs, sp.ngroups, bs_shift);                                   \
     else                                                                                           \
-      hipLaunchKernelGGL((attn_ring_kernel<T, V8, G, NWV, false>), dim3(grid), dim3(NWV * 64), 0,  \
-                         st, a, pairs, sp.ngroups, bs_shift);                                      \
+      hipLaunchKernelGGL((attn_ring_kernel<T, V8, G, NWV, RTV, false>), dim3(grid), dim3(NWV * 64),\
+                         0, st, a, pairs, sp.ngroups, bs_shift);                                   \
   } while (0)
-  switch (attn_waves(rtiles)) {
-    case 2: ACTKV_ATTN(2); break;
-    case 4: ACTKV_ATTN(4); break;
-    default: ACTKV_ATTN(8); break;
-  }
+  const RingCfg cfg = ring_cfg(rtiles);
+  if (cfg.nw == 2) ACTKV_ATTN(2, 1);
+  else if (cfg.nw == 4) ACTKV_ATTN(4, 1);
+  else ACTKV_ATTN(8, 1);
 #undef ACTKV_ATTN
   }
   int rc = actkv_check_launch();

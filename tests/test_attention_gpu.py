@@ -175,3 +175,47 @@ def test_token_split_and_single_pass_agree(monkeypatch, n_q):
     for out, lse in ((split_out, split_lse), (one_out, one_lse)):
         torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
         torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-2)
+
+
+@pytest.mark.parametrize("bs,lens,n_q,causal,split", [
+    (32, [3000, 1111], 40, True, True),      # ring kernel (160 rows), block 32
+    (64, [2600], 8, False, True),            # decode kernel (32 rows), block 64
+    (256, [5000, 700], 48, True, True),      # ring kernel; chunk starts are not block-aligned
+    (256, [5000], 3, True, False),           # decode kernel, one pass
+    (128, [3333], 100, False, False),        # ring kernel, one pass, 400 rows in two groups
+])
+def test_block_sizes_and_chunking(monkeypatch, bs, lens, n_q, causal, split):
+    """The matrix-core kernels take any power-of-two block of at least 16 tokens: the ring
+    kernel's loads are per block and its block-table window is indexed by block."""
+    from actkv import _hip
+    cache = _cache(lens, hkv=2, bs=bs, seed=bs + n_q)
+    reqs = list(range(len(lens)))
+    g = torch.Generator().manual_seed(bs)
+    q = torch.randn(len(lens), n_q, 8, 128, generator=g).to(torch.bfloat16)
+    kv_len = None
+    if causal:
+        kv_len = torch.stack([torch.randint(1, S + 1, (n_q,), generator=g) for S in lens]).to(torch.int32)
+    lib = _hip.lib()
+    if split:
+        assert lib.actkv_paged_attention_workspace_size(1, len(lens), n_q, 8, 2, 128,
+                                                        max(len(t) for t in cache.tables.values()), bs) > 0
+    else:
+        monkeypatch.setattr(lib, "actkv_paged_attention_workspace_size", lambda *a: 0)
+    out, lse = cache.decode_attention(reqs, q.cuda(), kv_len=None if kv_len is None else kv_len.cuda())
+    want_out, want_lse = _oracle(cache, reqs, q, 0, kv_len=None if kv_len is None else kv_len.tolist())
+    torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
+    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-2)
+
+
+def test_block_table_window_refill(monkeypatch):
+    """One workgroup attends 70k tokens of 16-token blocks in one pass: more blocks than the
+    ring kernel's LDS table window holds (4096), so the window is refilled mid-sequence."""
+    from actkv import _hip
+    cache = _cache([70000], hkv=1, seed=21)
+    g = torch.Generator().manual_seed(22)
+    q = torch.randn(1, 40, 4, 128, generator=g).to(torch.bfloat16)     # 160 rows: 8-wave groups
+    monkeypatch.setattr(_hip.lib(), "actkv_paged_attention_workspace_size", lambda *a: 0)
+    out, lse = cache.decode_attention([0], q.cuda())
+    want_out, want_lse = _oracle(cache, [0], q, 0)
+    torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
+    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-2)

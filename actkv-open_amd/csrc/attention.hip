@@ -101,9 +101,12 @@ __device__ __forceinline__ int attn_phys(const AttnArgs &a, int r, int b) {
 constexpr int DW = 4;                         // waves per decode workgroup
 constexpr int DREG = 2 * 32 * 256;            // LDS bytes per wave: K rows, then V rows
 
-// 16-byte chunk slot of chunk c of token t: distinct over 16 consecutive tokens (K
-// reads), and over the 8 chunks four consecutive tokens expose to a transposed V read
-__device__ __forceinline__ int dswz(int t) { return 2 * (t & 7) + ((t >> 3) & 1); }
+// 16-byte chunk slot of chunk c of token t is c ^ dswz(t).  Distinct slots, so no LDS bank
+// conflicts, for: 16 consecutive tokens at one chunk (K A-operand reads); four consecutive
+// tokens at four consecutive chunks (a 32-lane transposed V read: 16 slots); 16 chunks of
+// one token (row writes).  2 (t mod 8) + (t / 8 mod 2) left the transposed V reads
+// 2-way conflicted.
+__device__ __forceinline__ int dswz(int t) { return 4 * (t & 3) + ((t >> 2) & 3); }
 
 typedef short dv4s __attribute__((ext_vector_type(4)));
 

@@ -33,7 +33,8 @@ def test_known_answers_of_the_reference():
     (3, 8, [1000, 1717], [4, 0], 1760, "mean", 0.9),
     (2, 4, [33, 300, 65], [5, 7, 0], 320, "max", 0.5),
     (36, 8, [4096], [4], 4096, "mean", 0.9),
-    (1, 2, [50000], [4], 50016, "mean", 0.99),
+    (1, 2, [50000], [4], 50016, "mean", 0.99),             # scores through the workspace
+    (2, 8, [16384, 9000], [4, 0], 16384, "mean", 0.9),      # 16 tokens per thread in registers, full
 ])
 def test_lrfu_update_matches_the_oracle(L, H, seqs, prots, W, reduce, p):
     g = torch.Generator().manual_seed(sum(seqs))

@@ -88,7 +88,24 @@ def parse(argv=None):
     ap.add_argument("--serve-steps", type=int, default=48, help="decode steps per round")
     ap.add_argument("--serve-action", type=int, default=24, help="action tokens at the end of each round")
     ap.add_argument("--serve-budget", type=int, default=4096)
-    return ap.parse_args(argv)
+    args = ap.parse_args(argv)
+    if args.steps < 1:
+        ap.error("--steps must be at least 1 (the timed steps)")
+    if args.warmup < 0:
+        ap.error("--warmup must not be negative")
+    if args.ora_rounds < 1 or args.serve_rounds < 1 or args.serve_steps < 1:
+        ap.error("--ora-rounds, --serve-rounds and --serve-steps must be at least 1")
+    if not 0 <= args.serve_action <= args.serve_steps:
+        ap.error("--serve-action must be between 0 and --serve-steps")
+    return args
+
+
+def run_info(torch, dev):
+    """What ran: the GPU, the library build the kernels came from, and peak device memory."""
+    from actkv import _hip
+    return {"gpu": torch.cuda.get_device_name(dev),
+            "kernels": f"{_hip.lib().actkv_version().decode()} ({os.path.basename(_hip.LIB_PATH)})",
+            "peak_device_memory_bytes": int(torch.cuda.max_memory_allocated(dev))}
 
 
 class Workload:
@@ -374,7 +391,7 @@ def run_attn(args, dev):
     res["decode"] = dec
     res["value"] = rows["queries"]["us"]
     res["config"] = {"workload": res["queries"]["workload"], "parallelism": "single-gpu"}
-    res["gpu"] = torch.cuda.get_device_name(dev)
+    res.update(run_info(torch, dev))
     line = json.dumps(res)
     print(line)
     if args.out:
@@ -518,7 +535,7 @@ def run_ora(args, dev):
         "gc_us_max": round(max(p["gc_us"] for p in per_round), 1),
         "blocks_reclaimed_total": sum(p["blocks_reclaimed"] for p in per_round),
         "per_round": [{k: (round(v, 1) if isinstance(v, float) else v) for k, v in p.items()} for p in per_round],
-        "gpu": torch.cuda.get_device_name(dev),
+        **run_info(torch, dev),
     }
     line = json.dumps(result)
     print(line)
@@ -609,7 +626,7 @@ def run_serve(args, dev):
         "decode_ms_per_step_median": round(statistics.median(p["decode_ms_per_step"] for p in per_round), 2),
         "end_round_us_median": round(statistics.median(p["end_round_us"] for p in per_round), 1),
         "per_round": [{k: (round(v, 1) if isinstance(v, float) else v) for k, v in p.items()} for p in per_round],
-        "gpu": torch.cuda.get_device_name(dev),
+        **run_info(torch, dev),
     }
     line = json.dumps(result)
     print(line)
@@ -715,7 +732,7 @@ def main(argv=None):
         "single_layer": single,
         "checks": checks,
         "wall_s_incl_restore": round(m["wall_s_incl_restore"], 3),
-        "gpu": torch.cuda.get_device_name(dev),
+        **run_info(torch, dev),
     }
     line = json.dumps(result)
     print(line)

@@ -51,13 +51,79 @@ _tls = threading.local()   # the step being run by this thread's forward pass
 class _Step:
     """One forward pass over the batch: n new tokens per request."""
 
-    __slots__ = ("cache", "n", "starts", "plan", "seq", "bt", "kv_len", "capture", "q", "lse", "written")
+    __slots__ = ("cache", "n", "starts", "plan", "seq", "bt", "kv_len", "capture", "q", "lse", "written",
+                 "launch")
 
     def __init__(self, cache, n, starts, plan, seq, bt, kv_len, capture):
         self.cache, self.n, self.starts, self.plan = cache, n, starts, plan
         self.seq, self.bt, self.kv_len, self.capture = seq, bt, kv_len, capture
         self.q, self.lse = {}, {}
         self.written = 0
+        self.launch = None
+
+
+class _Launch:
+    """The step's append and attention launches on a GPU cache.  Everything that is the
+    same for every layer (cache strides, the append plan, block tables, the attention
+    workspace, the float32 output buffer) is set up once; a layer supplies its index and its
+    K/V or query tensors (a decode step runs these for each of the model's layers)."""
+
+    def __init__(self, st, key_states):
+        kv = st.cache.kv
+        t = kv.kv
+        b, hkv, n, d = key_states.shape
+        self.lib = _hip.lib()
+        self.dev = t.device
+        self.stream = _hip.stream(t.device)
+        es = t.element_size()
+        self.kv_ptr, self.kv_sl_bytes = t.data_ptr(), t.stride(0) * es
+        self.kv_code = _hip.dtype_code(t.dtype)
+        self.kv_strides = (t.stride(1), t.stride(2), t.stride(3), t.stride(4))
+        self.nb, self.bs, self.hkv, self.d = kv.num_blocks, kv.block_size, hkv, d
+        self.b, self.n = b, n
+        dev_plan, self.r_n, self.mb_plan, self.total = st.plan
+        self.plan_ptrs = (dev_plan[2 * self.r_n:].data_ptr(), dev_plan[3 * self.r_n:].data_ptr(),
+                          dev_plan.data_ptr(), dev_plan[4 * self.r_n:].data_ptr())
+        self.plan_keep = dev_plan
+        self.bt, self.seq, self.kv_len = st.bt, st.seq, st.kv_len
+        self.out = None
+
+    def append(self, layer, k, v):
+        """k, v: [B, n, Hkv, D] contiguous, one dtype -> the cache's layer `layer`."""
+        s1, s2, s3, s4 = self.kv_strides
+        rc = self.lib.actkv_append(
+            self.kv_ptr + layer * self.kv_sl_bytes, self.kv_code, 0, s1, s2, s3, s4, self.nb,
+            k.data_ptr(), v.data_ptr(), _hip.dtype_code(k.dtype), 0, self.hkv * self.d, self.d,
+            0, self.hkv * self.d, self.d, 1, self.hkv, self.d, self.r_n,
+            self.plan_ptrs[0], self.plan_ptrs[1], self.plan_ptrs[2], self.total,
+            self.plan_ptrs[3], self.mb_plan, self.mb_plan, self.bs, None, self.stream)
+        _hip.check(rc, "actkv_append")
+
+    def attend(self, layer, query, scale, capture):
+        """query [B, Hq, n, D] -> (out [B, n, Hq, D] float32, lse [B, n, Hq])."""
+        q = query.transpose(1, 2)
+        b, n, hq, d = q.shape
+        if self.out is None:
+            self.hq = hq
+            self.out = torch.empty(b, n, hq, d, dtype=torch.float32, device=self.dev)
+            self.lse_buf = torch.empty(b, n, hq, dtype=torch.float32, device=self.dev)
+            nbytes = int(self.lib.actkv_paged_attention_workspace_size(
+                1, b, n, hq, self.hkv, d, self.bt.shape[1], self.bs))
+            self.ws = _hip.scratch(self.dev, "attention", nbytes) if nbytes else None
+            self.ws_ptr, self.ws_bytes = (self.ws.data_ptr(), self.ws.numel()) if nbytes else (None, 0)
+        lse = torch.empty(b, n, hq, dtype=torch.float32, device=self.dev) if capture else self.lse_buf
+        out = self.out
+        qs = q.stride()
+        s1, s2, s3, s4 = self.kv_strides
+        rc = self.lib.actkv_paged_attention(
+            q.data_ptr(), _hip.dtype_code(q.dtype), 0, qs[0], qs[1], qs[2],
+            self.kv_ptr + layer * self.kv_sl_bytes, self.kv_code, 0, s1, s2, s3, s4, self.nb,
+            self.bt.data_ptr(), self.bt.stride(0), self.bt.shape[1], self.seq.data_ptr(), None,
+            _hip.ptr(self.kv_len), out.data_ptr(), 0, out.stride(0), out.stride(1), out.stride(2),
+            lse.data_ptr(), 0, lse.stride(0), lse.stride(1), 1, b, n, hq, self.hkv, d, self.bs,
+            float(scale), self.ws_ptr, self.ws_bytes, self.stream)
+        _hip.check(rc, "actkv_paged_attention")
+        return out, lse
 
 
 class _PagedLayer(CacheLayerMixin):
@@ -146,12 +212,17 @@ class PagedHFCache(Cache):
                 flat[1, slots] = value_states[i].transpose(0, 1).to(flat.dtype)
             st.written += 1
             return
-        # [B, Hkv, n, D] -> [1, B*n, Hkv, D]: request r's tokens are rows r*n .. r*n + n - 1
+        # [B, Hkv, n, D] -> [B, n, Hkv, D] contiguous: request r's tokens are rows r*n .. r*n + n - 1
         k = key_states.transpose(1, 2)
         v = value_states.transpose(1, 2)
-        k = (k if k.is_contiguous() else k.contiguous()).view(1, b * n, hkv, d)
-        v = (v if v.is_contiguous() else v.contiguous()).view(1, b * n, hkv, d)
-        self.kv._append_launch(st.plan, k, v, layer=layer)
+        k = k if k.is_contiguous() else k.contiguous()
+        v = v if v.is_contiguous() else v.contiguous()
+        if k.dtype == v.dtype and k.dtype in (torch.float32, torch.float16, torch.bfloat16):
+            if st.launch is None:
+                st.launch = _Launch(st, key_states)
+            st.launch.append(layer, k, v)
+        else:   # other source dtypes: the cache's general path converts them first
+            self.kv._append_launch(st.plan, k.view(1, b * n, hkv, d), v.view(1, b * n, hkv, d), layer=layer)
         st.written += 1
 
 
@@ -162,9 +233,12 @@ def paged_attention_forward(module, query, key, value, attention_mask, scaling=N
     if st is None:
         raise RuntimeError("actkv_paged attention runs with a PagedHFCache as past_key_values")
     layer = module.layer_idx
-    kv = st.cache.kv
     q = query.transpose(1, 2)                       # [B, n, Hq, D] view, unit last stride
-    out, lse = paged_decode_attention(q, kv.kv[layer], st.bt, st.seq, scaling, kv_len=st.kv_len)
+    if st.launch is not None:
+        scale = scaling if scaling is not None else query.shape[-1] ** -0.5
+        out, lse = st.launch.attend(layer, query, scale, st.capture)
+    else:
+        out, lse = paged_decode_attention(q, st.cache.kv.kv[layer], st.bt, st.seq, scaling, kv_len=st.kv_len)
     if st.capture:
         st.q[layer], st.lse[layer] = q, lse
     return out.to(query.dtype), None

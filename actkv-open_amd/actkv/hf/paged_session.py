@@ -170,6 +170,7 @@ class PagedHFCache(Cache):
         super().__init__(layers=[_PagedLayer(self, i) for i in range(kv.n_layers)])
         self.step: _Step | None = None
         self.capture = False      # keep q and lse of the next steps (action tokens)
+        self.static_step: _Step | None = None  # graph capture: the step's buffers are fixed
 
     def get_seq_length(self, layer_idx: int = 0) -> int:
         return max((self.kv.seq_used.get(r, 0) for r in self.reqs), default=0)
@@ -199,7 +200,12 @@ class PagedHFCache(Cache):
             raise ValueError(f"batch of {b} rows, the cache serves {len(self.reqs)} requests")
         st = self.step
         if layer == 0 or st is None or st.written >= self.kv.n_layers:
-            st = self.begin_step(n)
+            if self.static_step is not None:
+                # the caller has allocated the step and filled the static buffers
+                st = self.step = self.static_step
+                st.written = 0
+            else:
+                st = self.begin_step(n)
         elif st.n != n:
             raise RuntimeError("layers of one forward pass wrote different token counts")
         _tls.step = st
@@ -268,7 +274,7 @@ class PagedSession:
     (prefill, generate, end_round, _compress), with the paged cache instead of DynamicCache."""
 
     def __init__(self, model, batch: int, max_tokens: int, num_blocks: int | None = None,
-                 block_size: int = 16, lrfu: LRFUConfig | None = None):
+                 block_size: int = 16, lrfu: LRFUConfig | None = None, graph: bool = False):
         cfg = model.config
         types = set(getattr(cfg, "layer_types", None) or ["full_attention"])
         if types != {"full_attention"}:
@@ -292,6 +298,10 @@ class PagedSession:
         self.protected = [0] * batch      # protected prefix length
         self.n_action = [0] * batch       # action tokens kept this round
         self._act = []                    # per decode step with action tokens: (q, lse, kv_len, mask)
+        self.max_tokens = max_tokens
+        self.graph = graph                # decode steps replay a captured HIP graph
+        self._g = None                    # the captured step: graph, static buffers, staging
+        self._eager_decodes = 0
         model.set_attn_implementation(register())
 
     # ------------------------------------------------------------------ forward
@@ -325,6 +335,93 @@ class PagedSession:
         self.n_action = [0] * len(self.reqs)
         self._act = []
 
+    # ------------------------------------------------------------------ graph decode
+    # A decode step (one token for every sequence) launches a few hundred small kernels; with
+    # graph=True it is captured once as a HIP graph and replayed.  What changes between steps
+    # lives in fixed device buffers, refreshed by one host-to-device copy before each replay:
+    #   meta (int32): positions (int64 as lo/hi) | append plan: source offsets (int64),
+    #                 starts, counts, block tables [B, MBG] | lengths [B]
+    # The cache's hooks take a static step over these buffers (no allocation or upload while
+    # capturing), and the attention's launch shape depends only on the table width MBG.
+    def _graph_layout(self):
+        b = len(self.reqs)
+        mbg = -(-self.max_tokens // self.kv.block_size) + 1
+        return b, mbg, 2 * b, 2 * b + 4 * b + b * mbg   # B, MBG, plan offset, lengths offset
+
+    def _graph_fits(self) -> bool:
+        _, mbg, _, _ = self._graph_layout()
+        bs = self.kv.block_size
+        return all(-(-(self.kv.seq_used[r] + 1) // bs) <= mbg for r in self.reqs)
+
+    def _graph_prepare(self, ids: torch.Tensor) -> None:
+        """Host side of one graph step: allocate the new tokens' blocks (host free stack, in
+        request order), fill the static buffers, advance the lengths."""
+        g = self._g
+        b, mbg, po, lo = self._graph_layout()
+        kv = self.kv
+        starts = [kv.seq_used[r] for r in self.reqs]
+        for r, s0 in zip(self.reqs, starts):
+            kv._ensure(r, s0 + 1)
+        k = g["turn"]
+        g["turn"] ^= 1
+        g["events"][k].synchronize()          # the copy that last read this staging buffer
+        host = g["host"][k].numpy()
+        host[:po] = np.asarray(self.seen, dtype=np.int64).view(np.int32)
+        host[po: po + 2 * b] = np.arange(b, dtype=np.int64).view(np.int32)     # source rows
+        host[po + 2 * b: po + 3 * b] = starts
+        host[po + 3 * b: po + 4 * b] = 1
+        grid = host[po + 4 * b: lo].reshape(b, mbg)
+        grid[:] = 0
+        for i, r in enumerate(self.reqs):
+            t = kv.tables[r]
+            grid[i, : len(t)] = t.as_array() if hasattr(t, "as_array") else t
+        host[lo: lo + b] = [s0 + 1 for s0 in starts]
+        g["meta"].copy_(g["host"][k], non_blocking=True)
+        g["events"][k].record()
+        g["ids"].copy_(ids.view(b, 1), non_blocking=True)
+        for r, s0 in zip(self.reqs, starts):
+            kv.seq_used[r] = s0 + 1
+
+    def _graph_capture(self) -> None:
+        b, mbg, po, lo = self._graph_layout()
+        dev = self.kv.kv.device
+        meta = torch.zeros(lo + b, dtype=torch.int32, device=dev)
+        plan = (meta[po:lo], b, mbg, b)
+        st = _Step(self.cache, 1, None, plan, meta[lo:lo + b], meta[po + 4 * b: lo].view(b, mbg), None, True)
+        ids = torch.zeros(b, 1, dtype=torch.long, device=dev)
+        pos = meta[:po].view(torch.int64).view(b, 1)
+        # the attention workspace exists before the capture (it is cached beyond the graph)
+        lib = _hip.lib()
+        nbytes = int(lib.actkv_paged_attention_workspace_size(1, b, 1, self.n_q, self.n_kv, self.head_dim, mbg,
+                                                              self.kv.block_size))
+        if nbytes:
+            _hip.scratch(dev, "attention", nbytes)
+        torch.cuda.synchronize(dev)
+        self.cache.static_step = st
+        graph = torch.cuda.CUDAGraph()
+        try:
+            with torch.cuda.graph(graph):
+                logits = self.model(input_ids=ids, past_key_values=self.cache, position_ids=pos,
+                                    attention_mask={"full_attention": None}, use_cache=True,
+                                    logits_to_keep=1).logits[:, -1]
+        finally:
+            self.cache.static_step = None
+            self.cache.step = None
+        host = [torch.empty(lo + b, dtype=torch.int32, pin_memory=True) for _ in range(2)]
+        self._g = {"graph": graph, "logits": logits, "step": st, "meta": meta, "ids": ids, "host": host,
+                   "events": [torch.cuda.Event() for _ in range(2)], "turn": 0}
+        for e in self._g["events"]:
+            e.record()
+
+    @torch.no_grad()
+    def _graph_decode(self, ids: torch.Tensor) -> torch.Tensor:
+        if self._g is None:
+            self._graph_capture()
+        self._graph_prepare(ids)
+        self._g["graph"].replay()
+        self.seen = [s + 1 for s in self.seen]
+        return self._g["logits"].clone()
+
     def decode(self, ids: torch.Tensor, in_action=None) -> torch.Tensor:
         """ids [B]: one new token per sequence.  in_action [B] bools (or one bool): which of the
         tokens belong to an action region and are scored at the round's end."""
@@ -332,9 +429,16 @@ class PagedSession:
         flags = [bool(in_action)] * b if in_action is None or isinstance(in_action, bool) else \
             [bool(x) for x in in_action]
         capture = any(flags)
-        logits = self._forward(ids.view(b, 1), capture)
-        if capture:
+        # graph replay once an eager decode step has run (libraries set up their kernels for
+        # the decode shapes on first use, which a capture must not do)
+        if self.graph and self._eager_decodes >= 1 and self._graph_fits():
+            logits = self._graph_decode(ids)
+            st = self._g["step"]
+        else:
+            logits = self._forward(ids.view(b, 1), capture)
+            self._eager_decodes += 1
             st = self.cache.step
+        if capture:
             q = torch.stack([st.q[l][:, 0] for l in range(self.n_layers)])          # [L, B, Hq, D]
             lse = torch.stack([st.lse[l][:, 0] for l in range(self.n_layers)])      # [L, B, Hq]
             lim = [self.kv.seq_used[r] for r in self.reqs]

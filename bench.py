@@ -88,6 +88,8 @@ def parse(argv=None):
     ap.add_argument("--serve-steps", type=int, default=48, help="decode steps per round")
     ap.add_argument("--serve-action", type=int, default=24, help="action tokens at the end of each round")
     ap.add_argument("--serve-budget", type=int, default=4096)
+    ap.add_argument("--serve-eager", action="store_true",
+                    help="serve: launch every decode step from Python instead of replaying a HIP graph")
     args = ap.parse_args(argv)
     if args.steps < 1:
         ap.error("--steps must be at least 1 (the timed steps)")
@@ -574,7 +576,7 @@ def run_serve(args, dev):
         torch.set_default_dtype(prev)
     n_params = sum(p.numel() for p in model.parameters())
     max_tokens = P + rounds * steps + 64
-    sess = PagedSession(model, B, max_tokens=max_tokens, block_size=args.block_size)
+    sess = PagedSession(model, B, max_tokens=max_tokens, block_size=args.block_size, graph=not args.serve_eager)
     g = torch.Generator(device=dev).manual_seed(args.seed + 1)
     prompt = torch.randint(0, cfg.vocab_size, (B, P), generator=g, device=dev)
     gc.collect()
@@ -622,6 +624,7 @@ def run_serve(args, dev):
                                f"greedy decode steps, last {n_act} of each round scored as the action region, "
                                f"budget {budget}, LRFU decay 0.5 top-p 0.9, block {args.block_size}",
                    "parallelism": "single-gpu"},
+        "decode_launch": "python (eager)" if args.serve_eager else "hip graph replay",
         "prefill_tokens_per_s": round(B * P / prefill_s, 1),
         "decode_ms_per_step_median": round(statistics.median(p["decode_ms_per_step"] for p in per_round), 2),
         "end_round_us_median": round(statistics.median(p["end_round_us"] for p in per_round), 1),

@@ -172,3 +172,45 @@ def test_decoding_after_compression_equals_index_select_cache():
     want = _reference_run(model, "eager", prompts, toks, keep=keep, more=more)
     for b in range(B):
         torch.testing.assert_close(got[b], want[b], rtol=1e-4, atol=1e-4)
+
+
+def test_graph_decode_equals_eager_decode_across_a_compaction():
+    """Decode steps replayed from a captured HIP graph give the eager session's logits and
+    cache, step after step (the eager session's own launches run between the replays), also
+    after a round's compaction rewrites the block tables."""
+    model = _model(torch.bfloat16, layers=3)
+    B, n0, steps = 3, 150, 14
+    prompts, toks = _tokens(B, n0, steps, seed=9)
+    order = torch.randperm(B * 40, generator=torch.Generator().manual_seed(10)).tolist()
+    sessions = []
+    for graph in (False, True):
+        s = PagedSession(model, B, max_tokens=512, num_blocks=B * 40, graph=graph)
+        s.kv.free = list(order)
+        s.prefill(prompts[:, :4], protected=True)
+        s.prefill(prompts[:, 4:])
+        s.begin_round()
+        sessions.append(s)
+    eager, graph = sessions
+
+    def step(t, act):
+        le = eager.decode(t, in_action=act)
+        lg = graph.decode(t, in_action=act)
+        torch.testing.assert_close(lg.float(), le.float(), rtol=0, atol=2e-2)
+        assert torch.equal(lg.argmax(-1), le.argmax(-1))
+
+    for j in range(8):
+        step(toks[j], j >= 5)
+    assert graph._g is not None                     # replays after the first eager step
+    for a, b in zip(eager._act, graph._act):        # the action tokens' q and lse
+        torch.testing.assert_close(b[1], a[1], rtol=0, atol=1e-3)
+    pe = eager.end_round(budget=[60, 70, 80])
+    pg = graph.end_round(budget=[60, 70, 80])
+    assert [p.tolist() for p in pe] == [p.tolist() for p in pg]
+    eager.begin_round()
+    graph.begin_round()
+    for j in range(8, steps):
+        step(toks[j], False)
+    torch.cuda.synchronize()
+    assert eager.kv.free == graph.kv.free and eager.kv.seq_used == graph.kv.seq_used
+    assert {r: list(t) for r, t in eager.kv.tables.items()} == {r: list(t) for r, t in graph.kv.tables.items()}
+    torch.testing.assert_close(graph.kv.kv.float(), eager.kv.kv.float(), rtol=0, atol=2e-2)

@@ -58,7 +58,8 @@ struct AttnArgs {
   float scale;
   // token-range split (flash-decoding): chunks per sequence, tokens per chunk, and
   // the partial results of each chunk (row-major [pair][row][chunk])
-  int nchunk, tpc, rows_pad;
+  // dyn: the decode kernel's interleaved split (attn_dec_chunks); tpc is then unused
+  int nchunk, tpc, rows_pad, dyn;
   float *ws_o;   // [pairs][rows_pad][nchunk][128]: unnormalised sum p v
   float *ws_ml;  // [pairs][rows_pad][nchunk][2]: running max (log2 units), sum p
 };
@@ -86,6 +87,61 @@ __device__ __forceinline__ int attn_phys(const AttnArgs &a, int r, int b) {
   return (p >= 0 && p < a.num_blocks) ? (int)p : -1;
 }
 
+// ------------------------------------------------------------------ chunk merge
+// One wave merges the nc token chunks of query row `id` (pair * rows_pad + row) and writes
+// out and lse, two dims per lane:
+//   M = max_c m_c, w_c = 2^(m_c - M), out = sum_c w_c O_c / sum_c w_c l_c,
+//   lse = ln 2 * (M + log2 sum_c w_c l_c)
+// Lane c reads chunk c's (max, sum) for up to 64 chunks at a time (a butterfly max and sum);
+// the O rows of the first 16 chunks are loaded in the same round trip (rows past nc are
+// never written: their terms are selected away, not multiplied by zero), later ones after.
+__device__ __forceinline__ void attn_merge_row(const AttnArgs &a, int64_t id, int nc, int64_t o_off,
+                                               int64_t lse_off, int lane) {
+  constexpr int PRE = 16;
+  const float *ml = a.ws_ml + id * a.nchunk * 2;
+  const float *wo = a.ws_o + id * a.nchunk * 128;
+  float pre0[PRE], pre1[PRE];
+#pragma unroll
+  for (int j = 0; j < PRE; ++j) {
+    const int jc = max(0, min(j, nc - 1));  // an in-bounds row: the workspace holds nchunk >= max(nc, 1)
+    pre0[j] = wo[(int64_t)jc * 128 + lane];
+    pre1[j] = wo[(int64_t)jc * 128 + 64 + lane];
+  }
+  float M = -INFINITY;
+  for (int c = lane; c < nc; c += 64) M = fmaxf(M, ml[2 * c]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+  const float Ms = M == -INFINITY ? 0.f : M;
+  float Lsum = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int c0 = 0; c0 < nc; c0 += 64) {
+    const int c = c0 + lane;
+    const float w = c < nc ? __builtin_amdgcn_exp2f(ml[2 * c] - Ms) : 0.f;
+    float lw = c < nc ? w * ml[2 * c + 1] : 0.f;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) lw += __shfl_xor(lw, o, 64);
+    Lsum += lw;
+    if (c0 == 0) {
+#pragma unroll
+      for (int j = 0; j < PRE; ++j) {
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
+        o0 += j < nc ? wj * pre0[j] : 0.f;
+        o1 += j < nc ? wj * pre1[j] : 0.f;
+      }
+    }
+    const float *wc = wo + (int64_t)c0 * 128;
+    for (int j = c0 == 0 ? PRE : 0; j < min(64, nc - c0); ++j) {
+      const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
+      o0 += wj * wc[j * 128 + lane];
+      o1 += wj * wc[j * 128 + 64 + lane];
+    }
+  }
+  const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
+  float *op = a.out + o_off;
+  op[lane] = o0 * inv;
+  op[64 + lane] = o1 * inv;
+  if (lane == 0) a.lse[lse_off] = Lsum > 0.f ? (M + __log2f(Lsum)) * 0.6931471805599453f : -INFINITY;
+}
+
 // ------------------------------------------------------------------ MFMA path
 // ------------------------------------------------------------------ decode path
 // A pair whose query rows fit one 32-row tile (N*G <= 32: decode steps and short
@@ -97,9 +153,22 @@ __device__ __forceinline__ int attn_phys(const AttnArgs &a, int r, int b) {
 // chunks XOR-swizzled by token (conflict-free A-operand reads); V rows are stored the
 // same way and read back with ds_read_b64_tr_b16, which hands each lane four
 // consecutive tokens of one dim: the V^T operand with no register transpose.  The
-// waves' (max, sum, O) merge through LDS at the end.
+// waves' (max, sum, O) merge through LDS at the end.  The pairs are split into chunks
+// for one round of workgroups (chunks = 2 * CUs / pairs, slices interleaved over their
+// waves), merged by the combine launch; a sequence whose slices fit one chunk is written
+// here directly.
 constexpr int DW = 4;                         // waves per decode workgroup
 constexpr int DREG = 2 * 32 * 256;            // LDS bytes per wave: K rows, then V rows
+
+// The decode split (a.dyn): slice s of a pair (tokens 32s .. 32s + 31) goes to wave
+// s mod (nchunk * DW), that is wave s mod DW of chunk (s / DW) mod nchunk.  A wave's first
+// slice is known at launch, so its block-table entries load together with seq_used; every
+// request spreads over the chunks in proportion to its length; and the split depends on
+// the chunk count only, not on the block table's width.  Chunks holding slices of a
+// sequence of S tokens:
+__device__ __forceinline__ int attn_dec_chunks(const AttnArgs &a, int S) {
+  return min(a.nchunk, (((S + 31) >> 5) + DW - 1) / DW);
+}
 
 // 16-byte chunk slot of chunk c of token t is c ^ dswz(t).  Distinct slots, so no LDS bank
 // conflicts, for: 16 consecutive tokens at one chunk (K A-operand reads); four consecutive
@@ -124,9 +193,11 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
   const int nq = attn_nq(a, r);
   if (nq * G <= 0) return;
   const int S_all = attn_seq_len(a, r);
-  if (a.nchunk > 1 && chunk * a.tpc >= S_all) return;
-  const int c_begin = min(chunk * a.tpc, S_all);
-  const int S = min(S_all - c_begin, a.tpc);
+  // chunks holding slices; with one (or none: chunk 0 then writes the empty result) the
+  // workgroup writes the result itself, with more the combine launch merges them
+  const int nact = a.nchunk > 1 ? max(attn_dec_chunks(a, S_all), 1) : 1;
+  if (chunk >= nact) return;
+  const int S = S_all;
   const int BS = a.BS;
 
   const int tid = threadIdx.x;
@@ -135,7 +206,7 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
   const int row = lcol;
   const int n = row / G, g = row % G;
   const bool valid = n < nq;
-  const int lim = valid ? min(max(attn_lim(a, r, n, S_all) - c_begin, 0), S) : 0;
+  const int lim = valid ? min(max(attn_lim(a, r, n, S_all), 0), S) : 0;
   const int lim_m = valid ? lim : 0x7fffffff;
   int s_end = S;
   if constexpr (CAUSAL) {
@@ -145,7 +216,7 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
     __syncthreads();
     s_end = wg_lim;
   }
-  const int nsl = (s_end + 31) / 32;  // slices of the chunk anyone needs
+  const int nsl = (s_end + 31) / 32;  // slices of the pair anyone needs
 
   V8 qf[8];
   {
@@ -163,11 +234,10 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
   unsigned char *kl = reg_lds[wave];
   unsigned char *vl = kl + 32 * 256;
 
-  // block-table entry of token group i (tokens 4i..4i+3) of slice s: lane i < 8 holds it
-  auto slice_phys = [&](int s) {
-    const int t = s * 32 + 4 * (lane & 7);
-    return (s < nsl && t < S) ? attn_phys(a, r, (c_begin + t) >> bs_shift) : -1;
-  };
+  // block-table entry of token group i (tokens 4i..4i+3) of slice s: lane i < 8 holds it.
+  // Entries past the sequence are read too (bounds-checked by attn_phys): load_slice skips
+  // their tokens, and the first slices' entries need not wait for seq_used.
+  auto slice_phys = [&](int s) { return attn_phys(a, r, (s * 32 + 4 * (lane & 7)) >> bs_shift); };
   // lane: token rows 4i + lane/16 (i = 0..7), 16-byte chunk lane%16, of K and V
   uint4 kr[8], vr[8];
   auto load_slice = [&](int s, int ph) {
@@ -177,7 +247,7 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
       const int pb = __builtin_amdgcn_readlane(ph, i);
       const int t = s * 32 + 4 * i + (lane >> 4);
       const bool ok = pb >= 0 && t < S;
-      const int64_t off = ok ? (int64_t)pb * a.kv_sb + (int64_t)((c_begin + t) & (BS - 1)) * a.kv_ss + c * 8 : 0;
+      const int64_t off = ok ? (int64_t)pb * a.kv_sb + (int64_t)(t & (BS - 1)) * a.kv_ss + c * 8 : 0;
       kr[i] = *(const uint4 *)(kplane + off);
       vr[i] = *(const uint4 *)(vplane + off);
       if (!ok) { kr[i] = make_uint4(0, 0, 0, 0); vr[i] = make_uint4(0, 0, 0, 0); }
@@ -281,13 +351,14 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
   };
 
   // ---- the wave's slices: wave, wave + DW, ...; table entries two slices ahead
-  int s = wave;
-  int ph_next = slice_phys(s + DW);
+  const int step = a.nchunk * DW;
+  int s = chunk * DW + wave;
+  int ph_next = slice_phys(s + step);
   if (s < nsl) load_slice(s, slice_phys(s));
-  for (; s < nsl; s += DW) {
+  for (; s < nsl; s += step) {
     store_slice();
-    if (s + DW < nsl) load_slice(s + DW, ph_next);
-    ph_next = slice_phys(s + 2 * DW);
+    if (s + step < nsl) load_slice(s + step, ph_next);
+    ph_next = slice_phys(s + 2 * step);
     compute(s);
   }
 
@@ -302,56 +373,56 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
     if (lh == 0) { mrg_ml[wave][lcol][0] = m2; mrg_ml[wave][lcol][1] = lsum; }
   }
   __syncthreads();
-  if (wave != 0) return;
-  float M = -INFINITY;
+  if (wave == 0) {
+    float M = -INFINITY;
 #pragma unroll
-  for (int w = 0; w < DW; ++w) M = fmaxf(M, mrg_ml[w][lcol][0]);
-  const float Ms = M == -INFINITY ? 0.f : M;
-  float Lsum = 0.f, wgt[DW];
+    for (int w = 0; w < DW; ++w) M = fmaxf(M, mrg_ml[w][lcol][0]);
+    const float Ms = M == -INFINITY ? 0.f : M;
+    float Lsum = 0.f, wgt[DW];
 #pragma unroll
-  for (int w = 0; w < DW; ++w) {
-    wgt[w] = __builtin_amdgcn_exp2f(mrg_ml[w][lcol][0] - Ms);
-    Lsum += wgt[w] * mrg_ml[w][lcol][1];
-  }
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      float o = 0.f;
-#pragma unroll
-      for (int w = 0; w < DW; ++w) o += wgt[w] * ((const float *)reg_lds[w])[(dt * 16 + e) * 64 + lane];
-      oacc[dt][e] = o;
+    for (int w = 0; w < DW; ++w) {
+      wgt[w] = __builtin_amdgcn_exp2f(mrg_ml[w][lcol][0] - Ms);
+      Lsum += wgt[w] * mrg_ml[w][lcol][1];
     }
-  if (!valid) return;
-  if (a.nchunk > 1) {
-    const int64_t pr = ((int64_t)p * a.rows_pad + row) * a.nchunk + chunk;
-    float *wo = a.ws_o + pr * 128;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        f32x4 v;
-        v[0] = oacc[dt][4 * i]; v[1] = oacc[dt][4 * i + 1]; v[2] = oacc[dt][4 * i + 2]; v[3] = oacc[dt][4 * i + 3];
-        *(f32x4 *)(wo + 32 * dt + 8 * i + 4 * lh) = v;
+      for (int e = 0; e < 16; ++e) {
+        float o = 0.f;
+#pragma unroll
+        for (int w = 0; w < DW; ++w) o += wgt[w] * ((const float *)reg_lds[w])[(dt * 16 + e) * 64 + lane];
+        oacc[dt][e] = o;
       }
-    if (lh == 0) { a.ws_ml[pr * 2] = M; a.ws_ml[pr * 2 + 1] = Lsum; }
-    return;
-  }
-  const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
-  float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * G + g) * a.o_sh;
+    if (valid && nact > 1) {  // this chunk's partial result
+      const int64_t pr = ((int64_t)p * a.rows_pad + row) * a.nchunk + chunk;
+      float *wo = a.ws_o + pr * 128;
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int d0 = 32 * dt + 8 * i + 4 * lh;
-      f32x4 v;
-      v[0] = oacc[dt][4 * i] * inv; v[1] = oacc[dt][4 * i + 1] * inv;
-      v[2] = oacc[dt][4 * i + 2] * inv; v[3] = oacc[dt][4 * i + 3] * inv;
-      *(f32x4 *)(op + d0) = v;
+        for (int i = 0; i < 4; ++i) {
+          f32x4 v;
+          v[0] = oacc[dt][4 * i]; v[1] = oacc[dt][4 * i + 1]; v[2] = oacc[dt][4 * i + 2]; v[3] = oacc[dt][4 * i + 3];
+          *(f32x4 *)(wo + 32 * dt + 8 * i + 4 * lh) = v;
+        }
+      if (lh == 0) { a.ws_ml[pr * 2] = M; a.ws_ml[pr * 2 + 1] = Lsum; }
+    } else if (valid) {       // the whole sequence: the result
+      const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
+      float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * G + g) * a.o_sh;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d0 = 32 * dt + 8 * i + 4 * lh;
+          f32x4 v;
+          v[0] = oacc[dt][4 * i] * inv; v[1] = oacc[dt][4 * i + 1] * inv;
+          v[2] = oacc[dt][4 * i + 2] * inv; v[3] = oacc[dt][4 * i + 3] * inv;
+          *(f32x4 *)(op + d0) = v;
+        }
+      if (lh == 0)
+        a.lse[(int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * G + g] =
+            Lsum > 0.f ? (M + __log2f(Lsum)) * 0.6931471805599453f : -INFINITY;
     }
-  if (lh == 0)
-    a.lse[(int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * G + g] =
-        Lsum > 0.f ? (M + __log2f(Lsum)) * 0.6931471805599453f : -INFINITY;
+  }
 }
 
 // ------------------------------------------------------------------ ring path
@@ -718,9 +789,9 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
 }
 
 // ------------------------------------------------------------------ split combine
-// grid ceil(pairs*rows_pad/4), 256 threads: one wave per (pair, row), two dims per lane.
-//   M = max_c m_c, w_c = 2^(m_c - M), out = sum_c w_c O_c / sum_c w_c l_c,
-//   lse = ln 2 * (M + log2 sum_c w_c l_c)
+// grid ceil(pairs*rows_pad/4), 256 threads: one wave per (pair, row) merging with
+// attn_merge_row.  The decode kernel (a.dyn) wrote a sequence of at most one chunk's tokens
+// itself: those rows are skipped.
 __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int pairs) {
   const int64_t id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (id >= (int64_t)pairs * a.rows_pad) return;
@@ -731,28 +802,13 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int pairs
   const int l = p / (a.Hkv * a.R);
   const int n = row / a.G, g = row % a.G;
   if (n >= attn_nq(a, r)) return;
-  const float *ml = a.ws_ml + id * a.nchunk * 2;
-  const float *wo = a.ws_o + id * a.nchunk * 128;
   // chunks past the sequence were never written: they hold no token of this row
   const int S_all = attn_seq_len(a, r);
-  const int nc = min(a.nchunk, (S_all + a.tpc - 1) / a.tpc);
-  float M = -INFINITY;
-  for (int c = 0; c < nc; ++c) M = fmaxf(M, ml[2 * c]);
-  const float Ms = M == -INFINITY ? 0.f : M;
-  float Lsum = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int c = 0; c < nc; ++c) {
-    const float w = __builtin_amdgcn_exp2f(ml[2 * c] - Ms);
-    Lsum += w * ml[2 * c + 1];
-    o0 += w * wo[c * 128 + lane];
-    o1 += w * wo[c * 128 + 64 + lane];
-  }
-  const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
-  float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * a.G + g) * a.o_sh;
-  op[lane] = o0 * inv;
-  op[64 + lane] = o1 * inv;
-  if (lane == 0)
-    a.lse[(int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * a.G + g] =
-        Lsum > 0.f ? (M + __log2f(Lsum)) * 0.6931471805599453f : -INFINITY;
+  const int nc = a.dyn ? attn_dec_chunks(a, S_all) : min(a.nchunk, (S_all + a.tpc - 1) / a.tpc);
+  if (a.dyn && nc <= 1) return;
+  attn_merge_row(a, id, nc,
+                 (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * a.G + g) * a.o_sh,
+                 (int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * a.G + g, lane);
 }
 
 // ------------------------------------------------------------------ generic path
@@ -853,22 +909,32 @@ static RingCfg ring_cfg(int rtiles) {
 // resident workgroups (1 per CU at 8 waves, 2 at 4, 4 at 1-2 waves: the LDS stage
 // buffers), chunks of at least 256 tokens, a whole number of stages each.
 struct AttnSplit { int nchunk, tpc, rows_pad, ngroups; };
-static AttnSplit attn_split(int pairs, int N, int G, int span) {
+// compute units of the current device (256 on MI355X), queried once per device
+static int device_cus() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+static AttnSplit attn_split(int pairs, int N, int G, int span, int cus) {
   AttnSplit sp;
   const int rtiles = (N * G + 31) / 32;
   if (rtiles == 1) {
-    // decode kernel: DW waves per (pair, chunk), two workgroups per CU; about two rounds
-    // of them, each wave taking at least two 32-token slices of its chunk
+    // decode kernel: DW waves per (pair, chunk) and two resident workgroups per CU, so one
+    // round of workgroups fills the chip when pairs * nchunk is about 2 * CUs.  A second,
+    // partly filled round doubles a short call's time: chunks stop there.  The slices are
+    // interleaved over the chunks (attn_dec_chunks), so nothing depends on the block
+    // table's width: the same sequences give the same bits however wide the table is.
     sp.ngroups = 1;
     sp.rows_pad = 32;
-    const int unit = DW * 32;
-    const int64_t want = 2LL * 2 * 256;
-    const int nchunk = (int)std::min<int64_t>(std::max<int64_t>(1, (want + pairs - 1) / pairs),
-                                              std::max(1, span / (2 * unit)));
-    const int tpc = ((span + nchunk - 1) / nchunk + unit - 1) / unit * unit;
-    sp.nchunk = (span + tpc - 1) / tpc;
-    sp.tpc = tpc;
-    if (sp.nchunk <= 1) { sp.nchunk = 1; sp.tpc = std::max(span, 1); }
+    sp.nchunk = std::max(1, 2 * cus / std::max(pairs, 1));
+    sp.tpc = sp.nchunk > 1 ? 0 : std::max(span, 1);
     return sp;
   }
   const RingCfg cfg = ring_cfg(rtiles);
@@ -898,13 +964,14 @@ static int launch_attn_mfma(AttnArgs a, int bs_shift, void *ws, size_t ws_bytes,
   const int pairs = a.L * a.R * a.Hkv;
   const int rtiles = (a.N * a.G + 31) / 32;
   const bool causal = a.kv_len != nullptr;
-  AttnSplit sp = attn_split(pairs, a.N, a.G, a.max_blocks * a.BS);
+  AttnSplit sp = attn_split(pairs, a.N, a.G, a.max_blocks * a.BS, device_cus());
   const size_t need = attn_ws_bytes(pairs, sp);
   if (sp.nchunk > 1 && (!ws || ws_bytes < need)) {  // no (large enough) workspace: no split
     sp.nchunk = 1;
     sp.tpc = std::max(a.max_blocks * a.BS, 1);
   }
   a.nchunk = sp.nchunk; a.tpc = sp.tpc; a.rows_pad = sp.rows_pad;
+  a.dyn = rtiles == 1 && sp.nchunk > 1;
   a.ws_o = sp.nchunk > 1 ? (float *)ws : nullptr;
   a.ws_ml = sp.nchunk > 1 ? (float *)((char *)ws + (size_t)pairs * sp.rows_pad * sp.nchunk * 128 * sizeof(float)) : nullptr;
   if (rtiles == 1) {
@@ -989,7 +1056,8 @@ extern "C" int actkv_paged_attention(
   a.lse = lse; a.lse_sl = lse_sl; a.lse_sr = lse_sr; a.lse_sn = lse_sn;
   a.L = L; a.R = R; a.N = N; a.Hq = Hq; a.Hkv = Hkv; a.D = D; a.G = Hq / Hkv; a.BS = block_size;
   a.scale = scale;
-  a.nchunk = 1; a.tpc = max_blocks * block_size; a.rows_pad = 0; a.ws_o = nullptr; a.ws_ml = nullptr;
+  a.nchunk = 1; a.tpc = max_blocks * block_size; a.rows_pad = 0; a.dyn = 0;
+  a.ws_o = nullptr; a.ws_ml = nullptr;
   const int G = a.G;
   int bs_shift = -1;
   for (int sh = 4; sh < 31; ++sh)
@@ -1025,5 +1093,5 @@ extern "C" size_t actkv_paged_attention_workspace_size(int L, int R, int N, int 
   if (D != 128 || !(G == 1 || G == 2 || G == 4)) return 0;  // the float32 path does not split
   if ((int64_t)max_blocks * block_size > 0x7fffffffLL) return 0;
   const int pairs = L * R * Hkv;
-  return attn_ws_bytes(pairs, attn_split(pairs, N, G, max_blocks * block_size));
+  return attn_ws_bytes(pairs, attn_split(pairs, N, G, max_blocks * block_size, device_cus()));
 }

@@ -391,6 +391,9 @@ def run_attn(args, dev):
     dec["one_layer_us"] = round(t_one, 1)
     dec["torch_reference_one_layer_us"] = round(t_ref, 1)
     res["decode"] = dec
+    del cache, q1, q0
+    torch.cuda.empty_cache()
+    res["decode_per_layer"] = decode_per_layer(torch, dev, args, make_cache, timed)
     res["value"] = rows["queries"]["us"]
     res["config"] = {"workload": res["queries"]["workload"], "parallelism": "single-gpu"}
     res.update(run_info(torch, dev))
@@ -400,6 +403,37 @@ def run_attn(args, dev):
         with open(args.out, "w") as f:
             f.write(line + "\n")
     return 0
+
+
+def decode_per_layer(torch, dev, args, make_cache, timed):
+    """A serving decode step's attention: batch 4, one query per request, 4400 tokens each,
+    one call per layer (the cache pointer at the layer) for all layers, captured in a HIP graph
+    as a served decode step is.  Tables 4400 tokens wide, and 8400 wide (a session sized for
+    8400 tokens whose requests hold 4400 after a compaction).  Bytes: the K and V rows read."""
+    from actkv.kernels.lse_attn import paged_decode_attention
+    L, hq, hkv, d, bs = args.layers, args.q_heads, args.kv_heads, args.head_dim, args.block_size
+    B, S = 4, 4400
+    cache = make_cache([S] * B)
+    reqs = list(range(B))
+    seq, bt = cache._device_tables(reqs)
+    q = torch.randn(L, B, hq, d, device=dev, dtype=torch.bfloat16)
+    nbytes = 2.0 * B * S * hkv * d * 2 * L
+    out = {"workload": f"{L} layers x {B} requests x {S} tokens, one query each, one call per layer, "
+                       f"replayed from a HIP graph, bf16"}
+    for name, width in (("table_4400", -(-S // bs)), ("table_8400", -(-8400 // bs))):
+        wide = torch.zeros(B, width, dtype=torch.int32, device=dev)
+        wide[:, : bt.shape[1]] = bt
+        run = lambda: [paged_decode_attention(q[l], cache.kv[l], wide, seq) for l in range(L)]
+        run()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            run()
+        us = timed(g.replay, max(args.steps, 10)) / L
+        out[name] = {"us_per_layer": round(us, 2), "GBps": round(nbytes / L / (us * 1e-6) / 1e9, 1),
+                     "frac_of_hbm_peak": round(nbytes / L / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"decode per layer, {name}: {us:.2f} us, {out[name]['GBps']} GB/s")
+    return out
 
 
 def _append_summary(per_round, L, hkv, d):

@@ -101,13 +101,16 @@ def test_all_layers_with_ragged_query_counts():
     assert torch.equal(out[:, 1, 9:].cpu(), torch.zeros(layers, n_q - 9, 32, 128))
 
 
-def test_empty_sequence_gives_minus_inf_and_zero():
-    cache = _cache([40, 0], seed=9)
+@pytest.mark.parametrize("n0,n_q", [(40, 2), (3000, 2), (3000, 40)])
+def test_empty_sequence_gives_minus_inf_and_zero(n0, n_q):
+    """An empty request next to another: one pass, the decode kernel's split, the ring
+    kernel's split (its combine merges no chunk for the empty request)."""
+    cache = _cache([n0, 0], seed=9)
     assert cache.seq_used[1] == 0
-    q = torch.randn(2, 2, 32, 128).to(torch.bfloat16)
+    q = torch.randn(2, n_q, 32, 128).to(torch.bfloat16)
     out, lse = cache.decode_attention([0, 1], q.cuda())
     assert torch.isinf(lse[1]).all() and (lse[1] < 0).all()
-    assert torch.equal(out[1].cpu(), torch.zeros(2, 32, 128))
+    assert torch.equal(out[1].cpu(), torch.zeros(n_q, 32, 128))
     want_out, want_lse = _oracle(cache, [0], q[:1], 0)
     torch.testing.assert_close(lse[:1].cpu(), want_lse, rtol=0, atol=1e-4)
 
@@ -219,3 +222,51 @@ def test_block_table_window_refill(monkeypatch):
     want_out, want_lse = _oracle(cache, [0], q, 0)
     torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
     torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-2)
+
+
+@pytest.mark.parametrize("lens,hq,hkv,widen,causal", [
+    ([4400, 3000, 1, 4400], 32, 8, 2, False),        # table twice as wide as the sequences
+    ([4400, 2900], 32, 8, 3, True),                  # the same, causal limits
+    ([20000], 4, 1, 1, False),                       # one pair: 125 chunks, merged 64 at a time
+    ([50 + 7 * i for i in range(70)], 4, 1, 2, False),  # 70 requests: the longest is found across lanes
+])
+def test_decode_split_follows_the_longest_sequence(lens, hq, hkv, widen, causal):
+    """The decode kernel's chunk length is the longest sequence of the call over the chunk
+    count, whatever the block table's width (a wider table gives the same bits), and the
+    combine merges any number of chunks."""
+    from actkv import _hip
+    bs = 16
+    cache = _cache(lens, hkv=hkv, bs=bs, seed=len(lens) + hq)
+    reqs = list(range(len(lens)))
+    seq, bt = cache._device_tables(reqs)
+    wide = torch.zeros(len(lens), bt.shape[1] * widen, dtype=torch.int32, device="cuda")
+    wide[:, : bt.shape[1]] = bt
+    assert _hip.lib().actkv_paged_attention_workspace_size(1, len(lens), 1, hq, hkv, 128, wide.shape[1], bs) > 0
+    g = torch.Generator().manual_seed(len(lens))
+    q = torch.randn(len(lens), 1, hq, 128, generator=g).to(torch.bfloat16)
+    kv_len = None
+    if causal:
+        kv_len = torch.stack([torch.randint(1, S + 1, (1,), generator=g) for S in lens]).to(torch.int32)
+    out, lse = paged_decode_attention(q.cuda(), cache.kv[0], wide, seq,
+                                      kv_len=None if kv_len is None else kv_len.cuda())
+    want_out, want_lse = _oracle(cache, reqs, q, 0, kv_len=None if kv_len is None else kv_len.tolist())
+    torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
+    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-2)
+    # the split does not depend on the table's width: the tight table gives the same bits
+    tight_out, tight_lse = paged_decode_attention(q.cuda(), cache.kv[0], bt, seq,
+                                                  kv_len=None if kv_len is None else kv_len.cuda())
+    assert torch.equal(tight_out, out) and torch.equal(tight_lse, lse)
+
+
+def test_split_calls_of_different_shapes_share_the_workspace():
+    """Decode calls of different shapes, back to back on one workspace: each merges its own
+    chunks, whatever an earlier call of another shape left in the workspace."""
+    shapes = [([700, 1500], 32, 8), ([333, 1024, 17], 32, 8), ([4000], 4, 1), ([700, 1500], 32, 8)]
+    for i, (lens, hq, hkv) in enumerate(shapes):
+        cache = _cache(lens, hkv=hkv, seed=40 + i)
+        reqs = list(range(len(lens)))
+        q = torch.randn(len(lens), 1, hq, 128, generator=torch.Generator().manual_seed(i)).to(torch.bfloat16)
+        out, lse = cache.decode_attention(reqs, q.cuda())
+        want_out, want_lse = _oracle(cache, reqs, q, 0)
+        torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
+        torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-2)

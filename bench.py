@@ -233,6 +233,38 @@ def measure(w, steps, warmup):
             "step_us_sync": statistics.mean(t_sync), "wall_s_incl_restore": wall}
 
 
+def time_apply_copies(torch, w, moved, steps):
+    """apply_copies (the explicit src/dst row mover, compaction.py:79-106) on the workload's
+    cache with a plan of its compaction's size: `moved` rows of every plane (K and V of every
+    layer) from distinct source slots to distinct destination slots, the two sets disjoint as
+    plan_compaction makes them.  HIP events around back-to-back calls on the launch stream.
+    Algorithmic bytes: every moved row read and written, plus the two int64 index arrays."""
+    from actkv.kernels.compaction import apply_copies
+    kv = w.cache.kv
+    planes = kv.shape[0] * kv.shape[1]
+    flat = kv.view(planes, kv.shape[2] * kv.shape[3], kv.shape[4] * kv.shape[5])
+    slots = flat.shape[1]
+    g = torch.Generator().manual_seed(7)
+    pick = torch.randperm(slots, generator=g)[: 2 * moved]
+    src, dst = pick[:moved].to(w.dev), pick[moved:].to(w.dev)
+    apply_copies(flat, src, dst)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(w.dev)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(steps):
+        apply_copies(flat, src, dst)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / steps
+    nbytes = 2 * moved * planes * flat.shape[2] * flat.element_size() + 2 * moved * 8
+    return {"workload": f"{moved} rows x {planes} planes of {flat.shape[2] * flat.element_size()} B, "
+                        f"random disjoint source and destination slots", "us": round(us, 2),
+            "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "frac_of_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes": nbytes,
+            "kernel": "copy_slots_kernel (actkv_copy_slots)"}
+
+
 def check_step(w):
     """Run one step from a fresh copy and check it: keep mask == the oracle's keep mask on the
     GPU's own scores; survivors of layer 0 == the pre-compaction rows at perm; host lists."""
@@ -741,6 +773,9 @@ def main(argv=None):
                "step_s_extrapolated": round(c["extrapolated_step_s"], 1), "cpu_model": cpu_model(),
                "os_cpu_count": os.cpu_count()}
 
+    log("apply_copies on a plan of the compaction's size")
+    copies = time_apply_copies(torch, w, moved, max(args.steps, 5))  # rewrites rows: after every other leg
+
     result = {
         "metric": "score+compact HBM GB/s (% of 8 TB/s) and evict us/layer, Qwen3-8B shape 32k",
         "value": round(gbs, 1), "unit": "GB/s",
@@ -767,6 +802,7 @@ def main(argv=None):
                      "hbm_GBps_algorithmic": round(work["bytes_score"] / (k_us * 1e-6) / 1e9, 1)},
         "cpu_baseline": cpu,
         "single_layer": single,
+        "apply_copies": copies,
         "checks": checks,
         "wall_s_incl_restore": round(m["wall_s_incl_restore"], 3),
         **run_info(torch, dev),

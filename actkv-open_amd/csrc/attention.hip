@@ -161,11 +161,10 @@ constexpr int DW = 4;                         // waves per decode workgroup
 constexpr int DREG = 2 * 32 * 256;            // LDS bytes per wave: K rows, then V rows
 
 // The decode split (a.dyn): slice s of a pair (tokens 32s .. 32s + 31) goes to wave
-// s mod (nchunk * DW), that is wave s mod DW of chunk (s / DW) mod nchunk.  A wave's first
-// slice is known at launch, so its block-table entries load together with seq_used; every
-// request spreads over the chunks in proportion to its length; and the split depends on
-// the chunk count only, not on the block table's width.  Chunks holding slices of a
-// sequence of S tokens:
+// s mod (nchunk * DW), that is wave s mod DW of chunk (s / DW) mod nchunk.  A wave's slices
+// depend on the chunk count only (no other request's length is read); every request spreads
+// over the chunks in proportion to its length; and nothing depends on the block table's
+// width.  Chunks holding slices of a sequence of S tokens:
 __device__ __forceinline__ int attn_dec_chunks(const AttnArgs &a, int S) {
   return min(a.nchunk, (((S + 31) >> 5) + DW - 1) / DW);
 }
@@ -236,7 +235,7 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
 
   // block-table entry of token group i (tokens 4i..4i+3) of slice s: lane i < 8 holds it.
   // Entries past the sequence are read too (bounds-checked by attn_phys): load_slice skips
-  // their tokens, and the first slices' entries need not wait for seq_used.
+  // their tokens.
   auto slice_phys = [&](int s) { return attn_phys(a, r, (s * 32 + 4 * (lane & 7)) >> bs_shift); };
   // lane: token rows 4i + lane/16 (i = 0..7), 16-byte chunk lane%16, of K and V
   uint4 kr[8], vr[8];

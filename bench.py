@@ -238,8 +238,12 @@ def time_apply_copies(torch, w, moved, steps):
     cache with a plan of its compaction's size: `moved` rows of every plane (K and V of every
     layer) from distinct source slots to distinct destination slots, the two sets disjoint as
     plan_compaction makes them.  HIP events around back-to-back calls on the launch stream.
-    Algorithmic bytes: every moved row read and written, plus the two int64 index arrays."""
-    from actkv.kernels.compaction import apply_copies
+    Algorithmic bytes: every moved row read and written, plus the two int64 index arrays.
+    Beside it, on the same GPU: the reference's torch formulations of the same move
+    (apply_copies_ref, compaction.py:72-74) and of its gather baseline (gather_compaction,
+    compaction.py:109-114: the survivors of a keep set of the compaction's size copied into a
+    fresh buffer)."""
+    from actkv.kernels.compaction import apply_copies, apply_copies_ref, gather_compaction
     kv = w.cache.kv
     planes = kv.shape[0] * kv.shape[1]
     flat = kv.view(planes, kv.shape[2] * kv.shape[3], kv.shape[4] * kv.shape[5])
@@ -247,22 +251,33 @@ def time_apply_copies(torch, w, moved, steps):
     g = torch.Generator().manual_seed(7)
     pick = torch.randperm(slots, generator=g)[: 2 * moved]
     src, dst = pick[:moved].to(w.dev), pick[moved:].to(w.dev)
-    apply_copies(flat, src, dst)
-    torch.cuda.synchronize()
     stream = torch.cuda.current_stream(w.dev)
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
-    for _ in range(steps):
-        apply_copies(flat, src, dst)
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    us = ev0.elapsed_time(ev1) * 1e3 / steps
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        for _ in range(reps):
+            fn()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) * 1e3 / reps
+
+    us = timed(lambda: apply_copies(flat, src, dst), steps)
+    us_ref = timed(lambda: apply_copies_ref(flat, src, dst), max(steps // 4, 3))
+    keep = torch.sort(torch.randperm(slots, generator=g)[: w.budget + w.args.sinks]).values.to(w.dev)
+    us_gather = timed(lambda: gather_compaction(flat, keep), max(steps // 4, 3))
     nbytes = 2 * moved * planes * flat.shape[2] * flat.element_size() + 2 * moved * 8
+    gbytes = 2 * keep.numel() * planes * flat.shape[2] * flat.element_size() + keep.numel() * 8
     return {"workload": f"{moved} rows x {planes} planes of {flat.shape[2] * flat.element_size()} B, "
                         f"random disjoint source and destination slots", "us": round(us, 2),
             "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
             "frac_of_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes": nbytes,
-            "kernel": "copy_slots_kernel (actkv_copy_slots)"}
+            "kernel": "copy_slots_kernel (actkv_copy_slots)",
+            "apply_copies_ref_torch_us": round(us_ref, 2),
+            "gather_compaction_torch": {"kept_rows": keep.numel(), "us": round(us_gather, 2),
+                                        "GBps": round(gbytes / (us_gather * 1e-6) / 1e9, 1)}}
 
 
 def check_step(w):

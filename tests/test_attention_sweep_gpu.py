@@ -1,0 +1,66 @@
+"""Paged attention with the LSE by-product over a seeded random sweep of shapes, against the
+oracle's float64 restatement of lse_attn.py:42-60.
+
+Each case draws: 1-5 requests of 0-6000 tokens, the GQA shape (Hq/Hkv 32/8, 16/8, 8/8,
+16/4), 1-80 queries per request (so both matrix-core kernels: one 32-row tile or several),
+bf16 or fp16, block 16/32/64, causal limits or none, a partial query count per request or
+none, and a block table as wide as the longest request or twice that.  Tolerances as in
+test_attention_gpu.py: lse atol 1e-4; out atol 1e-2 (bf16) / 2e-3 (fp16), the rounding of
+the probabilities to the cache dtype for the P.V product.
+"""
+import math
+import random
+
+import pytest
+import torch
+
+from actkv.kernels.lse_attn import paged_decode_attention
+from actkv.paged import PagedKVCache
+from oracle import reference as ref
+
+pytestmark = pytest.mark.gpu
+
+GQA = [(32, 8), (16, 8), (8, 8), (16, 4)]
+
+
+def _case(seed):
+    rnd = random.Random(seed)
+    n_req = rnd.randint(1, 5)
+    lens = [rnd.choice([0, rnd.randint(1, 200), rnd.randint(200, 6000)]) for _ in range(n_req)]
+    if max(lens) == 0:
+        lens[0] = rnd.randint(1, 3000)
+    hq, hkv = rnd.choice(GQA)
+    return dict(lens=lens, hq=hq, hkv=hkv, n_q=rnd.choice([1, rnd.randint(2, 8), rnd.randint(9, 80)]),
+                dtype=rnd.choice([torch.bfloat16, torch.float16]), bs=rnd.choice([16, 32, 64]),
+                causal=rnd.random() < 0.5, partial=rnd.random() < 0.3, widen=rnd.choice([1, 2]))
+
+
+@pytest.mark.parametrize("seed", range(64))
+def test_random_shapes_match_the_oracle(seed):
+    c = _case(seed)
+    lens, hq, hkv, n_q, dtype, bs = c["lens"], c["hq"], c["hkv"], c["n_q"], c["dtype"], c["bs"]
+    print(f"case {seed}: {c}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    nb = sum(math.ceil(n / bs) for n in lens) + 3
+    cache = PagedKVCache(nb, bs, hkv, 128, n_layers=1, dtype=dtype, device="cuda")
+    cache.free = torch.randperm(nb, generator=g).tolist()
+    for r, n in enumerate(lens):
+        cache.append(r, torch.randn(1, n, hkv, 128, generator=g).to(dtype).cuda(),
+                     torch.randn(1, n, hkv, 128, generator=g).to(dtype).cuda())
+    reqs = list(range(len(lens)))
+    seq, bt = cache._device_tables(reqs)
+    table = torch.zeros(len(lens), bt.shape[1] * c["widen"], dtype=torch.int32, device="cuda")
+    table[:, : bt.shape[1]] = bt
+    q = torch.randn(len(lens), n_q, hq, 128, generator=g).to(dtype)
+    kv_len = (torch.stack([torch.randint(0, S + 4, (n_q,), generator=g) for S in lens]).to(torch.int32)
+              if c["causal"] else None)
+    n_valid = (torch.tensor([random.Random(seed + r).randint(0, n_q) for r in reqs], dtype=torch.int32)
+               if c["partial"] else None)
+    out, lse = paged_decode_attention(q.cuda(), cache.kv[0], table, seq,
+                                      kv_len=None if kv_len is None else kv_len.cuda(),
+                                      n_valid=None if n_valid is None else n_valid.cuda())
+    want_out, want_lse = ref.paged_attention(
+        q.float(), cache.kv[0].cpu().float(), [cache.tables[r] for r in reqs], [cache.seq_used[r] for r in reqs],
+        kv_len=None if kv_len is None else kv_len.tolist(), n_valid=None if n_valid is None else n_valid.tolist())
+    torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
+    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-2 if dtype == torch.bfloat16 else 2e-3)

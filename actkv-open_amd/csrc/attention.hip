@@ -154,9 +154,8 @@ __device__ __forceinline__ void attn_merge_row(const AttnArgs &a, int64_t id, in
 // same way and read back with ds_read_b64_tr_b16, which hands each lane four
 // consecutive tokens of one dim: the V^T operand with no register transpose.  The
 // waves' (max, sum, O) merge through LDS at the end.  The pairs are split into chunks
-// for one round of workgroups (chunks = 2 * CUs / pairs, slices interleaved over their
-// waves), merged by the combine launch; a sequence whose slices fit one chunk is written
-// here directly.
+// (max(8, 2 * CUs / pairs), slices interleaved over their waves: attn_split), merged by the
+// combine launch; a sequence whose slices fit one chunk is written here directly.
 constexpr int DW = 4;                         // waves per decode workgroup
 constexpr int DREG = 2 * 32 * 256;            // LDS bytes per wave: K rows, then V rows
 
@@ -926,13 +925,17 @@ static AttnSplit attn_split(int pairs, int N, int G, int span, int cus) {
   const int rtiles = (N * G + 31) / 32;
   if (rtiles == 1) {
     // decode kernel: DW waves per (pair, chunk) and two resident workgroups per CU, so one
-    // round of workgroups fills the chip when pairs * nchunk is about 2 * CUs.  A second,
-    // partly filled round doubles a short call's time: chunks stop there.  The slices are
-    // interleaved over the chunks (attn_dec_chunks), so nothing depends on the block
-    // table's width: the same sequences give the same bits however wide the table is.
+    // round of workgroups fills the chip when pairs * nchunk is about 2 * CUs.  A second
+    // round costs a short call about a third more: with few pairs the chunks stop at one
+    // round.  With many pairs there are several rounds anyway, and at least 8 chunks per
+    // pair keep the workgroups of the longest requests in a ragged batch from forming the
+    // tail (a chunk holds at least one slice per wave: attn_dec_chunks).  The slices are
+    // interleaved over the chunks, so nothing depends on the block table's width: the same
+    // sequences give the same bits however wide the table is.  Partial results are kept
+    // for the N * G rows that exist.
     sp.ngroups = 1;
-    sp.rows_pad = 32;
-    sp.nchunk = std::max(1, 2 * cus / std::max(pairs, 1));
+    sp.rows_pad = N * G;
+    sp.nchunk = std::max(8, 2 * cus / std::max(pairs, 1));
     sp.tpc = sp.nchunk > 1 ? 0 : std::max(span, 1);
     return sp;
   }

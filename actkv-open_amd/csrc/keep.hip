@@ -16,8 +16,8 @@
 // torch CPU sum order (aten SumKernel cascade_sum, pinned by the oracle tests):
 // for a reduction over n rows of a column block, the column's value is a
 // cascade of 16-row blocks (level_power 4) when the column lies in the
-// 32-column-aligned body, and the "row_sum" 4-way interleaved order for the
-// last S % 32 columns.  Division by the row count is IEEE (div_, not a
+// vectorized body (torch_body_end), and the "row_sum" 4-way interleaved order
+// for the other columns.  Division by the row count is IEEE (div_, not a
 // reciprocal multiply).
 #include "common.h"
 #include "torch_order.h"
@@ -64,7 +64,7 @@ __global__ void __launch_bounds__(REDUCE_THREADS) keep_reduce_kernel(KeepArgs a)
   if (t0 >= S) return;
   const int tok = threadIdx.x & 63, lg = threadIdx.x >> 6;
   const int t = t0 + tok;
-  const bool body = t < (S & ~31);
+  const bool body = t < torch_body_end(S);
   const ST *sbase = (const ST *)a.scores + (int64_t)r * a.s_sr;
   if (t < S) {
     for (int l = lg; l < a.L; l += REDUCE_THREADS / 64) {
@@ -126,7 +126,7 @@ __device__ __forceinline__ void hist_add_wave(uint32_t *hist, uint32_t key) {
 // reduces the heads of 4 consecutive tokens with 16-byte loads; phase 2: each of
 // the first 256 threads averages the layers of one token.  Same per-token float
 // order as keep_reduce_kernel (a 4-token quad lies wholly in or out of the
-// 32-column-aligned body).
+// body: torch_body_end is a multiple of 4).
 template <int HH>
 __global__ void __launch_bounds__(REDUCE_THREADS) keep_reduce4_kernel(KeepArgs a) {
   extern __shared__ float lvals[];  // [L][256]
@@ -136,7 +136,7 @@ __global__ void __launch_bounds__(REDUCE_THREADS) keep_reduce4_kernel(KeepArgs a
   if (t0 >= S) return;
   const int quad = threadIdx.x & 63, lg = threadIdx.x >> 6;
   const int tq = t0 + 4 * quad;
-  const bool body4 = tq < (S & ~31);
+  const bool body4 = tq < torch_body_end(S);
   const float *sbase = (const float *)a.scores + (int64_t)r * a.s_sr;
   // the quad's 4 scores of one (layer, head) row; the last quad of a sequence
   // reads only its tokens below S
@@ -177,7 +177,7 @@ __global__ void __launch_bounds__(REDUCE_THREADS) keep_reduce4_kernel(KeepArgs a
   if (threadIdx.x >= 256) return;
   const int tok = threadIdx.x;
   const int t = t0 + tok;
-  const bool body = t < (S & ~31);
+  const bool body = t < torch_body_end(S);
   uint32_t key = 0;
   const bool in = t < S;
   if (in && !is_protected(a, r, t)) {

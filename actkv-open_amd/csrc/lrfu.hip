@@ -125,7 +125,7 @@ __global__ void __launch_bounds__(LT) lrfu_update_kernel(LrfuArgs a) {
   const int tid = threadIdx.x;
 
   // ---- per-token action score and the float64 total over [P, S)
-  const int body_end = S & ~31;
+  const int body_end = torch_body_end(S);
   auto head_act = [&](int t) {
     const float *col = sbase + t;
     if (a.head_reduce == ACTKV_REDUCE_MAX) {
@@ -293,14 +293,18 @@ __global__ void __launch_bounds__(LT) lrfu_update_kernel(LrfuArgs a) {
   }
   // ---- keep-score update over [P, S)
   for_each([&](int t, float v) {
+    // two roundings, as the reference's ks.mul_(decay) then ks[hit] += act: the compiler
+    // must not fuse them into one FMA.  hipcc contracts by default, and the pragma reaches
+    // only operations written in this scope (not those inside __fmul_rn / __fadd_rn).
+#pragma clang fp contract(off)
     if (pin && pin[t]) {
       if (hit) hit[t] = 0;
       return;
     }
     const uint32_t k = __float_as_uint(v);
     const bool h = v > 0.f && (k > kthr || (k == kthr && t < cut));
-    float x = __fmul_rn(a.decay, ks[t]);
-    if (h) x = __fadd_rn(x, v);
+    float x = a.decay * ks[t];
+    if (h) x = x + v;
     ks[t] = x;
     if (hit) hit[t] = h ? 1 : 0;
   });

@@ -2,9 +2,9 @@
 // keep-mask and LRFU kernels.
 //
 // torch CPU sum order (aten SumKernel cascade_sum): for a reduction over n rows
-// of a column block, the column's value is a cascade of 16-row blocks (level
-// power 4) when the column lies in the 32-column-aligned body, and the 4-way
-// interleaved "row_sum" order for the last S % 32 columns.
+// of an S-column block, the column's value is a cascade of 16-row blocks (level
+// power 4) when the column lies in the vectorized body (torch_body_end), and the
+// 4-way interleaved "row_sum" order for the other columns.
 #pragma once
 
 #include "common.h"
@@ -52,6 +52,14 @@ __device__ __forceinline__ float ilp4_sum(F ld, int n) {
   p0 = __fadd_rn(p0, p3);
   return p0;
 }
+
+// Columns [0, torch_body_end(S)) of an S-column reduction are in the vectorized body:
+// whole 32-column blocks (four 8-lane vectors), or, in a row of 4-7 columns, one
+// 4-column block.  The rest (1-3 columns, every remainder after the 32-column blocks)
+// take row_sum.  Checked against torch 2.10's CPU mean for 1-80 columns and 2-64 rows,
+// strided and contiguous; a contiguous single column of 16 or more rows (torch's inner
+// reduction) takes another order and is not modelled.
+__device__ __forceinline__ int torch_body_end(int S) { return S >= 8 ? (S & ~31) : (S >= 4 ? 4 : 0); }
 
 template <typename F>
 __device__ __forceinline__ float torch_sum(F ld, int n, bool body) {

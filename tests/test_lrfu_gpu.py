@@ -35,6 +35,7 @@ def test_known_answers_of_the_reference():
     (36, 8, [4096], [4], 4096, "mean", 0.9),
     (1, 2, [50000], [4], 50016, "mean", 0.99),             # scores through the workspace
     (2, 8, [16384, 9000], [4, 0], 16384, "mean", 0.9),      # 16 tokens per thread in registers, full
+    (3, 8, [4, 5, 6, 7, 3, 1, 9], [0, 1, 0, 2, 0, 0, 0], 40, "mean", 0.9),  # torch's 4-column body of 4-7 tokens
 ])
 def test_lrfu_update_matches_the_oracle(L, H, seqs, prots, W, reduce, p):
     g = torch.Generator().manual_seed(sum(seqs))
@@ -159,3 +160,34 @@ def test_agent_loop_rounds_match_the_oracle():
         for r in reqs:
             if r in model.pinned:
                 assert np.array_equal(cache.pinned[r].cpu().numpy(), model.pinned[r])
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_lrfu_update_random_shapes_match_the_oracle(seed):
+    """Seeded random shapes: 1-5 requests of 1-20000 tokens (some past the 16-per-thread
+    register path), 1-4 layers, 1-8 heads, table width up to twice the longest request,
+    mean or max head reduction, top_p 0.5-0.99, decay 0.3-0.9, protected prefixes, inactive
+    requests, score vectors with zeros and exact ties; keep scores and hits bit-exact."""
+    import random
+    rnd = random.Random(3000 + seed)
+    R = rnd.randint(1, 5)
+    seqs = [rnd.choice([rnd.randint(1, 64), rnd.randint(64, 4096), rnd.randint(4096, 20000)]) for _ in range(R)]
+    L, H = rnd.randint(1, 4), rnd.choice([1, 2, 4, 8])
+    W = max(seqs) + rnd.choice([0, rnd.randint(1, max(seqs))])
+    prots = [rnd.randint(0, min(s, 8)) for s in seqs]
+    active = [rnd.random() < 0.8 for _ in seqs]
+    reduce, p, decay = rnd.choice(["mean", "max"]), rnd.choice([0.5, 0.9, 0.99]), rnd.choice([0.3, 0.5, 0.9])
+    g = torch.Generator().manual_seed(seed)
+    scores = (torch.rand(L, R, H, W, generator=g) ** 8) * 1e-2
+    scores[torch.rand(L, R, H, W, generator=g) < 0.05] = 0.0
+    scores[torch.rand(L, R, H, W, generator=g) < 0.02] = 1e-3          # exact ties
+    ks0 = torch.rand(L, R, W, generator=g) * 1e-3
+    ks = ks0.clone().cuda()
+    hits = lrfu_update(scores.cuda(), ks, seqs, prots, active, decay, p, reduce, return_hits=True)
+    ks_o = ks0.clone()
+    for r in range(R):
+        act = ref.paged_lrfu_act(scores[:, r], seqs[r], reduce)
+        h_o = ref.paged_lrfu_update(ks_o[:, r], act, seqs[r], prots[r], decay, p, active[r], stable=True,
+                                    total64=True)
+        assert torch.equal(hits[:, r, prots[r]:seqs[r]].cpu(), h_o[:, prots[r]:]), f"request {r}: hits differ"
+    assert torch.equal(ks.cpu(), ks_o), "keep scores differ"

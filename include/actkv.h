@@ -114,9 +114,10 @@ int actkv_copy_slots(void *kv_flat, int64_t planes, int64_t stride_plane_bytes,
  *   s[t] = mean_l( reduce_h scores[l,r,h,t] )      reduce = mean | max
  *
  * with the float32 summation order of torch's CPU `mean` (a cascade of
- * 16-row blocks; the last S%32 columns use its 4-way interleaved order) and a
- * correctly rounded division, so s is bit-identical to the reference on the
- * same scores.  keep = protected  OR  the k = clamp(budget[r], 0, #unprotected)
+ * 16-row blocks over its vectorized columns: whole 32-column blocks, or the
+ * first 4 columns of a 4-7-column row; its 4-way interleaved order for the
+ * others) and a correctly rounded division, so s is bit-identical to the
+ * reference on the same scores.  keep = protected  OR  the k = clamp(budget[r], 0, #unprotected)
  * largest s among unprotected tokens; among equal scores at the boundary the
  * lower index wins.  protected is a per-request count of leading tokens
  * (protected_count) or a bool mask (protected_mask, row stride pm_sr); exactly

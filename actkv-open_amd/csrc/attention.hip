@@ -929,13 +929,15 @@ static AttnSplit attn_split(int pairs, int N, int G, int span, int cus) {
     // round costs a short call about a third more: with few pairs the chunks stop at one
     // round.  With many pairs there are several rounds anyway, and at least 8 chunks per
     // pair keep the workgroups of the longest requests in a ragged batch from forming the
-    // tail (a chunk holds at least one slice per wave: attn_dec_chunks).  The slices are
-    // interleaved over the chunks, so nothing depends on the block table's width: the same
-    // sequences give the same bits however wide the table is.  Partial results are kept
-    // for the N * G rows that exist.
+    // tail (a chunk holds at least one slice per wave: attn_dec_chunks).  From 16 rounds of
+    // pairs on, the tail is a small part of the call and one pass per pair keeps the
+    // workspace from growing with the batch (8 chunks of 256k pairs would want gigabytes).
+    // The slices are interleaved over the chunks, so nothing depends on the block table's
+    // width: the same sequences give the same bits however wide the table is.  Partial
+    // results are kept for the N * G rows that exist.
     sp.ngroups = 1;
     sp.rows_pad = N * G;
-    sp.nchunk = std::max(8, 2 * cus / std::max(pairs, 1));
+    sp.nchunk = pairs >= 32 * cus ? 1 : std::max(8, 2 * cus / std::max(pairs, 1));
     sp.tpc = sp.nchunk > 1 ? 0 : std::max(span, 1);
     return sp;
   }

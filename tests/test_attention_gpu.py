@@ -270,3 +270,21 @@ def test_split_calls_of_different_shapes_share_the_workspace():
         want_out, want_lse = _oracle(cache, reqs, q, 0)
         torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
         torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-2)
+
+
+def test_many_pairs_take_one_pass_without_a_workspace():
+    """36 layers x 29 requests x 8 KV heads = 8352 pairs, 16 rounds of resident workgroups:
+    the decode kernel attends each pair in one pass and asks for no workspace; the first and
+    last layers match the oracle."""
+    from actkv import _hip
+    layers, lens = 36, [40 + 7 * i for i in range(29)]
+    cache = _cache(lens, layers=layers, seed=31)
+    reqs = list(range(len(lens)))
+    width = max(len(cache.tables[r]) for r in reqs)
+    assert _hip.lib().actkv_paged_attention_workspace_size(layers, len(lens), 1, 32, 8, 128, width, 16) == 0
+    q = torch.randn(layers, len(lens), 1, 32, 128, generator=torch.Generator().manual_seed(32)).to(torch.bfloat16)
+    out, lse = cache.decode_attention(reqs, q.cuda(), layer=None)
+    for l in (0, layers - 1):
+        want_out, want_lse = _oracle(cache, reqs, q[l], l)
+        torch.testing.assert_close(lse[l].cpu(), want_lse, rtol=0, atol=1e-4)
+        torch.testing.assert_close(out[l].cpu(), want_out, rtol=0, atol=1e-2)

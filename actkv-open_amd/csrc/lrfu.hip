@@ -96,11 +96,38 @@ __device__ int crossing_bin(const uint32_t *cnt, const double *sum, int nb, doub
   return b;
 }
 
-// grid (L, R), LT threads.  KMAX > 0: thread i keeps the action scores of its tokens
-// t = P + i + j*LT (j < KMAX, segments of up to KMAX*LT tokens) in registers, computed once
-// with all their loads in flight, and every later pass walks the registers (the passes
-// over a workspace waited on one load per token in turn); KMAX = 0: the scores go through
-// the workspace (longer segments).  Measured on the agent-loop rounds: 91 us against 103 us
+// Per-token action score of a segment: the head reduction (mean in torch's CPU float32
+// order, or max) of the scores at token t.
+__device__ __forceinline__ float lrfu_head_act(const LrfuArgs &a, const float *sbase, int t, int body_end) {
+  const float *col = sbase + t;
+  if (a.head_reduce == ACTKV_REDUCE_MAX) {
+    float v = col[0];
+    for (int hh = 1; hh < a.H; ++hh) v = nanmax(v, col[(int64_t)hh * a.s_sh]);
+    return v;
+  }
+  auto ld = [&](int hh) { return col[(int64_t)hh * a.s_sh]; };
+  return __fdiv_rn(torch_sum(ld, a.H, t < body_end), (float)a.H);
+}
+
+// grid (ceil(max_seq / 256), L, R), 256 threads: act[t] of every segment's tokens [P, S), one
+// token per thread.  It runs ahead of lrfu_update_kernel so that the head reduction's reads
+// (Hkv scores per token) are spread over the whole chip instead of one workgroup per segment.
+__global__ void __launch_bounds__(256) lrfu_act_kernel(LrfuArgs a) {
+  const int l = blockIdx.y, r = blockIdx.z;
+  const int S = min(max(a.seq_used[r], 0), a.max_seq);
+  const int P = a.prot ? min(max(a.prot[r], 0), S) : 0;
+  const int t = P + blockIdx.x * 256 + threadIdx.x;
+  if (t >= S) return;
+  const float *sbase = a.scores + (int64_t)l * a.s_sl + (int64_t)r * a.s_sr;
+  a.act[((int64_t)l * a.R + r) * a.act_sr + t] = lrfu_head_act(a, sbase, t, torch_body_end(S));
+}
+
+// grid (L, R), LT threads, after lrfu_act_kernel has written the action scores to the
+// workspace.  KMAX > 0: thread i keeps the action scores of its tokens t = P + i + j*LT
+// (j < KMAX, segments of up to KMAX*LT tokens) in registers, loaded once with all their
+// loads in flight, and every later pass walks the registers (the passes over a workspace
+// wait on one load per token in turn); KMAX = 0: every pass reads the workspace (longer
+// segments).  Measured on the agent-loop rounds: 91 us against 103 us
 // at ~15k tokens with KMAX 16; KMAX 24 (121 registers) took 150 us at ~17k tokens, slower
 // than the workspace path, and 32 spills.
 template <int KMAX>
@@ -119,30 +146,18 @@ __global__ void __launch_bounds__(LT) lrfu_update_kernel(LrfuArgs a) {
   const uint8_t *pin = a.pmask ? a.pmask + (int64_t)r * a.pm_sr : nullptr;
   const bool active = a.active ? a.active[r] != 0 : true;
   float *act = a.act + ((int64_t)l * a.R + r) * a.act_sr;
-  const float *sbase = a.scores + (int64_t)l * a.s_sl + (int64_t)r * a.s_sr;
   float *ks = a.ks + (int64_t)l * a.ks_sl + (int64_t)r * a.ks_sr;
   uint8_t *hit = a.hit ? a.hit + (int64_t)l * a.hit_sl + (int64_t)r * a.hit_sr : nullptr;
   const int tid = threadIdx.x;
 
-  // ---- per-token action score and the float64 total over [P, S)
-  const int body_end = torch_body_end(S);
-  auto head_act = [&](int t) {
-    const float *col = sbase + t;
-    if (a.head_reduce == ACTKV_REDUCE_MAX) {
-      float v = col[0];
-      for (int hh = 1; hh < a.H; ++hh) v = nanmax(v, col[(int64_t)hh * a.s_sh]);
-      return v;
-    }
-    auto ld = [&](int hh) { return col[(int64_t)hh * a.s_sh]; };
-    return __fdiv_rn(torch_sum(ld, a.H, t < body_end), (float)a.H);
-  };
+  // ---- per-token action score (from lrfu_act_kernel) and the float64 total over [P, S)
   float vals[REG ? KMAX : 1];
   double part = 0.0;
   if constexpr (REG) {
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) {
       const int t = P + tid + j * LT;
-      vals[j] = t < S ? head_act(t) : 0.f;
+      vals[j] = t < S ? act[t] : 0.f;
     }
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) {
@@ -151,8 +166,7 @@ __global__ void __launch_bounds__(LT) lrfu_update_kernel(LrfuArgs a) {
     }
   } else {
     for (int t = P + tid; t < S; t += LT) {
-      const float v = head_act(t);
-      act[t] = v;
+      const float v = act[t];
       if (!pin || !pin[t]) part += (double)v;
     }
   }
@@ -348,6 +362,9 @@ extern "C" int actkv_lrfu_update(const float *scores, int64_t s_sl, int64_t s_sr
   // tokens per segment past the protected prefix are at most max_seq
   const dim3 grid(L, R);
   hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(lrfu_act_kernel, dim3((max_seq + 255) / 256, L, R), dim3(256), 0, st, a);
+  int rc = actkv_check_launch();
+  if (rc) return rc;
   if (max_seq <= 16 * LT) hipLaunchKernelGGL(lrfu_update_kernel<16>, grid, dim3(LT), 0, st, a);
   else hipLaunchKernelGGL(lrfu_update_kernel<0>, grid, dim3(LT), 0, st, a);
   return actkv_check_launch();

@@ -1,7 +1,7 @@
 """CPU oracle for the ActKV eviction hot path -- TEST INFRASTRUCTURE, NOT PRODUCT CODE.
 
 A restatement of the reference's algorithm (Maurya30/actkv-open: actkv/kernels/lse_attn.py,
-actkv/kernels/compaction.py, actkv/paged.py) used only as the checker:
+actkv/kernels/compaction.py, actkv/paged.py) used only to compare and time against:
 
   * tests/ compare the HIP kernels against it on identical seeded inputs;
   * __graft_entry__.smoke() checks one small run against it;

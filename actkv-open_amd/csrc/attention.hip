@@ -154,7 +154,7 @@ __device__ __forceinline__ void attn_merge_row(const AttnArgs &a, int64_t id, in
 // same way and read back with ds_read_b64_tr_b16, which hands each lane four
 // consecutive tokens of one dim: the V^T operand with no register transpose.  The
 // waves' (max, sum, O) merge through LDS at the end.  The pairs are split into chunks
-// (max(8, 2 * CUs / pairs), slices interleaved over their waves: attn_split), merged by the
+// (max(8, 1.5 * CUs / pairs), slices interleaved over their waves: attn_split), merged by the
 // combine launch; a sequence whose slices fit one chunk is written here directly.
 constexpr int DW = 4;                         // waves per decode workgroup
 constexpr int DREG = 2 * 32 * 256;            // LDS bytes per wave: K rows, then V rows
@@ -924,10 +924,10 @@ static AttnSplit attn_split(int pairs, int N, int G, int span, int cus) {
   AttnSplit sp;
   const int rtiles = (N * G + 31) / 32;
   if (rtiles == 1) {
-    // decode kernel: DW waves per (pair, chunk) and two resident workgroups per CU, so one
-    // round of workgroups fills the chip when pairs * nchunk is about 2 * CUs.  A second
-    // round costs a short call about a third more: with few pairs the chunks stop at one
-    // round.  With many pairs there are several rounds anyway, and at least 8 chunks per
+    // decode kernel: DW waves per (pair, chunk), two resident workgroups per CU.  With few
+    // pairs the chunks stop at about 1.5 workgroups per CU, within one round: a served decode
+    // step's per-layer call (32 pairs x 4400 tokens) took 27.7 / 28.1 / 26.1 / 28.3 / 31.7 /
+    // 33.7 us with 8 / 10 / 12 / 16 / 20 / 24 chunks, and 37 us with a second round (32).  With many pairs there are several rounds anyway, and at least 8 chunks per
     // pair keep the workgroups of the longest requests in a ragged batch from forming the
     // tail (a chunk holds at least one slice per wave: attn_dec_chunks).  From 16 rounds of
     // pairs on, the tail is a small part of the call and one pass per pair keeps the
@@ -937,7 +937,7 @@ static AttnSplit attn_split(int pairs, int N, int G, int span, int cus) {
     // results are kept for the N * G rows that exist.
     sp.ngroups = 1;
     sp.rows_pad = N * G;
-    sp.nchunk = pairs >= 32 * cus ? 1 : std::max(8, 2 * cus / std::max(pairs, 1));
+    sp.nchunk = pairs >= 32 * cus ? 1 : std::max(8, 3 * cus / 2 / std::max(pairs, 1));
     sp.tpc = sp.nchunk > 1 ? 0 : std::max(span, 1);
     return sp;
   }

@@ -110,6 +110,11 @@ def available() -> bool:
     return os.path.exists(LIB_PATH) and torch.cuda.is_available()
 
 
+def debug() -> bool:
+    """ACTKV_DEBUG=1 turns on host-side checks that read kernel reports back (they synchronise)."""
+    return os.environ.get("ACTKV_DEBUG", "0") not in ("", "0")
+
+
 def check(rc: int, what: str) -> None:
     if rc != 0:
         raise RuntimeError(f"{what} failed: {lib().actkv_error_string(rc).decode()}")

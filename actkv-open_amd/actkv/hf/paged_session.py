@@ -209,15 +209,14 @@ class PagedHFCache(Cache):
         elif st.n != n:
             raise RuntimeError("layers of one forward pass wrote different token counts")
         _tls.step = st
-        if self.kv.kv.device.type != "cuda":
-            # a CPU-resident cache (host-side use): the same rows written with torch
-            flat = self.kv.kv[layer].view(2, -1, hkv, d)
-            for i, r in enumerate(self.reqs):
-                slots = self.kv.slot_map(r, st.starts[i] + n)[st.starts[i]:]
-                flat[0, slots] = key_states[i].transpose(0, 1).to(flat.dtype)
-                flat[1, slots] = value_states[i].transpose(0, 1).to(flat.dtype)
-            st.written += 1
-            return
+        self._store(layer, st, key_states, value_states)
+        st.written += 1
+
+    def _store(self, layer: int, st: "_Step", key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        """The step's new rows of one layer into the paged cache: one actkv_append launch
+        (GPU caches only; there is no CPU path)."""
+        _hip.require_gpu("PagedHFCache", self.kv.kv)
+        b, hkv, n, d = key_states.shape
         # [B, Hkv, n, D] -> [B, n, Hkv, D] contiguous: request r's tokens are rows r*n .. r*n + n - 1
         k = key_states.transpose(1, 2)
         v = value_states.transpose(1, 2)
@@ -229,7 +228,6 @@ class PagedHFCache(Cache):
             st.launch.append(layer, k, v)
         else:   # other source dtypes: the cache's general path converts them first
             self.kv._append_launch(st.plan, k.view(1, b * n, hkv, d), v.view(1, b * n, hkv, d), layer=layer)
-        st.written += 1
 
 
 def paged_attention_forward(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):

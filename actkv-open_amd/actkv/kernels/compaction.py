@@ -1,16 +1,11 @@
 """In-place KV cache compaction on a paged layout (ActKV Algorithm 4), on gfx950.
 
-Drop-in for the reference module actkv/kernels/compaction.py.  Token eviction leaves holes
-scattered over pages; the survivors are moved with conflict-free copies:
-
-    X     = ceil(B / block_size)              blocks needed after compaction
-    start = (Y - X) * block_size              Y = blocks used before compaction
-    end   = start + B
-    dst   = evicted slots inside [start, end)
-    src   = kept slots outside [start, end)
-
-src and dst are disjoint, so every copy can run in parallel in one pass with no scratch
-buffer.  Afterwards the request's first Y - X logical blocks are free.
+Drop-in for the reference module actkv/kernels/compaction.py.  A request of S tokens holds
+Y = ceil(S / block_size) blocks; B survivors need X = ceil(B / block_size).  They end up in
+the logical window [start, start + B) with start = (Y - X) * block_size: each hole of the
+window (a non-kept position, ascending) receives the next survivor from outside the window
+(ascending), so sources and destinations never overlap and every row move is independent of
+the others.  The first Y - X logical blocks are then empty and go back to the allocator.
 
 `plan_compaction` and `apply_copies` run HIP kernels of libactkv_hip.so (the planner is the
 same kernel PagedKVCache.compact fuses with the moves, run with its copy phase off).  There
@@ -90,11 +85,13 @@ def plan_compaction(keep_mask: torch.Tensor, seq_used: int, block_table_row: tor
 
 
 def apply_copies_ref(kv_flat: torch.Tensor, src: torch.Tensor, dst: torch.Tensor) -> None:
-    """kv_flat [N, slots, H*D]; disjoint src/dst, so a single vectorized copy is safe.
+    """kv_flat [N, slots, H*D]: row dst[i] of every plane receives row src[i], in torch.
+    src and dst are disjoint, so reading every source before writing is the same as moving
+    the rows one by one.
 
     Reference formulation: actkv/kernels/compaction.py:72-74.
     """
-    kv_flat[:, dst] = kv_flat[:, src]
+    kv_flat.index_copy_(1, dst.to(kv_flat.device), kv_flat.index_select(1, src.to(kv_flat.device)))
 
 
 def apply_copies(kv_flat: torch.Tensor, src: torch.Tensor, dst: torch.Tensor) -> None:
@@ -119,8 +116,9 @@ def apply_copies(kv_flat: torch.Tensor, src: torch.Tensor, dst: torch.Tensor) ->
 
 
 def gather_compaction(kv_flat: torch.Tensor, keep_slots: torch.Tensor) -> torch.Tensor:
-    """Gather-based baseline (paged R-KV style): survivors go into a fresh contiguous buffer.
+    """Gather-based baseline (paged R-KV style): the survivors' rows of every plane copied into
+    a fresh contiguous buffer [N, len(keep_slots), H*D].
 
     Reference formulation: actkv/kernels/compaction.py:109-114 (benchmark comparison only).
     """
-    return kv_flat[:, keep_slots].clone()
+    return kv_flat.index_select(1, keep_slots.to(kv_flat.device))

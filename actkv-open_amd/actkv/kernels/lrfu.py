@@ -115,11 +115,15 @@ class PagedLRFU:
         dev = cache.kv.device
         L, R, H = cache.n_layers, len(self.reqs), cache.n_kv_heads
         self.max_tokens = max_tokens
-        self.ks = torch.zeros(L, R, max_tokens, dtype=torch.float32, device=dev)
+        # per-token buffers span whole blocks: cal_attn writes every slot of a request's last
+        # block, so its output must be as wide as the block table covers (lse_attn.py:139-142)
+        width = -(-max_tokens // cache.block_size) * cache.block_size
+        self.width = width
+        self.ks = torch.zeros(L, R, width, dtype=torch.float32, device=dev)
         self._ks_alt = torch.zeros_like(self.ks)
-        self.scores = torch.zeros(L, R, H, max_tokens, dtype=torch.float32, device=dev)
+        self.scores = torch.zeros(L, R, H, width, dtype=torch.float32, device=dev)
         self.n_seen = torch.zeros(R, dtype=torch.int32, device=dev)
-        self.pins = torch.zeros(R, max_tokens, dtype=torch.bool, device=dev)
+        self.pins = torch.zeros(R, width, dtype=torch.bool, device=dev)
         self._pins_alt = torch.zeros_like(self.pins)
         self.pin_counts = None           # host counts once the batch has been evicted
 
@@ -166,7 +170,7 @@ class PagedLRFU:
         rc = _hip.lib().actkv_gather_tokens(
             self.ks.data_ptr(), self.ks.stride(0), self.ks.stride(1),
             self._ks_alt.data_ptr(), self._ks_alt.stride(0), self._ks_alt.stride(1),
-            L, R, self.max_tokens, perm.data_ptr(), perm.stride(0), kept_dev.data_ptr(), _hip.stream(dev))
+            L, R, self.width, perm.data_ptr(), perm.stride(0), kept_dev.data_ptr(), _hip.stream(dev))
         _hip.check(rc, "actkv_gather_tokens")
         self.ks, self._ks_alt = self._ks_alt, self.ks
         self.pins, self._pins_alt = self._pins_alt, self.pins

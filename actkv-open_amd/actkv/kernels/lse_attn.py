@@ -43,53 +43,57 @@ HAS_TRITON = HAS_KERNELS
 def gather_kv(kv: torch.Tensor, block_table: torch.Tensor, seq_used: int, row: int):
     """Contiguous K, V [S, H, D] for one request (what a gather-based approach materializes).
 
-    Reference: actkv/kernels/lse_attn.py:32-39.
+    Token t of the request sits in slot block_table[row, t // bs] * bs + t % bs of either
+    plane.  Reference: actkv/kernels/lse_attn.py:32-39.
     """
     bs = kv.shape[2]
-    n_blocks = math.ceil(seq_used / bs)
-    blocks = block_table[row, :n_blocks].long()
-    k = kv[0, blocks].reshape(-1, kv.shape[3], kv.shape[4])[:seq_used]
-    v = kv[1, blocks].reshape(-1, kv.shape[3], kv.shape[4])[:seq_used]
-    return k, v
+    t = torch.arange(seq_used, device=kv.device)
+    slots = block_table[row].to(device=kv.device, dtype=torch.long)[t // bs] * bs + t % bs
+    planes = kv.reshape(2, -1, kv.shape[3], kv.shape[4])
+    return planes[0].index_select(0, slots), planes[1].index_select(0, slots)
+
+
+def _group_logits(q_r: torch.Tensor, k: torch.Tensor, scale: float) -> torch.Tensor:
+    """scale * q . k for one request, grouped by KV head: q_r [Hq, D], k [S, Hkv, D] ->
+    [Hkv, G, S] float32 (query head h*G + g reads KV head h)."""
+    hkv = k.shape[1]
+    qg = q_r.float().reshape(hkv, -1, q_r.shape[-1])                 # [Hkv, G, D]
+    return torch.matmul(qg, k.float().permute(1, 2, 0)) * scale      # [Hkv, G, S]
 
 
 def paged_decode_attention_ref(q, kv, block_table, seq_used, scale=None):
-    """Plain decode attention over a paged cache. Returns (out [R,Hq,D], lse [R,Hq]).
+    """Plain decode attention over a paged cache. Returns (out [R,Hq,D], lse [R,Hq]), float32.
 
-    Reference: actkv/kernels/lse_attn.py:42-60 (stands in for the paged FlashAttention
-    backend whose LSE by-product Algorithm 3 consumes).
+    lse[r, h] = logsumexp_t scale * q[r, h] . k_t and out = softmax @ V over the request's
+    tokens.  Reference: actkv/kernels/lse_attn.py:42-60 (stands in for the paged
+    FlashAttention backend whose LSE by-product Algorithm 3 consumes).
     """
     r_n, hq, d = q.shape
-    hkv = kv.shape[3]
-    g = hq // hkv
-    scale = scale if scale is not None else d ** -0.5
-    out = torch.empty_like(q, dtype=torch.float32)
+    scale = d ** -0.5 if scale is None else scale
+    out = torch.empty(r_n, hq, d, dtype=torch.float32, device=q.device)
     lse = torch.empty(r_n, hq, dtype=torch.float32, device=q.device)
     for r in range(r_n):
         k, v = gather_kv(kv, block_table, int(seq_used[r]), r)
-        k = k.float().repeat_interleave(g, dim=1)
-        v = v.float().repeat_interleave(g, dim=1)
-        logits = torch.einsum("hd,shd->hs", q[r].float(), k) * scale
-        lse[r] = torch.logsumexp(logits, -1)
-        out[r] = torch.einsum("hs,shd->hd", torch.softmax(logits, -1), v)
+        logits = _group_logits(q[r], k, scale)                        # [Hkv, G, S]
+        lse[r] = torch.logsumexp(logits, -1).reshape(hq)
+        probs = torch.softmax(logits, -1)
+        out[r] = torch.matmul(probs, v.float().transpose(0, 1)).reshape(hq, d)
     return out, lse
 
 
 def action_scores_ref(q, kv, block_table, seq_used, lse, out, n_seen, scale=None):
-    """One action-query fold per request in torch. Reference: lse_attn.py:63-78."""
+    """One action-query fold per request in torch (Algorithm 3): p = max over the GQA group of
+    exp(scale * q . k - lse), folded into the running mean out += (p - out) / (n_seen + 1),
+    then n_seen += 1.  Reference: lse_attn.py:63-78."""
     r_n, hq, d = q.shape
-    hkv = kv.shape[3]
-    g = hq // hkv
-    scale = scale if scale is not None else d ** -0.5
+    scale = d ** -0.5 if scale is None else scale
     for r in range(r_n):
         s = int(seq_used[r])
         k, _ = gather_kv(kv, block_table, s, r)
-        k = k.float().repeat_interleave(g, dim=1)
-        logits = torch.einsum("hd,shd->hs", q[r].float(), k) * scale
-        p = torch.exp(logits - lse[r].unsqueeze(-1))
-        p = p.view(hkv, g, s).amax(1)
-        n = float(n_seen[r])
-        out[r, :, :s] += (p - out[r, :, :s]) / (n + 1.0)
+        logits = _group_logits(q[r], k, scale)                        # [Hkv, G, S]
+        p = torch.exp(logits - lse[r].reshape(logits.shape[0], -1, 1)).amax(1)
+        cur = out[r, :, :s]
+        cur += (p - cur) / (float(n_seen[r]) + 1.0)
     n_seen += 1
     return out
 

@@ -24,7 +24,7 @@ import torch
 
 from . import _hip
 from .kernels.compaction import keep_words, upload_i32
-from .kernels.lse_attn import action_scores, paged_decode_attention, paged_decode_attention_ref
+from .kernels.lse_attn import action_scores, paged_decode_attention
 
 
 class OutOfBlocks(RuntimeError):
@@ -161,6 +161,40 @@ def keep_mask_from_scores(scores: torch.Tensor, seq_used: int, budget: int,
     return keep[0, :seq_used]
 
 
+def _check_compaction(reqs, seqs, kept, block_size, bits, counts, src, dst) -> None:
+    """Debug-mode check of one actkv_compact launch (synchronises): the kernel's report
+    {B, M, drop, X} per request must equal the host's counts (reference compaction.py:48-52,
+    :61) and the plan's source and destination slots must be distinct and disjoint
+    (compaction.py:3-13), which is what makes the in-place moves order-free."""
+    rep = counts.cpu().numpy()
+    words = bits.cpu().numpy().astype(np.uint32)
+    src_h, dst_h = src.cpu().numpy(), dst.cpu().numpy()
+    for i, r in enumerate(reqs):
+        b, m, drop, x = (int(v) for v in rep[i])
+        if b == -1:
+            raise RuntimeError(f"actkv_compact: request {r} keeps more tokens than the launch was sized for")
+        if b == -2:
+            raise RuntimeError(f"actkv_compact: request {r} holds more tokens than the launch's max_seq")
+        s = seqs[i]
+        y = -(-s // block_size)
+        mask = np.unpackbits(words[i].view(np.uint8), bitorder="little")[: y * block_size].astype(bool)
+        if mask[s:].any():
+            raise RuntimeError(f"actkv_compact: request {r} has keep bits past its {s} tokens")
+        want_x = -(-kept[i] // block_size)
+        start = (y - want_x) * block_size
+        want_m = int(mask[:start].sum()) + int(mask[start + kept[i]:].sum())
+        if (b, m, drop, x) != (kept[i], want_m, y - want_x, want_x) or int(mask.sum()) != kept[i]:
+            raise RuntimeError(f"actkv_compact: request {r}: device reports B={b} M={m} drop={drop} X={x}, "
+                               f"host expects B={kept[i]} M={want_m} drop={y - want_x} X={want_x} "
+                               f"(keep bits hold {int(mask.sum())})")
+        ps, pd = src_h[i, :m], dst_h[i, :m]
+        if (ps < 0).any() or (pd < 0).any():
+            raise RuntimeError(f"actkv_compact: request {r}: a move outside the block pool")
+        if np.unique(ps).size != m or np.unique(pd).size != m or np.intersect1d(ps, pd).size:
+            raise RuntimeError(f"actkv_compact: request {r}: source and destination slots are not "
+                               "distinct and disjoint")
+
+
 class PagedKVCache:
     def __init__(self, num_blocks: int, block_size: int, n_kv_heads: int, head_dim: int,
                  n_layers: int = 1, dtype=torch.float16, device="cpu"):
@@ -200,17 +234,11 @@ class PagedKVCache:
         On a GPU cache one actkv_append launch writes every layer's K and V rows (converted to
         the cache dtype); the blocks come from the host free stack first, as in the reference.
         Reference: actkv/paged.py:76-84."""
+        _hip.require_gpu("PagedKVCache.append", self.kv)
         n = k.shape[1]
         start = self.seq_used.get(req, 0)
         self._ensure(req, start + n)
-        if self.kv.device.type == "cuda":
-            self._append_device([req], [start], [n], k, v)
-        else:
-            # a CPU-resident cache (host-side allocator use): the same copy in torch
-            slots = self.slot_map(req, start + n)[start:]
-            flat = self.kv.view(self.n_layers, 2, -1, self.n_kv_heads, self.head_dim)
-            flat[:, 0, slots] = k.to(device=self.kv.device, dtype=self.kv.dtype)
-            flat[:, 1, slots] = v.to(device=self.kv.device, dtype=self.kv.dtype)
+        self._append_device([req], [start], [n], k, v)
         self.seq_used[req] = start + n
 
     def append_batch(self, reqs, k: torch.Tensor, v: torch.Tensor, counts=None) -> None:
@@ -304,11 +332,8 @@ class PagedKVCache:
         """Physical slot of each of the first n logical positions (int64 [n]); on a GPU cache
         computed by actkv_slot_map from the request's device block table.
         Reference: actkv/paged.py:93-97."""
+        _hip.require_gpu("PagedKVCache.slot_map", self.kv)
         n = self.seq_used[req] if n is None else n
-        if self.kv.device.type != "cuda":
-            table = torch.tensor(self.tables[req], dtype=torch.long, device=self.device)
-            pos = torch.arange(n, device=self.device)
-            return table[pos // self.block_size] * self.block_size + pos % self.block_size
         table = self.tables[req]
         if n < 0 or n > len(table) * self.block_size:
             raise IndexError(f"slot_map: {n} positions, the table covers {len(table) * self.block_size}")
@@ -407,6 +432,9 @@ class PagedKVCache:
         kept counts; then the host allocator updates in request order (sequential semantics).
         pinned_in [R, >=S] bool or pin_count [R] int32 (device) gives the pinned tokens;
         pin_out (optional, bool [R, >=max(kept)]) receives the survivors' pins.
+        The kernel always reports each request's {B, M, drop, X} into a device buffer; with
+        ACTKV_DEBUG=1 in the environment that report and the plan are read back and checked
+        against the host's counts (one synchronisation per call).
         Returns perm [R, max(kept)] int64 and pinned_out [R, max(kept)] bool (or None)."""
         dev = self.kv.device
         bs = self.block_size
@@ -419,6 +447,12 @@ class PagedKVCache:
         perm = torch.empty(r_n, bmax, dtype=torch.int64, device=dev)
         if pin_out is None and (pinned_in is not None or pin_count is not None):
             pin_out = torch.empty(r_n, bmax, dtype=torch.bool, device=dev)
+        counts = _hip.scratch(dev, "compact_counts", 16 * r_n)
+        debug = _hip.debug()
+        if debug:
+            smax = max(max(seqs), 1)
+            src = torch.full((r_n, smax), -1, dtype=torch.int64, device=dev)
+            dst = torch.full((r_n, smax), -1, dtype=torch.int64, device=dev)
         es = self.kv.element_size()
         row = self.n_kv_heads * self.head_dim
         flat = self.kv.view(self.n_layers * 2, -1, row)
@@ -428,9 +462,13 @@ class PagedKVCache:
             bt_dev.data_ptr(), mb, bs,
             perm.data_ptr(), bmax, _hip.ptr(pinned_in), 0 if pinned_in is None else pinned_in.stride(0),
             _hip.ptr(pin_count), _hip.ptr(pin_out), bmax if pin_out is None else pin_out.stride(0),
-            None, 0, None, 0, None, None, 0, None,
+            None, 0, None, 0, _hip.ptr(src) if debug else None, _hip.ptr(dst) if debug else None,
+            src.shape[1] if debug else 0, counts.data_ptr(),
             1, max(seqs), max(kept), _hip.stream(dev))
         _hip.check(rc, "actkv_compact")
+        if debug:
+            _check_compaction(reqs, seqs, kept, bs, bits, counts.view(torch.int32)[: 4 * r_n].view(r_n, 4),
+                              src, dst)
         for i, r in enumerate(reqs):
             drop = ys[i] - math.ceil(kept[i] / bs)
             table = self.tables[r]
@@ -482,10 +520,13 @@ class PagedKVCache:
         list ends in the same order).  scores: a list with one [S]/[Hkv, S]/[L, Hkv, S] tensor
         per request, or one tensor [..., R, Hkv, W] (leading dims are layers), e.g. the
         [L, R, Hkv, W] output of a multi-layer cal_attn.  budget / protected: an int for every
-        request or one per request.
+        request or one per request.  Each request may appear once (ValueError otherwise).
+        head_reduce is checked once a request is over its budget (ValueError), as the
+        reference checks it in keep_mask_from_scores after the within-budget return.
         """
-        if head_reduce not in _REDUCE:
-            raise ValueError(head_reduce)
+        reqs = list(reqs)
+        if len(set(reqs)) != len(reqs):
+            raise ValueError("evict_batch: each request once")
         r_n = len(reqs)
         budgets = list(budget) if isinstance(budget, (list, tuple)) else [budget] * r_n
         prots = list(protected) if isinstance(protected, (list, tuple)) else [protected] * r_n
@@ -510,6 +551,10 @@ class PagedKVCache:
                 kept.append(cnt + max(budgets[i], 0))
                 counts.append(cnt)
                 continue
+            if pinned.numel() > n:
+                # the reference's torch.cat with a negative-size pad raises here (paged.py:151)
+                raise RuntimeError(f"evict: request {req} has {pinned.numel()} pinned flags for {n} tokens "
+                                   "(a compact() since the last evict() left them unmapped)")
             cnt = self._pinned_count(req, pinned)
             if pinned.numel() < n:                      # tokens appended since
                 pinned = torch.cat([pinned, pinned.new_zeros(n - pinned.numel())])
@@ -524,6 +569,8 @@ class PagedKVCache:
             counts.append(cnt)
         if not active:
             return out
+        if head_reduce not in _REDUCE:
+            raise ValueError(head_reduce)
         _hip.require_gpu("PagedKVCache.evict", self.kv)
         a_reqs = [reqs[i] for i in active]
         seqs = [self.seq_used[r] for r in a_reqs]

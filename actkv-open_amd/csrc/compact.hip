@@ -163,7 +163,13 @@ __global__ void __launch_bounds__(CT) compact_kernel(CompactArgs a) {
   const int S = max(a.seq_used[r], 0);
   const int Y = (S + a.BS - 1) / a.BS;
   const int nw = (Y * a.BS + 31) >> 5;
-  if (nw > a.max_words) return;  // host sized max_words from max_seq
+  if (nw > a.max_words) {  // longer than the launch's max_seq: left untouched, reported as -2
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0 && a.counts) {
+      int32_t *c = a.counts + (int64_t)r * 4;
+      c[0] = -2; c[1] = -2; c[2] = -2; c[3] = -2;
+    }
+    return;
+  }
   uint32_t *words = sm;
   uint32_t *pre = sm + a.max_words;
   const uint32_t *brow = a.bits + (int64_t)r * a.bits_sr;
@@ -175,7 +181,7 @@ __global__ void __launch_bounds__(CT) compact_kernel(CompactArgs a) {
   const int X = (B + a.BS - 1) / a.BS;
   const int drop = Y - X;
   const int start = drop * a.BS, end = start + B;
-  if (B > a.max_kept) {  // grid too small for this request: leave it untouched
+  if (B > a.max_kept) {  // grid too small for this request: left untouched, reported as -1
     if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0 && a.counts) {
       int32_t *c = a.counts + (int64_t)r * 4;
       c[0] = -1; c[1] = -1; c[2] = -1; c[3] = -1;

@@ -174,7 +174,9 @@ int actkv_pack_keep(const uint8_t *keep, int64_t keep_sr, int R, const int32_t *
  *   freed_out  int32 [R, >=drop]: freed blocks in free-list push order,
  *              i.e. block_table[r, drop-1-j] (paged.py:135-137)
  *   src_out/dst_out int64 [R, >=M]: physical slots of the plan (compaction.py:69)
- *   counts_out int32 [R, 4]: {B, M, drop, X}
+ *   counts_out int32 [R, 4]: {B, M, drop, X}; a request the launch does not move is
+ *              reported as {-1, -1, -1, -1} (B > max_kept) or {-2, -2, -2, -2}
+ *              (seq_used[r] > max_seq), and its rows, perm and tables are not written
  * do_copy = 0 computes the plan outputs without moving rows (plan_compaction).
  * kv strides are in BYTES; row_bytes is the contiguous row (n_kv_heads*head_dim*esize).
  * max_kept bounds B over all requests (sizes the grid; checked in-kernel).

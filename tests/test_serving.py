@@ -1,5 +1,6 @@
 """The HF paged backend's host logic on the CPU: a tiny Qwen3 served through PagedHFCache on a
-CPU-resident PagedKVCache, with the oracle's paged attention standing in for the kernel, must
+CPU-resident PagedKVCache, with the oracle's paged attention standing in for the attention kernel
+and a torch row write standing in for the append kernel, must
 give the logits of the same model on eager attention with a contiguous DynamicCache (the
 reference session's cache, actkv/hf/session.py:91-111): block allocation per step, per-layer
 writes, RoPE positions, causal limits of a multi-token step, and the captured q and lse."""
@@ -29,6 +30,25 @@ def _oracle_attention(q, kv_layer, bt, seq, scale, kv_len=None):
                                kv_len=None if kv_len is None else kv_len.tolist())
 
 
+def _store_host(self, layer, st, key_states, value_states):
+    """Test stand-in for the append launch on a CPU-resident cache: the step's rows written with
+    torch at the slots the block table gives (reference paged.py:76-84, :93-97)."""
+    b, hkv, n, d = key_states.shape
+    bs = self.kv.block_size
+    flat = self.kv.kv[layer].view(2, -1, hkv, d)
+    for i, r in enumerate(self.reqs):
+        pos = torch.arange(st.starts[i], st.starts[i] + n)
+        slots = torch.tensor(self.kv.tables[r], dtype=torch.long)[pos // bs] * bs + pos % bs
+        flat[0, slots] = key_states[i].transpose(0, 1).to(flat.dtype)
+        flat[1, slots] = value_states[i].transpose(0, 1).to(flat.dtype)
+
+
+def _rows_host(kv, req, layer):
+    """K and V rows [S, Hkv, D] of a request in logical order, read through its block table."""
+    s = kv.seq_used[req]
+    return (ref.gather_k(kv.kv[layer], kv.tables[req], s), ref.gather_v(kv.kv[layer], kv.tables[req], s))
+
+
 def _reference_logits(model, prompt, steps):
     """Eager attention and a DynamicCache, one sequence at a time."""
     model.set_attn_implementation("eager")
@@ -51,6 +71,7 @@ def test_paged_backend_matches_eager_dynamic_cache(monkeypatch):
     refs = [_reference_logits(model, prompts[b], toks[:, b]) for b in range(B)]
 
     monkeypatch.setattr(ps, "paged_decode_attention", _oracle_attention)
+    monkeypatch.setattr(ps.PagedHFCache, "_store", _store_host)
     kv = PagedKVCache(24, 4, 2, 16, n_layers=3, dtype=torch.float32, device="cpu")
     kv.free = torch.randperm(24, generator=g).tolist()
     cache = ps.PagedHFCache(kv, [0, 1])
@@ -77,7 +98,7 @@ def test_paged_backend_matches_eager_dynamic_cache(monkeypatch):
     for b in range(B):
         dyn = refs[b][1]
         for layer in range(3):
-            k, v = kv.gather(b, layer)
+            k, v = _rows_host(kv, b, layer)
             torch.testing.assert_close(k.transpose(0, 1), dyn.layers[layer].keys[0], rtol=0, atol=1e-6)
             torch.testing.assert_close(v.transpose(0, 1), dyn.layers[layer].values[0], rtol=0, atol=1e-6)
     # blocks came off the free stack request by request, step by step (as appends in order)
@@ -99,6 +120,7 @@ def test_multi_token_step_is_causal_and_positions_are_logical(monkeypatch):
         want = model(input_ids=more, past_key_values=dyn, position_ids=torch.arange(106, 109)[None],
                      use_cache=True).logits[0]
     monkeypatch.setattr(ps, "paged_decode_attention", _oracle_attention)
+    monkeypatch.setattr(ps.PagedHFCache, "_store", _store_host)
     kv = PagedKVCache(8, 4, 2, 16, n_layers=3, dtype=torch.float32, device="cpu")
     cache = ps.PagedHFCache(kv, [5])
     model.set_attn_implementation(ps.register())

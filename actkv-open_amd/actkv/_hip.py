@@ -20,6 +20,8 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libactkv_hi
 F32, F16, BF16 = 0, 1, 2
 REDUCE_MEAN, REDUCE_MAX = 0, 1
 WS_KEEP_MASK = 0
+ERR_WORKSPACE = 3
+KEEP_MASK_SCRATCH_BYTES = 8 << 20       # the static device scratch of actkv_keep_mask_noalloc
 
 _DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
@@ -47,6 +49,13 @@ _SIGNATURES = {
         _c_i32,                                                  # head_reduce
         _c_p, _c_i64, _c_p, _c_i64,                              # keep, keep_sr, bits, bits_sr
         _c_i32, _c_i32, _c_p, _c_sz, _c_p]),                     # bs, max_seq, ws, ws_bytes, stream
+    "actkv_keep_mask_noalloc": (_c_i32, [
+        _c_p, _c_i32, _c_i64, _c_i64, _c_i64,                    # scores
+        _c_i32, _c_i32, _c_i32,                                  # L H R
+        _c_p, _c_p, _c_p, _c_p, _c_i64,                          # seq_used budget prot_count prot_mask pm_sr
+        _c_i32,                                                  # head_reduce
+        _c_p, _c_i64, _c_p, _c_i64,                              # keep, keep_sr, bits, bits_sr
+        _c_i32, _c_i32, _c_p]),                                  # bs, max_seq, stream
     "actkv_pack_keep": (_c_i32, [_c_p, _c_i64, _c_i32, _c_p, _c_i32, _c_p, _c_i64, _c_p, _c_i32, _c_p]),
     "actkv_compact": (_c_i32, [
         _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,            # kv planes sp ss row_bytes num_blocks

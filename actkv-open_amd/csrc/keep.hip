@@ -22,6 +22,8 @@
 #include "common.h"
 #include "torch_order.h"
 
+#include <mutex>
+
 namespace actkv {
 
 constexpr int HIST_BINS = 2048;
@@ -421,13 +423,14 @@ extern "C" size_t actkv_workspace_size(int kind, int R, int max_seq) {
          align256((size_t)R * 16);
 }
 
-extern "C" int actkv_keep_mask(const void *scores, int scores_dtype, int64_t s_sl, int64_t s_sr,
-                               int64_t s_sh, int L, int H, int R, const int32_t *seq_used,
-                               const int32_t *budget, const int32_t *protected_count,
-                               const uint8_t *protected_mask, int64_t pm_sr, int head_reduce,
-                               uint8_t *keep, int64_t keep_sr, uint32_t *keep_bits,
-                               int64_t bits_sr, int block_size, int max_seq, void *workspace,
-                               size_t workspace_bytes, void *stream) {
+// The launches of actkv_keep_mask on a workspace of workspace_bytes bytes.
+static int keep_mask_impl(const void *scores, int scores_dtype, int64_t s_sl, int64_t s_sr,
+                          int64_t s_sh, int L, int H, int R, const int32_t *seq_used,
+                          const int32_t *budget, const int32_t *protected_count,
+                          const uint8_t *protected_mask, int64_t pm_sr, int head_reduce,
+                          uint8_t *keep, int64_t keep_sr, uint32_t *keep_bits, int64_t bits_sr,
+                          int block_size, int max_seq, void *workspace, size_t workspace_bytes,
+                          void *stream) {
   if (!scores || !seq_used || !budget || !keep || L < 1 || H < 1 || R < 1 || max_seq < 0 ||
       block_size < 1)
     return ACTKV_ERR_INVALID_ARG;
@@ -484,6 +487,66 @@ extern "C" int actkv_keep_mask(const void *scores, int scores_dtype, int64_t s_s
   dim3 g3((unsigned)((padded + 255) / 256), R);
   hipLaunchKernelGGL(keep_write_kernel, g3, dim3(256), 0, st, a);
   return actkv_check_launch();
+}
+
+extern "C" int actkv_keep_mask(const void *scores, int scores_dtype, int64_t s_sl, int64_t s_sr,
+                               int64_t s_sh, int L, int H, int R, const int32_t *seq_used,
+                               const int32_t *budget, const int32_t *protected_count,
+                               const uint8_t *protected_mask, int64_t pm_sr, int head_reduce,
+                               uint8_t *keep, int64_t keep_sr, uint32_t *keep_bits,
+                               int64_t bits_sr, int block_size, int max_seq, void *workspace,
+                               size_t workspace_bytes, void *stream) {
+  return keep_mask_impl(scores, scores_dtype, s_sl, s_sr, s_sh, L, H, R, seq_used, budget,
+                        protected_count, protected_mask, pm_sr, head_reduce, keep, keep_sr,
+                        keep_bits, bits_sr, block_size, max_seq, workspace, workspace_bytes,
+                        stream);
+}
+
+// ---------------------------------------------------------------- no-allocation variant
+// The workspace of actkv_keep_mask_noalloc: one array per GPU, part of the library's device
+// code object, so it exists from module load until the process ends and no call allocates.
+// Its host-side name is a stand-in, not a device address: host code uses only the address
+// hipGetSymbolAddress returns for the current device, looked up once per device.
+static __device__ __align__(256) unsigned char scratch[ACTKV_KEEP_MASK_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void *scratch_dev[MAX_DEVICES];
+
+int scratch_address(void **out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return ACTKV_ERR_LAUNCH;
+  if (dev < 0 || dev >= MAX_DEVICES) return ACTKV_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_dev[dev]) {
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return ACTKV_ERR_LAUNCH;
+    scratch_dev[dev] = p;
+  }
+  *out = scratch_dev[dev];
+  return ACTKV_OK;
+}
+}  // namespace
+
+extern "C" int actkv_keep_mask_noalloc(const void *scores, int scores_dtype, int64_t s_sl,
+                                       int64_t s_sr, int64_t s_sh, int L, int H, int R,
+                                       const int32_t *seq_used, const int32_t *budget,
+                                       const int32_t *protected_count,
+                                       const uint8_t *protected_mask, int64_t pm_sr,
+                                       int head_reduce, uint8_t *keep, int64_t keep_sr,
+                                       uint32_t *keep_bits, int64_t bits_sr, int block_size,
+                                       int max_seq, void *stream) {
+  if (R < 1 || max_seq < 0) return ACTKV_ERR_INVALID_ARG;
+  if (actkv_workspace_size(ACTKV_WS_KEEP_MASK, R, max_seq) > ACTKV_KEEP_MASK_SCRATCH_BYTES)
+    return ACTKV_ERR_WORKSPACE;
+  void *ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc) return rc;
+  return keep_mask_impl(scores, scores_dtype, s_sl, s_sr, s_sh, L, H, R, seq_used, budget,
+                        protected_count, protected_mask, pm_sr, head_reduce, keep, keep_sr,
+                        keep_bits, bits_sr, block_size, max_seq, ws,
+                        ACTKV_KEEP_MASK_SCRATCH_BYTES, stream);
 }
 
 extern "C" int actkv_pack_keep(const uint8_t *keep, int64_t keep_sr, int R, const int32_t *seq_used,

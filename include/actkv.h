@@ -140,6 +140,28 @@ int actkv_keep_mask(const void *scores, int scores_dtype, int64_t s_sl, int64_t 
                     void *stream);
 
 /*
+ * actkv_keep_mask_noalloc -- actkv_keep_mask without a caller workspace.
+ *
+ * No counterpart in the reference: an addition for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid allocation).  Same
+ * arguments, results and errors as actkv_keep_mask, minus the workspace: the keys,
+ * histogram and selection live in a file-scope device array of
+ * ACTKV_KEEP_MASK_SCRATCH_BYTES bytes per GPU, held from the library's load until the
+ * process ends.  Calls whose actkv_workspace_size(ACTKV_WS_KEEP_MASK, R, max_seq) exceeds
+ * it return ACTKV_ERR_WORKSPACE and launch nothing.  The array's address is looked up on
+ * the current device at its first call there, so `stream` must belong to the current
+ * device.  Every call on a GPU shares that GPU's array (each clears what it accumulates
+ * into): calls that may overlap on one GPU race and must be ordered on one stream.
+ */
+#define ACTKV_KEEP_MASK_SCRATCH_BYTES ((size_t)8 << 20)
+int actkv_keep_mask_noalloc(const void *scores, int scores_dtype, int64_t s_sl, int64_t s_sr,
+                            int64_t s_sh, int L, int H, int R, const int32_t *seq_used,
+                            const int32_t *budget, const int32_t *protected_count,
+                            const uint8_t *protected_mask, int64_t pm_sr, int head_reduce,
+                            uint8_t *keep, int64_t keep_sr, uint32_t *keep_bits, int64_t bits_sr,
+                            int block_size, int max_seq, void *stream);
+
+/*
  * actkv_pack_keep -- bool keep mask [R, >=S] -> packed bits (LSB-first),
  * zero beyond seq_used[r] up to a whole number of blocks, plus the popcount
  * of each request's mask in kept_out[r] (optional).  Support for

@@ -163,7 +163,8 @@ class PagedLRFU:
         ks4 = self.ks.unsqueeze(2)
         _, bits = _keep_mask_launch(ks4, L, 1, self.ks.stride(0), self.ks.stride(1), 0, R, seq_dev, bud_dev,
                                     cnt_dev if first else None, None if first else self.pins,
-                                    0 if first else self.pins.stride(0), "mean", cache.block_size, smax, dev)
+                                    0 if first else self.pins.stride(0), "mean", cache.block_size, smax, dev,
+                                    want_keep=False)
         self._pins_alt.zero_()
         perm, _ = cache._compact_launch(self.reqs, bits, kept, None if first else self.pins,
                                         cnt_dev if first else None, pin_out=self._pins_alt)

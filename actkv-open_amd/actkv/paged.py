@@ -109,17 +109,17 @@ def _scores_layout(scores: torch.Tensor, seq_used: int):
 
 
 def _keep_mask_launch(s, L, H, s_sl, s_sr, s_sh, R, seq_dev, budget_dev, prot_count_dev,
-                      prot_mask, pm_sr, head_reduce, block_size, max_seq, device):
-    """Run actkv_keep_mask; returns (keep [R, max_seq] bool, bits [R, words] int32)."""
-    keep = torch.empty(R, max(max_seq, 1), dtype=torch.bool, device=device)
+                      prot_mask, pm_sr, head_reduce, block_size, max_seq, device, want_keep=True):
+    """Run actkv_keep_mask; returns (keep [R, max_seq] bool or None, bits [R, words] int32)."""
+    keep = torch.empty(R, max(max_seq, 1), dtype=torch.bool, device=device) if want_keep else None
     nw = keep_words(max_seq, block_size)
     bits = torch.empty(R, max(nw, 1), dtype=torch.int32, device=device)
     ws = _hip.workspace(device, _hip.WS_KEEP_MASK, R, max_seq)
     rc = _hip.lib().actkv_keep_mask(
         s.data_ptr(), _hip.dtype_code(s.dtype), s_sl, s_sr, s_sh, L, H, R,
         seq_dev.data_ptr(), budget_dev.data_ptr(), _hip.ptr(prot_count_dev), _hip.ptr(prot_mask), pm_sr,
-        _REDUCE[head_reduce], keep.data_ptr(), keep.shape[1], bits.data_ptr(), bits.shape[1],
-        block_size, max_seq, ws.data_ptr(), ws.numel(), _hip.stream(device))
+        _REDUCE[head_reduce], _hip.ptr(keep), 0 if keep is None else keep.shape[1], bits.data_ptr(),
+        bits.shape[1], block_size, max_seq, ws.data_ptr(), ws.numel(), _hip.stream(device))
     _hip.check(rc, "actkv_keep_mask")
     return keep, bits
 
@@ -626,7 +626,7 @@ class PagedKVCache:
         _, bits = _keep_mask_launch(sc, L, H, sc.stride(0), sc.stride(1), sc.stride(2), ra,
                                     params[:ra], params[ra:2 * ra], prot_count, pin_mat,
                                     0 if pin_mat is None else pin_mat.stride(0),
-                                    head_reduce, self.block_size, smax, dev)
+                                    head_reduce, self.block_size, smax, dev, want_keep=False)
         perm, pin_out = self._compact_launch(a_reqs, bits, kept, pin_mat, prot_count)
         for j, i in enumerate(active):
             b = kept[j]

@@ -19,6 +19,7 @@
 #include "common.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace actkv {
 
@@ -377,6 +378,41 @@ __global__ void bump_n_seen_kernel(int32_t *n_seen, const int32_t *n_valid, int 
   if (r < R) n_seen[r] += n_valid ? min(max(n_valid[r], 0), N) : N;
 }
 
+// Compute units of the current device (one query per device, cached).
+static int device_cus() {
+  static std::mutex mu;
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Token range per workgroup of the MFMA kernel.  One workgroup fills a CU (its
+// query tile takes most of the LDS), so the grid is sized in waves of CU-count
+// workgroups: as many waves as keep every wave at least MIN_SLICES 32-token
+// slices per wave of the workgroup, at most MAX_WAVES (each workgroup re-stages
+// its query tile; fewer, larger workgroups amortise that), and the token range
+// split evenly over the chunks of a pair.  A small problem -- one layer of one
+// request -- thus still spreads over every CU.
+static int mfma_tokens_per_wg(int pairs, int span, int nw) {
+  constexpr int MIN_SLICES = 2, MAX_WAVES = 8, MAX_TOKENS = 8192;  // 8192: the block-table slice
+  const int64_t cus = device_cus();
+  const int64_t spp = (span + 31) / 32;                       // slices per pair
+  const int64_t total = (int64_t)pairs * spp;
+  const int64_t waves = std::min<int64_t>(MAX_WAVES, std::max<int64_t>(1, total / (cus * nw * MIN_SLICES)));
+  const int64_t padded = ((pairs + 7) / 8) * 8;               // pairs rounded to whole XCD groups
+  const int64_t cpp = std::max<int64_t>(1, (waves * cus + padded - 1) / padded);
+  const int64_t per = std::min<int64_t>(MAX_TOKENS / 32, (spp + cpp - 1) / cpp);
+  return (int)(per * 32);
+}
+
 template <typename T, typename V8, int G>
 static int launch_mfma(const ScoreArgs &a0, int bs_shift, hipStream_t st) {
   const int pairs = a0.L * a0.R * a0.Hkv;
@@ -389,14 +425,9 @@ static int launch_mfma(const ScoreArgs &a0, int bs_shift, hipStream_t st) {
     a.qcn = std::min(q_per_launch, a0.N - qc0);
     const int rows = a.qcn * G;
     // NW waves (NW/4 per SIMD: 3 keeps the VALU post-processing overlapped with
-    // the matrix core), 32-token slices.  Token range per workgroup: a multiple of
-    // NW*32, at least 4 slices per wave so the staged query tile is reused, about
-    // 2048 workgroups in total, at most 8192 tokens (the block-table slice).
+    // the matrix core), 32-token slices dealt round-robin to the waves.
     constexpr int NW = 12, TT = 1;
-    constexpr int round = NW * 32 * TT;
-    const int64_t rounds = (int64_t)pairs * ((span + round - 1) / round);
-    int per_wg = (int)std::min<int64_t>(8192 / round, std::max<int64_t>(4, (rounds + 2047) / 2048));
-    int tpw = per_wg * round;
+    const int tpw = mfma_tokens_per_wg(pairs, span, NW);
     const int cpp = (span + tpw - 1) / tpw;
     const int grid = ((pairs + 7) / 8) * 8 * cpp;
 #define ACTKV_LAUNCH(ROWSV)                                                                        \

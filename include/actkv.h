@@ -124,12 +124,13 @@ int actkv_copy_slots(void *kv_flat, int64_t planes, int64_t stride_plane_bytes,
  * one of the two may be non-NULL (both NULL: nothing protected).
  *
  * keep (bool bytes, row stride keep_sr) receives S entries per request.
- * keep_bits (optional, row stride bits_sr in uint32 words) receives the same
- * mask packed LSB-first, zero-padded to a whole number of blocks of
- * block_size tokens: the input of actkv_compact.
+ * keep_bits (row stride bits_sr in uint32 words) receives the same mask packed
+ * LSB-first, zero-padded to a whole number of blocks of block_size tokens: the
+ * input of actkv_compact.  Either may be NULL, not both.
  * workspace must hold actkv_workspace_size(ACTKV_WS_KEEP_MASK, R, max_seq)
- * bytes; it needs no initialisation (the call clears what it accumulates
- * into).  Calls that share a workspace must be stream-ordered.
+ * bytes (the per-token keys); it needs no initialisation.  Calls that share a
+ * workspace must be stream-ordered.  Limits: L <= 120 (ACTKV_ERR_UNSUPPORTED
+ * beyond).
  */
 int actkv_keep_mask(const void *scores, int scores_dtype, int64_t s_sl, int64_t s_sr,
                     int64_t s_sh, int L, int H, int R, const int32_t *seq_used,

@@ -353,6 +353,46 @@ def test_keep_mask_bit_exact_with_the_oracle(L, H, S, W, budget, prot, reduce):
     assert int(got.sum()) == min(prot, S) + budget
 
 
+@pytest.mark.parametrize("dtype,reduce,prot_kind", [
+    (torch.float32, "mean", "count"),
+    (torch.float32, "max", "mask"),
+    (torch.bfloat16, "mean", "mask"),
+])
+def test_keep_mask_ragged_batch_in_one_call_matches_the_oracle(dtype, reduce, prot_kind):
+    """One keep-mask call over ragged requests -- past the selection's 32768-token register
+    chunk, exactly one chunk, a few blocks, a few tokens -- equals the oracle request by
+    request: the bool mask, and the packed bits (LSB-first, zero up to whole blocks)."""
+    from actkv import _hip
+    from actkv.paged import _keep_mask_launch
+    lens = [70001, 13103, 5, 40000, 1, 32768, 257]
+    budgets = [7000, 1027, 2, 0, 1, 3276, 300]
+    L, H, R, bs = 4, 8, len(lens), 16
+    W = max(lens) + 3
+    g = torch.Generator().manual_seed(31)
+    scores = (torch.rand(L, R, H, W, generator=g) * torch.exp(torch.randn(L, R, H, W, generator=g))).to(dtype)
+    dev = torch.device("cuda")
+    sc = scores.to(dev)
+    seq = _hip.upload_i32(lens, dev)
+    bud = _hip.upload_i32(budgets, dev)
+    if prot_kind == "count":
+        prots = [4, 0, 2, 9, 0, 4, 300]
+        pc, pm = _hip.upload_i32(prots, dev), None
+        pm_cpu = [torch.arange(s) < p for s, p in zip(lens, prots)]
+    else:
+        pm_full = torch.rand(R, W, generator=g) < 0.03
+        pc, pm = None, pm_full.to(dev)
+        pm_cpu = [pm_full[r, :s] for r, s in enumerate(lens)]
+    keep, bits = _keep_mask_launch(sc, L, H, sc.stride(0), sc.stride(1), sc.stride(2), R, seq, bud, pc, pm,
+                                   0 if pm is None else pm.stride(0), reduce, bs, max(lens), dev)
+    keep, bits = keep.cpu(), bits.cpu().numpy().view(np.uint32)
+    for r, S in enumerate(lens):
+        want = ref.keep_mask_from_scores(scores[:, r].float(), S, budgets[r], protected=pm_cpu[r], head_reduce=reduce)
+        assert torch.equal(keep[r, :S], want), f"request {r} ({S} tokens): keep mask differs"
+        padded = -(-S // bs) * bs
+        unpacked = np.unpackbits(bits[r].view(np.uint8), bitorder="little")[:padded].astype(bool)
+        assert np.array_equal(unpacked[:S], want.numpy()) and not unpacked[S:].any(), f"request {r}: keep bits"
+
+
 def test_keep_mask_ties_keep_the_lower_index():
     """Equal scores straddling the top-k boundary: the lower index wins (documented rule)."""
     S = 5000
@@ -363,6 +403,23 @@ def test_keep_mask_ties_keep_the_lower_index():
     want = ref.keep_mask_lowest_index_ties(scores, S, 350, protected=3)
     assert torch.equal(keep, want)
     assert keep[:3].all() and keep[3000:3050].all() and keep[100:400].all() and not keep[400:1100].any()
+
+
+@pytest.mark.parametrize("n_tied,spread", [(5000, True), (3000, False), (40, True)])
+def test_keep_mask_many_ties_keep_the_lower_index(n_tied, spread):
+    """More tied scores at the boundary than the selection ranks in LDS (2048), scattered over
+    the request or in one run, and a few ties among distinct scores: lowest indices first."""
+    S = 40000
+    g = torch.Generator().manual_seed(n_tied)
+    scores = torch.rand(3, 2, S, generator=g) * 0.4            # distinct, below the tie value
+    pos = torch.randperm(S - 8, generator=g)[:n_tied] + 8 if spread else torch.arange(1000, 1000 + n_tied)
+    scores[..., pos] = 0.5
+    scores[..., S - 100:] = 0.9                                # 100 strictly higher
+    budget = 100 + n_tied // 3
+    keep = keep_mask_from_scores(scores.cuda(), S, budget, protected=4).cpu()
+    want = ref.keep_mask_lowest_index_ties(scores, S, budget, protected=4)
+    assert torch.equal(keep, want)
+    assert int(keep.sum()) == 4 + budget
 
 
 def test_batched_evict_mixes_first_and_repeated_evictions():

@@ -51,7 +51,7 @@ def test_noalloc_keep_mask_equals_the_workspace_entry_point():
         else:
             prot_mask = (torch.rand(R, max_seq, generator=g) < 0.05).to(dev)
         need = int(_hip.lib().actkv_workspace_size(_hip.WS_KEEP_MASK, R, max_seq))
-        ws = torch.empty(need, dtype=torch.uint8, device=dev)
+        ws = torch.zeros(need, dtype=torch.uint8, device=dev)
         ka, ba = _keep("workspace", scores, L, H, R, seq, budget, prot_count, prot_mask, reduce, max_seq, ws=ws)
         kb, bb = _keep("noalloc", scores, L, H, R, seq, budget, prot_count, prot_mask, reduce, max_seq)
         torch.cuda.synchronize()

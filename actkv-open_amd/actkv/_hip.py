@@ -171,37 +171,56 @@ _workspaces: dict = {}
 
 
 class _PinnedRing:
-    """Host-to-device int32 uploads through a ring of pinned staging buffers.
+    """Host-to-device int32 uploads through one pinned staging buffer, used as a ring.
 
-    Allocating pinned memory per call (torch's pin_memory) can stall the host for tens of
-    milliseconds when a new size is first needed; the ring allocates a few buffers, grown
-    geometrically, and reuses each one once the copy that last read it has completed (an event
-    recorded after the copy; with 8 buffers it has completed long before)."""
+    Each upload copies into the next free span of the buffer and queues an asynchronous copy
+    from it.  The buffer is split in two halves: leaving a half records an event after its last
+    copy, and coming back to that half waits for that event, so no span is rewritten before its
+    copy has run.  One event per half-buffer of uploads (thousands of calls), instead of one per
+    upload (an event record costs a current-stream lookup, several microseconds).  Uploads larger
+    than half the buffer are copied synchronously from pageable memory."""
 
-    SLOTS = 8
+    SIZE = 1 << 18          # int32 entries (1 MiB)
 
     def __init__(self):
-        self.bufs = [None] * self.SLOTS
-        self.events = [None] * self.SLOTS
-        self.i = 0
+        self.buf = None
+        self.np = None
+        self.off = 0
+        self.events = [None, None]       # per half: event after its last copy, or "sync"
+        self.streams = [set(), set()]    # per half: the streams its copies were queued on
 
     def upload_i32(self, values, device: torch.device) -> torch.Tensor:
         arr = np.asarray(values, dtype=np.int32).reshape(-1)
         n = arr.size
-        k = self.i % self.SLOTS
-        self.i += 1
-        if self.events[k] is not None:
-            self.events[k].synchronize()
-        buf = self.bufs[k]
-        if buf is None or buf.numel() < n:
-            old = 0 if buf is None else buf.numel()
-            buf = torch.empty(max(n, 2 * old, 1 << 14), dtype=torch.int32, pin_memory=True)
-            self.bufs[k] = buf
-        buf.numpy()[:n] = arr
-        out = buf[:n].to(device, non_blocking=True)
-        if self.events[k] is None:
-            self.events[k] = torch.cuda.Event()
-        self.events[k].record()
+        half = self.SIZE // 2
+        if n > half:
+            return torch.from_numpy(arr.copy()).to(device)
+        if self.buf is None:
+            self.buf = torch.empty(self.SIZE, dtype=torch.int32, pin_memory=True)
+            self.np = self.buf.numpy()
+        h = self.off // half
+        cur = stream(device)
+        if self.off + n > (h + 1) * half:
+            # leave half h (its copies are all queued): an event on the stream that queued them
+            # covers them; copies queued on several streams are covered by a device sync later
+            if self.streams[h] <= {cur}:
+                ev = torch.cuda.Event()
+                ev.record()
+                self.events[h] = ev
+            else:
+                self.events[h] = "sync"
+            h = 1 - h
+            self.off = h * half
+            if self.events[h] == "sync":
+                torch.cuda.synchronize(device)
+            elif self.events[h] is not None:
+                self.events[h].synchronize()
+            self.events[h] = None
+            self.streams[h] = set()
+        self.streams[h].add(cur)
+        self.np[self.off:self.off + n] = arr
+        out = self.buf[self.off:self.off + n].to(device, non_blocking=True)
+        self.off += n
         return out
 
 

@@ -72,6 +72,9 @@ def parse(argv=None):
                     help="run the agent-loop workload instead (rounds of append + causal action scoring + "
                          "LRFU keep + compaction on a 36-layer batch of 4) and print its own JSON line")
     ap.add_argument("--ora-rounds", type=int, default=50)
+    ap.add_argument("--ora-short", type=int, default=10,
+                    help="rounds of the agent-loop workload reported in the default JSON line (0: none)")
+    ap.add_argument("--no-table1", action="store_true", help="skip the reference bench's Table-1 cases")
     ap.add_argument("--no-gc-freeze", action="store_true",
                     help="agent loop: leave the startup heap in the collected generations (by default it "
                          "is frozen after setup, as a serving process does after loading)")
@@ -95,6 +98,8 @@ def parse(argv=None):
         ap.error("--steps must be at least 1 (the timed steps)")
     if args.warmup < 0:
         ap.error("--warmup must not be negative")
+    if args.ora_short < 0:
+        ap.error("--ora-short must not be negative")
     if args.ora_rounds < 1 or args.serve_rounds < 1 or args.serve_steps < 1:
         ap.error("--ora-rounds, --serve-rounds and --serve-steps must be at least 1")
     if not 0 <= args.serve_action <= args.serve_steps:
@@ -305,8 +310,121 @@ def check_step(w):
     nblk = math.ceil(w.S / w.bs)
     ok_host = (w.cache.seq_used[0] == int(keep_o.sum()) and len(w.cache.tables[0]) == nblk - drop
                and len(w.cache.free) == w.nb - (nblk - drop))
+    ok_out = outputs_match(w, slots_before, keep_o)
     return {"keep_mask_matches_oracle": ok_mask, "perm_matches_oracle": ok_perm,
-            "layer0_rows_match": ok_rows, "allocator_state_ok": ok_host}, int(src.size), int(drop)
+            "layer0_rows_match": ok_rows, "allocator_state_ok": ok_host,
+            "outputs_match": ok_out}, int(src.size), int(drop)
+
+
+def outputs_match(w, slots_before, keep):
+    """The reference bench's attention check (benchmarks/bench_kernels.py:126-133): decode
+    attention of a fresh query after the step equals the same attention over the gather
+    baseline, within rtol = atol = 1e-3.  The compacted cache is attended by the paged
+    attention kernel; the baseline is the pre-step cache's survivors (the oracle's keep mask on
+    the step's scores) gathered into a fresh contiguous buffer (gather_compaction,
+    compaction.py:109-114) and attended by the torch reference (lse_attn.py:42-60)."""
+    import torch
+    from actkv.kernels.compaction import gather_compaction
+    from actkv.kernels.lse_attn import paged_decode_attention, paged_decode_attention_ref
+    g = torch.Generator(device=w.dev).manual_seed(w.args.seed + 7)
+    q2 = torch.randn(1, w.hq, w.d, generator=g, device=w.dev, dtype=torch.bfloat16)
+    seq, bt = w.cache._device_tables([0])
+    got, _ = paged_decode_attention(q2, w.cache.kv[0], bt, seq)
+    keep_slots = slots_before[torch.from_numpy(keep.numpy()).to(w.dev)]
+    flat0 = w.kv0[0].view(2, -1, w.hkv * w.d)
+    base = gather_compaction(flat0, keep_slots)                  # [2, B, Hkv*D]
+    b = base.shape[1]
+    nblk = -(-b // w.bs)
+    pad = torch.zeros(2, nblk * w.bs - b, base.shape[2], dtype=base.dtype, device=w.dev)
+    kv_base = torch.cat([base, pad], 1).view(2, nblk, w.bs, w.hkv, w.d)
+    table = torch.arange(nblk, dtype=torch.int32, device=w.dev).view(1, -1)
+    want, _ = paged_decode_attention_ref(q2, kv_base, table, torch.tensor([b], device=w.dev))
+    return bool(torch.allclose(got, want, rtol=1e-3, atol=1e-3))
+
+
+def extra_memory_mb(w):
+    """Peak device memory one step allocates above what it started with (the reference bench's
+    extra-memory column, benchmarks/bench_kernels.py:143-151), after a warm step."""
+    import torch
+    w.restore()
+    w.step()
+    w.restore()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(w.dev)
+    base = torch.cuda.memory_allocated(w.dev)
+    w.step()
+    torch.cuda.synchronize()
+    return round((torch.cuda.max_memory_allocated(w.dev) - base) / 2 ** 20, 3)
+
+
+# The reference's published Table-1 step times (NVIDIA A100-SXM4-80GB, fp16, one layer, one
+# action query; median of 5 after 1 warm-up): results/bench_kernels.txt:3-14 of the reference.
+TABLE1_A100_MS = {(1024, 512, 1): 1.233, (1024, 512, 4): 4.128, (1024, 512, 16): 15.690, (1024, 512, 64): 61.856,
+                  (2048, 1536, 1): 1.248, (2048, 1536, 4): 4.290, (2048, 1536, 16): 16.214, (2048, 1536, 64): 63.968,
+                  (6144, 4096, 1): 1.394, (6144, 4096, 4): 4.753, (6144, 4096, 16): 18.111, (6144, 4096, 64): 71.083}
+
+
+def run_table1(torch, dev, seed=0, warmup=1, iters=5):
+    """The reference bench's Table-1 cases on this GPU, for context (benchmarks/bench_kernels.py:
+    67-151): r requests of n tokens in one fp16 layer (32 q / 8 KV heads, head_dim 128, block 16,
+    physical blocks shuffled), one action query per request with its lse from decode attention.
+    A step is what the reference times: block table, cal_attn of the query, then evict of each
+    request in a Python loop (paged.py:141-157); `batched_ms` is the same step with one
+    evict_batch call.  Wall time with a synchronisation on both sides, median of `iters` steps on
+    fresh caches after `warmup`, as the reference does."""
+    from actkv.paged import PagedKVCache
+    hq, hkv, d, bs = 32, 8, 128, 16
+
+    def build(r, n):
+        nb = r * math.ceil(n / bs) + 4
+        cache = PagedKVCache(nb, bs, hkv, d, dtype=torch.float16, device=dev)
+        cache.free = torch.randperm(nb, generator=torch.Generator().manual_seed(seed)).tolist()
+        g = torch.Generator(device=dev).manual_seed(seed)
+        k = torch.randn(1, r * n, hkv, d, generator=g, device=dev, dtype=torch.float16)
+        v = torch.randn(k.shape, generator=g, device=dev, dtype=torch.float16)
+        cache.append_batch(list(range(r)), k, v, [n] * r)
+        return cache
+
+    def step(cache, reqs, q, lse, budget, batched):
+        bt = cache.block_table(reqs)
+        out = torch.zeros(len(reqs), hkv, bt.shape[1] * bs, device=dev)
+        nseen = torch.zeros(len(reqs), dtype=torch.int32, device=dev)
+        cache.cal_attn(reqs, q, lse, out, nseen)
+        if batched:
+            cache.evict_batch(reqs, out, budget)
+        else:
+            for i in reqs:
+                cache.evict(i, out[i], budget)
+
+    def timed(r, n, reqs, q, lse, budget, batched):
+        for _ in range(warmup):
+            step(build(r, n), reqs, q, lse, budget, batched)
+        times = []
+        for _ in range(iters):
+            cache = build(r, n)
+            torch.cuda.synchronize()
+            t = time.perf_counter()
+            step(cache, reqs, q, lse, budget, batched)
+            torch.cuda.synchronize()
+            times.append((time.perf_counter() - t) * 1e3)
+        return statistics.median(times)
+
+    rows = []
+    for (n, budget, r), a100 in TABLE1_A100_MS.items():
+        reqs = list(range(r))
+        q = torch.randn(r, hq, d, generator=torch.Generator(device=dev).manual_seed(1), device=dev,
+                        dtype=torch.float16)
+        probe = build(r, n)
+        _, lse = probe.decode_attention(reqs, q)
+        del probe
+        ms = timed(r, n, reqs, q, lse, budget, False)
+        ms_b = timed(r, n, reqs, q, lse, budget, True)
+        rows.append({"n": n, "budget": budget, "r": r, "ms": round(ms, 3), "batched_ms": round(ms_b, 3),
+                     "a100_published_ms": a100, "speedup_vs_a100": round(a100 / ms, 1)})
+    return {"workload": "the reference bench's Table-1 cases: 1 fp16 layer, 32 q / 8 KV heads, head_dim 128, "
+                        "block 16, one action query; step = cal_attn + evict per request (batched_ms: one "
+                        "evict_batch); wall time, median of 5 after 1 warm-up",
+            "cases": rows}
 
 
 def cpu_baseline(w, layers):
@@ -353,6 +471,14 @@ def cpu_model():
     except OSError:
         pass
     return None
+
+
+def score_source_sha():
+    """sha256 of the scoring kernel's source: a stored counter figure is used only for the
+    kernel it was measured on."""
+    import hashlib
+    with open(os.path.join(ROOT, "actkv-open_amd", "csrc", "score.hip"), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
 
 
 def load_traffic(path):
@@ -497,6 +623,17 @@ def _append_summary(per_round, L, hkv, d):
 
 
 def run_ora(args, dev):
+    """The agent-loop workload on its own (bench.py --ora): prints its JSON line."""
+    result = ora_rounds(args, dev, args.ora_rounds, per_round=True)
+    line = json.dumps(result)
+    print(line)
+    if args.out:
+        with open(args.out, "w") as f:
+            f.write(line + "\n")
+    return 0
+
+
+def ora_rounds(args, dev, rounds, per_round=False):
     """Agent-loop workload: 50 rounds on a Qwen3-8B-shaped 36-layer cache holding 4 sequences.
     Each round appends, per sequence, U[512, 2048] observation + U[128, 512] reasoning +
     U[32, 64] action tokens (bf16 K/V ~ N(0,1), seeded; one batched append launch, timed on
@@ -511,7 +648,6 @@ def run_ora(args, dev):
     from actkv.paged import PagedKVCache
 
     L, hq, hkv, d, bs, R = args.layers, args.q_heads, args.kv_heads, args.head_dim, args.block_size, 4
-    rounds = args.ora_rounds
     b_lo, b_hi, sinks = 4096, 16384, 4
     cap = ((b_hi + sinks + 2048 + 512 + 64 + bs - 1) // bs) * bs
     nb = R * (cap // bs + 2) + 64
@@ -540,8 +676,9 @@ def run_ora(args, dev):
         gc.collect()
         gc.freeze()
     log(f"agent loop: {rounds} rounds, {R} sequences, {L} layers")
+    schedule = max(args.ora_rounds, rounds)
     for rnd in range(rounds):
-        budget = int(round(b_lo + (b_hi - b_lo) * rnd / max(rounds - 1, 1)))
+        budget = int(round(b_lo + (b_hi - b_lo) * rnd / max(schedule - 1, 1)))
         n_act, counts = [], []
         for r in reqs:
             n_new = int(rng.integers(512, 2049)) + int(rng.integers(128, 513))
@@ -617,15 +754,14 @@ def run_ora(args, dev):
         "gc_frozen": not args.no_gc_freeze,
         "gc_us_max": round(max(p["gc_us"] for p in per_round), 1),
         "blocks_reclaimed_total": sum(p["blocks_reclaimed"] for p in per_round),
-        "per_round": [{k: (round(v, 1) if isinstance(v, float) else v) for k, v in p.items()} for p in per_round],
-        **run_info(torch, dev),
     }
-    line = json.dumps(result)
-    print(line)
-    if args.out:
-        with open(args.out, "w") as f:
-            f.write(line + "\n")
-    return 0
+    if per_round:
+        result["per_round"] = [{k: (round(v, 1) if isinstance(v, float) else v) for k, v in p.items()}
+                               for p in per_round]
+        result.update(run_info(torch, dev))
+    del cache, lr
+    torch.cuda.empty_cache()
+    return result
 
 
 def run_serve(args, dev):
@@ -743,6 +879,11 @@ def main(argv=None):
 
     log(f"building the {args.layers}-layer workload")
     w = Workload(args, args.layers, dev)
+    # a full collection walks every tracked object of the process (torch's import alone leaves
+    # hundreds of thousands) and stalls the host for tens of milliseconds; the startup heap is
+    # frozen after setup, as a serving process does after loading
+    gc.collect()
+    gc.freeze()
     log("checking one step against the oracle")
     checks, moved, drop = check_step(w)
     log(f"checks {checks}; timing {args.warmup} + {args.steps} steps")
@@ -755,10 +896,11 @@ def main(argv=None):
     traffic = load_traffic(args.traffic)
     traffic_bytes = None
     if traffic and traffic.get("layers") == args.layers and traffic.get("seq") == args.seq \
-            and traffic.get("queries") == args.queries:
+            and traffic.get("queries") == args.queries and traffic.get("score_hip_sha256") == score_source_sha():
         traffic_bytes = traffic.get("hbm_bytes_per_launch")
 
     log(f"step {m['step_us']:.1f} us (synchronised launches {m['step_us_sync']:.1f} us), scoring call {k_us:.1f} us")
+    extra_mb = extra_memory_mb(w)
     single = None
     if not args.no_single_layer and args.layers != 1:
         log("one-layer workload")
@@ -790,6 +932,18 @@ def main(argv=None):
 
     log("apply_copies on a plan of the compaction's size")
     copies = time_apply_copies(torch, w, moved, max(args.steps, 5))  # rewrites rows: after every other leg
+    del w
+    torch.cuda.empty_cache()
+    table1 = None
+    if not args.no_table1:
+        log("the reference bench's Table-1 cases")
+        table1 = run_table1(torch, dev, seed=args.seed)
+    ora = None
+    if args.ora_short > 0 and args.layers == 36:
+        log(f"agent loop, first {args.ora_short} rounds")
+        ora = ora_rounds(args, dev, args.ora_short)
+        ora = {k: ora[k] for k in ("config", "rounds", "evict_us", "evict_us_per_layer_median", "append",
+                                   "blocks_reclaimed_total", "gc_us_max")}
 
     result = {
         "metric": "score+compact HBM GB/s (% of 8 TB/s) and evict us/layer, Qwen3-8B shape 32k",
@@ -818,6 +972,9 @@ def main(argv=None):
         "cpu_baseline": cpu,
         "single_layer": single,
         "apply_copies": copies,
+        "extra_mb_per_step": extra_mb,
+        "table1": table1,
+        "ora": ora,
         "checks": checks,
         "wall_s_incl_restore": round(m["wall_s_incl_restore"], 3),
         **run_info(torch, dev),

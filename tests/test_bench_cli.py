@@ -19,6 +19,7 @@ def _run(*args):
     (["--steps", "0"], "--steps must be at least 1"),
     (["--warmup", "-1"], "--warmup must not be negative"),
     (["--ora", "--ora-rounds", "0"], "must be at least 1"),
+    (["--ora-short", "-1"], "--ora-short must not be negative"),
     (["--serve", "--serve-action", "60", "--serve-steps", "48"], "--serve-action must be between"),
 ])
 def test_invalid_runs_are_rejected(args, msg):

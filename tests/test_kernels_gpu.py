@@ -465,3 +465,26 @@ def test_launches_follow_torch_current_stream():
     nb = torch.zeros_like(na)
     cache.cal_attn([0, 1], q, lse, b, nb, layer=0)
     assert torch.equal(a, b) and na.tolist() == nb.tolist() == [1, 1]
+
+
+def test_pinned_uploads_survive_ring_wraps_and_side_streams():
+    """Host-to-device uploads through the pinned staging ring: enough of them to wrap the ring
+    several times, every third queued on a side stream, and one larger than half the ring;
+    every uploaded tensor holds its values."""
+    from actkv import _hip
+    dev = torch.device("cuda")
+    ring = _hip._PinnedRing()
+    side = torch.cuda.Stream()
+    outs = []
+    for i in range(1200):
+        vals = list(range(i * 1000, i * 1000 + 700 + i % 5))
+        if i % 3 == 0:
+            with torch.cuda.stream(side):
+                outs.append((vals, ring.upload_i32(vals, dev)))
+        else:
+            outs.append((vals, ring.upload_i32(vals, dev)))
+    big = list(range(_hip._PinnedRing.SIZE // 2 + 10))
+    outs.append((big, ring.upload_i32(big, dev)))
+    torch.cuda.synchronize()
+    for vals, t in outs:
+        assert t.cpu().tolist() == vals

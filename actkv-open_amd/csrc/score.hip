@@ -3,14 +3,18 @@
 // Reference: actkv/kernels/lse_attn.py:85-163.  The reference launches one
 // Triton program per (request, logical block, KV head) and folds ONE action
 // query per launch, so K is re-read from HBM once per action token.  Here one
-// workgroup owns a (layer, request, KV head, token range) work item, holds the
-// whole action-query tile of that head (N queries x G group heads) in VGPRs as
-// MFMA A-operands, and streams the head's K rows through LDS exactly once:
+// workgroup owns a (layer, request, KV head) pair and a token range, holds the
+// head's whole action-query tile (N queries x G group heads) on chip and reads
+// the range's K rows from HBM exactly once.  Two MFMA kernels: above 384 query
+// rows the tile sits in registers while K chunks are shared through LDS
+// (score_qreg_kernel: fewer LDS reads per MFMA, the matrix cores bound it); up
+// to 384 rows each wave streams its own K slices into registers against the
+// tile in LDS (score_kslice_kernel: more K in flight).  Both compute
 //
 //   acc[row, t] = q_row . k_t - lse_row / scale            (bf16/fp16 MFMA, fp32 acc)
 //   p[n, t]     = exp2(scale*log2(e) * max_g acc[(n,g), t]) (max over the GQA group
 //                                                           before the exp: exp is monotonic)
-//   sum[t]      = sum_n p[n, t]                              (lane shuffles + LDS)
+//   sum[t]      = sum_n p[n, t]                              (per-wave sums + LDS)
 //   out[t]      = (out[t] * n_seen + sum[t]) / (n_seen + nq) (== nq reference folds)
 //
 // The generic kernel covers every other shape/dtype (fp32 caches, head_dim not
@@ -22,6 +26,12 @@
 #include <mutex>
 
 namespace actkv {
+
+// Longest token range of one MFMA workgroup (its block-table slice holds
+// MFMA_MAX_TOKENS / 16 entries, one per thread of the 512).
+constexpr int MFMA_MAX_TOKENS = 8192;
+// Tokens per K chunk of the query-tile kernel (4 tiles of 32).
+constexpr int QREG_CHUNK = 128;
 
 struct ScoreArgs {
   const void *q;
@@ -112,8 +122,8 @@ __global__ void __launch_bounds__(256) score_generic_kernel(ScoreArgs a) {
   if (valid) *optr = acc;
 }
 
-// ------------------------------------------------------------------ MFMA tile
-// One workgroup (NW waves) owns a (layer, request, KV head) pair and a
+// ------------------------------------------------------------------ MFMA, K slices in registers
+// For query tiles of at most 384 rows.  One workgroup (NW waves) owns a (layer, request, KV head) pair and a
 // token range.  The pair's whole action-query tile -- rows (query n, group head g),
 // nq*G <= ROWS of them, head_dim 128, bf16/fp16 -- is staged ONCE into LDS
 // (rows padded to 272 bytes: conflict-free A-operand reads), with the
@@ -133,9 +143,9 @@ __global__ void __launch_bounds__(256) score_generic_kernel(ScoreArgs a) {
 // max_g exp(x_g) = exp(max_g x_g) costs one exp per (query, token).
 template <typename T, typename V8, int G, int ROWS, bool CAUSAL, int NW, int TT>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
-score_mfma_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
+score_kslice_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
   // NW waves (NW/4 per SIMD), TT 32-token tiles per wave slice
-  constexpr int SLICE = TT * 32, KS = 8, MAXBT = 8192 / 16 + 2;
+  constexpr int SLICE = TT * 32, KS = 8, MAXBT = MFMA_MAX_TOKENS / 16 + 2;
   constexpr int QG = 4 / G;  // queries in an aligned group of four rows
   // query rows are padded to 272 bytes: 16 consecutive rows then start in 16
   // distinct 16-byte bank groups (conflict-free A reads) and every A-operand
@@ -373,6 +383,266 @@ score_mfma_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
   }
 }
 
+// ------------------------------------------------------------------ MFMA, query tile in registers
+// For query tiles of 385..512 rows.  One workgroup of 8 waves (2 per SIMD) owns
+// a (layer, request, KV head) pair and a token range.  The pair's action-query
+// tile -- rows (query n, group head g), nq*G <= 512 of them, head_dim 128,
+// bf16/fp16 -- is split over 8 row groups of 64 rows: each wave keeps its two
+// 32-row tiles as MFMA A operands in registers for the whole range, with their
+// accumulator seeds -lse/scale (-inf for padding rows, which then add
+// exp2(-inf) = 0) as the C operand of each chain's first MFMA.
+//
+// K streams through LDS in chunks of CH tokens, double buffered: the waves load
+// chunk c+1 straight from HBM into LDS (global_load_lds_dwordx4) while they
+// multiply chunk c, and one barrier per chunk hands a chunk over.  A chunk is
+// stored as 1 KiB B fragments, [tile][k step][lane] x 16 bytes, so every
+// fragment read (ds_read_b128) is one contiguous, conflict-free 1 KiB and feeds
+// two MFMAs (one per row tile).
+//
+// v_mfma_f32_32x32x16 lane layout: lane L supplies A[L%32][8*(L/32)+j] and
+// B[8*(L/32)+j][L%32] (j < 8) and receives D[8*(r/4) + 4*(L/32) + r%4][L%32] in
+// register r < 16.  Rows are ordered (n, g); with G = 4 each aligned group of
+// four rows is one query's four group heads, so a lane holds four queries x four
+// heads at one token: the GQA max is in-register and max_g exp(x_g) =
+// exp(max_g x_g) costs one exp per (query, token).
+//
+// Per 32-token tile a wave runs the MFMA chain of row tile 0 beside the
+// exp/max/sum of row tile 1 of the previous tile, then the chain of row tile 1
+// beside the exp/max/sum of row tile 0 and the B-fragment reads of the next
+// tile.  Per-token partial sums (one per row group and lane half) go to LDS at
+// the end of the chunk; after the next barrier the first CH threads add them in
+// a fixed order and write the running means.
+template <typename T, typename V8, int G, bool CAUSAL>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
+  constexpr int NW = 8, RG = 8, TG = NW / RG, KS = 8, QG = 4 / G;
+  constexpr int TPC = QREG_CHUNK / 32;  // 32-token tiles per chunk
+  constexpr int CH = QREG_CHUNK;        // tokens per chunk
+  constexpr int NT = TPC / TG;          // tiles per wave per chunk
+  constexpr int LPW = TPC * KS / NW;    // fragment loads per wave per chunk
+  constexpr int NRED = 2 * RG;          // partial sums per token
+  static_assert(KS % LPW == 0, "a wave's loads stay within one tile");
+  // the two K buffers are distinct arrays: the compiler then knows that reads of
+  // one need not wait for the loads in flight into the other
+  __shared__ __attribute__((aligned(16))) unsigned char kbuf_a[TPC * KS * 1024];
+  __shared__ __attribute__((aligned(16))) unsigned char kbuf_b[TPC * KS * 1024];
+  __shared__ float red[2][NRED][CH];
+  __shared__ int bts[MFMA_MAX_TOKENS / 16];
+
+  // XCD-aware work mapping: all token ranges of one (layer, request, head)
+  // pair land on the same XCD (blockIdx % 8), so its query tile is fetched
+  // from HBM into that XCD's L2 once.
+  const int bid = blockIdx.x;
+  const int xcd = bid & 7, jj = bid >> 3;
+  const int p = (jj / cpp) * 8 + xcd;
+  const int chunk = jj % cpp;
+  if (p >= pairs) return;
+  const int h = p % a.Hkv;
+  const int r = (p / a.Hkv) % a.R;
+  const int l = p / (a.Hkv * a.R);
+  const int S = seq_len_of(a, r);
+  const int t_begin = chunk * tpw;
+  if (t_begin >= S) return;
+  const int t_end = min(t_begin + tpw, S);
+  const int nq_all = a.n_valid ? min(max(a.n_valid[r], 0), a.N) : a.N;
+  const int nq = min(max(nq_all - a.qc0, 0), a.qcn);
+  if (nq <= 0) return;
+  const int n0 = a.n_seen[r] + min(nq_all, a.qc0);
+  const int BS = a.BS;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int lcol = lane & 31, lh = lane >> 5;
+  const int rg = wave % RG, tg = wave / RG;
+  const bool active = rg * 64 < nq * G;  // this wave's rows hold at least one query row
+
+  // ---- set-up: every load goes out before the first wait
+  const int b0 = t_begin >> bs_shift;
+  const int nbt = ((t_end - 1) >> bs_shift) - b0 + 1;  // <= 512: one entry per thread
+  const int bt_own = a.bt[(int64_t)r * a.bt_sr + b0 + min(tid, nbt - 1)];
+  V8 af[2][KS];
+  f32x16 seed[2];
+  int lim[2][4][QG];
+  {
+    const T *qbase = (const T *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr;
+    const float *lbase = a.lse + (int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr;
+    const float inv_scale = 1.0f / a.scale;
+    // unconditional loads at clamped rows: no branch serialises them
+#pragma unroll
+    for (int jt = 0; jt < 2; ++jt) {
+      const int row = rg * 64 + jt * 32 + lcol;
+      const int n = row / G, g = row % G;
+      const T *qp = qbase + (int64_t)(a.qc0 + min(n, nq - 1)) * a.q_sn + (int64_t)(h * G + g) * a.q_sh + lh * 8;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const V8 v = *(const V8 *)(qp + ks * 16);
+        af[jt][ks] = n < nq ? v : (V8)(T)0;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int rw = rg * 64 + jt * 32 + 8 * i + 4 * lh + j;
+          const int nn = rw / G, gg = rw % G;
+          const float v = lbase[(int64_t)(a.qc0 + min(nn, nq - 1)) * a.lse_sn + h * G + gg];
+          seed[jt][4 * i + j] = nn < nq ? -v * inv_scale : -INFINITY;
+        }
+        if constexpr (CAUSAL) {
+#pragma unroll
+          for (int qg = 0; qg < QG; ++qg) {
+            const int nn = (rg * 64 + jt * 32 + 8 * i + 4 * lh + qg * G) / G;
+            const int v = a.kv_len[(int64_t)r * a.N + a.qc0 + min(nn, nq - 1)];
+            lim[jt][i][qg] = nn < nq ? v : 0;
+          }
+        }
+      }
+    }
+  }
+  if (tid < nbt) bts[tid] = (bt_own >= 0 && bt_own < a.num_blocks) ? bt_own : -1;
+  __syncthreads();
+
+  const T *kbase = (const T *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh + lh * 8;
+  const float c2 = a.scale * 1.4426950408889634f;
+  float *obase = a.out + (int64_t)l * a.out_sl + (int64_t)r * a.out_sr + (int64_t)h * a.out_sh;
+  const float fn0 = (float)n0, fden = (float)(n0 + nq);
+  const int ld_tile = (wave * LPW) / KS, ld_ks = (wave * LPW) % KS;
+
+  // This wave's share of a chunk: LPW B fragments of tile ld_tile, HBM -> LDS
+  // (lane i of a global_load_lds_dwordx4 writes bytes [16i, 16i+16) of the 1 KiB
+  // fragment).  A token past t_end, or in a block the table marks invalid, reads
+  // row 0 of block 0 instead; its score is never written.
+  auto load_chunk = [&](int cbase, unsigned char *kb) {
+    const int t = cbase + ld_tile * 32 + lcol;
+    const int bi = min((t >> bs_shift) - b0, nbt - 1);
+    int phys = bts[bi];
+    const bool ok = t < t_end && phys >= 0;
+    phys = ok ? phys : 0;
+    const int slot = ok ? (t & (BS - 1)) : 0;
+    const T *kp = kbase + (int64_t)phys * a.kv_sb + (int64_t)slot * a.kv_ss + ld_ks * 16;
+#pragma unroll
+    for (int i = 0; i < LPW; ++i)
+      __builtin_amdgcn_global_load_lds((const void *)(kp + i * 16),
+                                       (__attribute__((address_space(3))) void *)&kb[(wave * LPW + i) * 1024],
+                                       16, 0, 0);
+  };
+  auto read_b = [&](V8 (&b8)[KS], const unsigned char *kb, int tile) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) b8[ks] = *(const V8 *)(&kb[((tile * KS + ks) * 64 + lane) * 16]);
+  };
+  auto mfma8 = [&](const V8 (&a8)[KS], const V8 (&b8)[KS], const f32x16 &c) {
+    f32x16 acc = c;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if constexpr (__is_same(T, __bf16))
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a8[ks], b8[ks], acc, 0, 0, 0);
+      else
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a8[ks], b8[ks], acc, 0, 0, 0);
+    }
+    return acc;
+  };
+  // exp/max/sum of one row tile at token t: sum over this lane's 16 rows
+  auto post = [&](const f32x16 &acc, const int (&lm)[4][QG], int t) {
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float a0 = acc[4 * i], a1 = acc[4 * i + 1], a2 = acc[4 * i + 2], a3 = acc[4 * i + 3];
+      if constexpr (G == 4) {
+        const float e = __builtin_amdgcn_exp2f(vmax(vmax(a0, a1), vmax(a2, a3)) * c2);
+        if constexpr (CAUSAL) sum += t < lm[i][0] ? e : 0.f;
+        else sum += e;
+      } else if constexpr (G == 2) {
+        const float e0 = __builtin_amdgcn_exp2f(vmax(a0, a1) * c2);
+        const float e1 = __builtin_amdgcn_exp2f(vmax(a2, a3) * c2);
+        if constexpr (CAUSAL) sum += (t < lm[i][0] ? e0 : 0.f) + (t < lm[i][1] ? e1 : 0.f);
+        else sum += e0 + e1;
+      } else {
+        const float v[4] = {a0, a1, a2, a3};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e = __builtin_amdgcn_exp2f(v[j] * c2);
+          if constexpr (CAUSAL) sum += t < lm[i][j] ? e : 0.f;
+          else sum += e;
+        }
+      }
+    }
+    return sum;
+  };
+  auto compute_chunk = [&](const unsigned char *kb, int buf, int cbase) {
+    if (!active) {
+#pragma unroll
+      for (int k = 0; k < NT; ++k) red[buf][2 * rg + lh][(tg + k * TG) * 32 + lcol] = 0.f;
+      return;
+    }
+    V8 bfa[KS], bfb[KS];
+    read_b(bfa, kb, tg);
+    f32x16 acc0, acc1;
+    float s0 = 0.f, part[NT];
+#pragma unroll
+    for (int k = 0; k < NT; ++k) {
+      const int tile = tg + k * TG;
+      V8 (&cur)[KS] = (k & 1) ? bfb : bfa;
+      V8 (&nxt)[KS] = (k & 1) ? bfa : bfb;
+      acc0 = mfma8(af[0], cur, seed[0]);
+      if (k > 0) part[k - 1] = s0 + post(acc1, lim[1], cbase + (tile - TG) * 32 + lcol);
+      acc1 = mfma8(af[1], cur, seed[1]);
+      if (k + 1 < NT) read_b(nxt, kb, tile + TG);
+      s0 = post(acc0, lim[0], cbase + tile * 32 + lcol);
+      // chain 0 with the VALU work of the previous tile, chain 1 with the
+      // fragment reads of the next tile and the VALU work of chain 0
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+        if (k > 0) __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (k + 1 < NT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    part[NT - 1] = s0 + post(acc1, lim[1], cbase + (tg + (NT - 1) * TG) * 32 + lcol);
+    // stored after the loop: an LDS store waits for the chunk loads in flight
+#pragma unroll
+    for (int k = 0; k < NT; ++k) red[buf][2 * rg + lh][(tg + k * TG) * 32 + lcol] = part[k];
+  };
+  auto reduce_chunk = [&](int cbase, int buf, float old) {
+    if (tid < CH) {
+      const int t = cbase + tid;
+      if (t < t_end && bts[(t >> bs_shift) - b0] >= 0) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < NRED; ++i) s += red[buf][i][tid];
+        obase[t] = (old * fn0 + s) / fden;
+      }
+    }
+  };
+
+  const int nch = (t_end - t_begin + CH - 1) / CH;
+  const int otid = tid % CH;
+  float old = 0.f;  // running means of the chunk being multiplied (read one chunk ahead)
+  auto step = [&](int c, const unsigned char *kcur, unsigned char *knext) {
+    const int cbase = t_begin + c * CH;
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's share of chunk c is in LDS
+    __syncthreads();                     // ... and every wave's; chunk c-1 is finished
+    if (c >= 1) reduce_chunk(cbase - CH, (c - 1) & 1, old);
+    old = obase[min(cbase + otid, t_end - 1)];
+    load_chunk(cbase + CH, knext);       // past the end: harmless in-bounds rows
+    __builtin_amdgcn_sched_barrier(0);
+    compute_chunk(kcur, c & 1, cbase);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  load_chunk(t_begin, kbuf_a);
+  for (int c = 0; c < nch; c += 2) {
+    step(c, kbuf_a, kbuf_b);
+    if (c + 1 < nch) step(c + 1, kbuf_b, kbuf_a);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);    // no load into LDS outlives the workgroup
+  __syncthreads();
+  reduce_chunk(t_begin + (nch - 1) * CH, (nch - 1) & 1, old);
+}
+
 __global__ void bump_n_seen_kernel(int32_t *n_seen, const int32_t *n_valid, int R, int N) {
   const int r = blockIdx.x * blockDim.x + threadIdx.x;
   if (r < R) n_seen[r] += n_valid ? min(max(n_valid[r], 0), N) : N;
@@ -394,15 +664,15 @@ static int device_cus() {
   return cus[dev];
 }
 
-// Token range per workgroup of the MFMA kernel.  One workgroup fills a CU (its
+// Token range per workgroup of the K-slice kernel.  One workgroup fills a CU (its
 // query tile takes most of the LDS), so the grid is sized in waves of CU-count
 // workgroups: as many waves as keep every wave at least MIN_SLICES 32-token
 // slices per wave of the workgroup, at most MAX_WAVES (each workgroup re-stages
 // its query tile; fewer, larger workgroups amortise that), and the token range
 // split evenly over the chunks of a pair.  A small problem -- one layer of one
 // request -- thus still spreads over every CU.
-static int mfma_tokens_per_wg(int pairs, int span, int nw) {
-  constexpr int MIN_SLICES = 2, MAX_WAVES = 8, MAX_TOKENS = 8192;  // 8192: the block-table slice
+static int kslice_tokens_per_wg(int pairs, int span, int nw) {
+  constexpr int MIN_SLICES = 2, MAX_WAVES = 8, MAX_TOKENS = MFMA_MAX_TOKENS;
   const int64_t cus = device_cus();
   const int64_t spp = (span + 31) / 32;                       // slices per pair
   const int64_t total = (int64_t)pairs * spp;
@@ -413,36 +683,71 @@ static int mfma_tokens_per_wg(int pairs, int span, int nw) {
   return (int)(per * 32);
 }
 
+// Token range per workgroup of the query-tile kernel: a whole number of chunks.  One
+// workgroup fills a CU, so the launch runs in rounds of CU-count workgroups, and
+// each workgroup pays a set-up (block-table slice, query tile, first chunk) of
+// about SETUP chunks before its pipeline runs.  The range minimises
+// rounds x (SETUP + chunks per workgroup): one layer of one request spreads over
+// every CU, 36 layers run 9 full rounds of 4096 tokens.
+static int qreg_tokens_per_wg(int pairs, int span) {
+  constexpr double SETUP = 1.5;  // measured: ~5 us against ~3.7 us per 512-row chunk
+  constexpr int chunk = QREG_CHUNK;
+  const int64_t cus = device_cus();
+  const int span_chunks = (span + chunk - 1) / chunk;
+  const int max_chunks = std::min(span_chunks, MFMA_MAX_TOKENS / chunk);
+  int best = 1;
+  double best_cost = 0.0;
+  for (int k = 1; k <= max_chunks; ++k) {
+    const int64_t items = (int64_t)pairs * ((span_chunks + k - 1) / k);
+    const double cost = (double)((items + cus - 1) / cus) * (SETUP + k);
+    if (k == 1 || cost < best_cost) { best_cost = cost; best = k; }
+  }
+  return best * chunk;
+}
+
 template <typename T, typename V8, int G>
 static int launch_mfma(const ScoreArgs &a0, int bs_shift, hipStream_t st) {
   const int pairs = a0.L * a0.R * a0.Hkv;
   const int span = a0.max_blocks * a0.BS;
-  const int q_per_launch = 512 / G;  // LDS holds at most 512 query rows (128 KiB)
+  const int q_per_launch = 512 / G;  // both kernels take at most 512 query rows
   const bool causal = a0.kv_len != nullptr;
   for (int qc0 = 0; qc0 < a0.N; qc0 += q_per_launch) {
     ScoreArgs a = a0;
     a.qc0 = qc0;
     a.qcn = std::min(q_per_launch, a0.N - qc0);
     const int rows = a.qcn * G;
-    // NW waves (NW/4 per SIMD: 3 keeps the VALU post-processing overlapped with
-    // the matrix core), 32-token slices dealt round-robin to the waves.
-    constexpr int NW = 12, TT = 1;
-    const int tpw = mfma_tokens_per_wg(pairs, span, NW);
-    const int cpp = (span + tpw - 1) / tpw;
-    const int grid = ((pairs + 7) / 8) * 8 * cpp;
+    if (rows > 384) {
+      // the matrix cores bound the call: query tile in registers, K shared through LDS
+      const int tpw = qreg_tokens_per_wg(pairs, span);
+      const int cpp = (span + tpw - 1) / tpw;
+      const int grid = ((pairs + 7) / 8) * 8 * cpp;
+      if (causal)
+        hipLaunchKernelGGL((score_qreg_kernel<T, V8, G, true>), dim3(grid), dim3(512), 0, st, a, tpw, cpp,
+                           pairs, bs_shift);
+      else
+        hipLaunchKernelGGL((score_qreg_kernel<T, V8, G, false>), dim3(grid), dim3(512), 0, st, a, tpw, cpp,
+                           pairs, bs_shift);
+    } else {
+      // fewer rows: 12 waves stream their own K slices against the tile in LDS,
+      // which keeps more K in flight (measured faster up to 384 rows)
+      constexpr int NW = 12, TT = 1;
+      const int tpw = kslice_tokens_per_wg(pairs, span, NW);
+      const int cpp = (span + tpw - 1) / tpw;
+      const int grid = ((pairs + 7) / 8) * 8 * cpp;
 #define ACTKV_LAUNCH(ROWSV)                                                                        \
   do {                                                                                             \
     if (causal)                                                                                    \
-      hipLaunchKernelGGL((score_mfma_kernel<T, V8, G, ROWSV, true, NW, TT>), dim3(grid),           \
+      hipLaunchKernelGGL((score_kslice_kernel<T, V8, G, ROWSV, true, NW, TT>), dim3(grid),         \
                          dim3(NW * 64), 0, st, a, tpw, cpp, pairs, bs_shift);                      \
     else                                                                                           \
-      hipLaunchKernelGGL((score_mfma_kernel<T, V8, G, ROWSV, false, NW, TT>), dim3(grid),          \
+      hipLaunchKernelGGL((score_kslice_kernel<T, V8, G, ROWSV, false, NW, TT>), dim3(grid),        \
                          dim3(NW * 64), 0, st, a, tpw, cpp, pairs, bs_shift);                      \
   } while (0)
-    if (rows <= 128) ACTKV_LAUNCH(128);
-    else if (rows <= 256) ACTKV_LAUNCH(256);
-    else ACTKV_LAUNCH(512);
+      if (rows <= 128) ACTKV_LAUNCH(128);
+      else if (rows <= 256) ACTKV_LAUNCH(256);
+      else ACTKV_LAUNCH(512);
 #undef ACTKV_LAUNCH
+    }
     int rc = actkv_check_launch();
     if (rc) return rc;
   }

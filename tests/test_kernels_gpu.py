@@ -87,7 +87,10 @@ def test_action_scores_matches_oracle(lens, hq, hkv, d, bs, dtype):
 
 @pytest.mark.parametrize("n_q,hq,hkv,dtype", [(37, 32, 8, torch.bfloat16), (129, 32, 8, torch.bfloat16),
                                               (40, 16, 8, torch.float16), (9, 6, 3, torch.float32),
-                                              (300, 16, 8, torch.float16), (600, 8, 8, torch.bfloat16)])
+                                              (300, 16, 8, torch.float16), (600, 8, 8, torch.bfloat16),
+                                              # 320, 400 and 512 query rows: both MFMA kernels
+                                              (80, 32, 8, torch.bfloat16), (100, 32, 8, torch.bfloat16),
+                                              (128, 32, 8, torch.float16)])
 def test_action_scores_n_queries_in_one_launch(n_q, hq, hkv, dtype):
     """N action tokens folded by one call == N reference folds (additive extension)."""
     lens = [200, 1000, 17]
@@ -279,9 +282,10 @@ def test_evict_keeps_the_protected_tokens_across_repeated_evictions():
 @pytest.mark.parametrize("dtype,hq,hkv,d,bs,n_q", [
     (torch.bfloat16, 32, 8, 128, 16, 23), (torch.float16, 16, 8, 128, 32, 23),
     (torch.bfloat16, 8, 8, 128, 16, 23), (torch.float32, 6, 3, 24, 8, 23),
-    # query tiles of more than 256 rows (the query-stationary kernel)
+    # query tiles of 385..512 rows (query tile in registers) and 257..384 rows (K slices)
     (torch.bfloat16, 32, 8, 128, 16, 100), (torch.float16, 16, 8, 128, 16, 150),
-    (torch.bfloat16, 8, 8, 128, 16, 300)])
+    (torch.bfloat16, 8, 8, 128, 16, 300), (torch.float16, 32, 8, 128, 16, 128),
+    (torch.bfloat16, 16, 8, 128, 64, 200)])
 def test_action_scores_causal_region_and_ragged_query_counts(dtype, hq, hkv, d, bs, n_q):
     """kv_len (query n sees tokens t < kv_len[r, n]) and n_valid (request r folds its first
     n_valid[r] queries): the causal action region of an agent round (additive extension)."""

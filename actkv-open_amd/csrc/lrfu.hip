@@ -56,42 +56,47 @@ __device__ double block_sum_f64(double v, double *scratch) {
   return tot;
 }
 
-// Walk nb bins from the top (bin nb-1 first) with running float64 sum `base`:
-// find the first bin where the rounded running sum reaches thr.  Thread i owns
-// bins nb-1-2i and nb-2-2i.  Returns the bin (or -1 if the sum never reaches
-// thr); *above = base + sum of the bins above it.
-__device__ int crossing_bin(const uint32_t *cnt, const double *sum, int nb, double base, float thr,
-                            double *above, double *scratch_d, int *found) {
+// Walk nb bins from the top (bin nb-1 first) with running sum `base`: find the first
+// bin where the running sum, scaled back by qinv and rounded to float32, reaches thr.
+// Sums are fixed-point integers (see lrfu_update_kernel), so every order of
+// accumulation gives the same bits.  Thread i owns bins nb-1-2i and nb-2-2i.
+// Returns the bin (or -1 if the sum never reaches thr); *above = base + sum of the
+// bins above it.
+typedef unsigned long long u64;
+__device__ __forceinline__ float fixed_to_f32(u64 x, double qinv) { return (float)((double)x * qinv); }
+
+__device__ int crossing_bin(const uint32_t *cnt, const u64 *sum, int nb, u64 base, float thr, double qinv,
+                            u64 *above, u64 *scratch_q, int *found) {
   const int per = nb / LT;  // 2 or 1
   const int top = nb - 1 - (int)threadIdx.x * per;
-  double s = 0.0;
+  u64 s = 0;
   for (int j = 0; j < per; ++j) s += sum[top - j];
   // inclusive scan over threads in descending-bin order
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  double inc = s;
+  u64 inc = s;
   for (int o = 1; o < 64; o <<= 1) {
-    const double v = __shfl_up(inc, o, 64);
+    const u64 v = __shfl_up(inc, o, 64);
     if (lane >= o) inc += v;
   }
   if (threadIdx.x == 0) *found = -1;
   __syncthreads();
-  if (lane == 63) scratch_d[w] = inc;
+  if (lane == 63) scratch_q[w] = inc;
   __syncthreads();
-  double before = base;
-  for (int i = 0; i < w; ++i) before += scratch_d[i];
-  double run = before + inc - s;  // everything above my bins
+  u64 before = base;
+  for (int i = 0; i < w; ++i) before += scratch_q[i];
+  u64 run = before + inc - s;  // everything above my bins
   for (int j = 0; j < per; ++j) {
     const int b = top - j;
-    const double next = run + sum[b];
-    if (cnt[b] != 0 && (float)run < thr && (float)next >= thr) {
+    const u64 next = run + sum[b];
+    if (cnt[b] != 0 && fixed_to_f32(run, qinv) < thr && fixed_to_f32(next, qinv) >= thr) {
       *found = b;
-      scratch_d[LT / 64] = run;
+      scratch_q[LT / 64] = run;
     }
     run = next;
   }
   __syncthreads();
   const int b = *found;
-  if (b >= 0) *above = scratch_d[LT / 64];
+  if (b >= 0) *above = scratch_q[LT / 64];
   __syncthreads();
   return b;
 }
@@ -134,8 +139,9 @@ template <int KMAX>
 __global__ void __launch_bounds__(LT) lrfu_update_kernel(LrfuArgs a) {
   constexpr bool REG = KMAX > 0;
   __shared__ uint32_t cnt[LB];
-  __shared__ double sum[LB];
-  __shared__ double scratch_d[LT / 64 + 1];
+  __shared__ u64 sum[LB];
+  __shared__ double scratch_d[LT / 64];
+  __shared__ u64 scratch_q[LT / 64 + 1];
   __shared__ uint32_t scratch_u[LT / 64];
   __shared__ int found;
   __shared__ int cut_s;
@@ -189,83 +195,91 @@ __global__ void __launch_bounds__(LT) lrfu_update_kernel(LrfuArgs a) {
   uint32_t kthr = 0xFFFFFFFFu;  // hit: key > kthr, or key == kthr and t < cut
   int cut = 0;
   if (active && S > P && total_f > 0.f) {
+    // Bin sums in fixed point: v -> floor(v * 2^(61-E)), E = the total's exponent, so
+    // every value and every sum stays below 2^62 and integer atomics add them in any
+    // order to the same bits (float64 atomics would round differently per order).
+    // Values below 2^(E-61) count as 0 in the sums; a sum is off by at most one unit per
+    // value, under 2^-46 of the total at 32k tokens, far below float32's 2^-24 at thr.
+    const int E = ilogb(total);
+    const double qscale = ldexp(1.0, 61 - E), qinv = ldexp(1.0, E - 61);
+    auto quant = [&](float v) { return (u64)((double)v * qscale); };
     // pass 1: top 11 bits
-    for (int b = tid; b < LB; b += LT) { cnt[b] = 0; sum[b] = 0.0; }
+    for (int b = tid; b < LB; b += LT) { cnt[b] = 0; sum[b] = 0; }
     __syncthreads();
     for_each([&](int t, float v) {
       if (pin && pin[t]) return;
       const uint32_t k = __float_as_uint(v);
       atomicAdd(&cnt[k >> 21], 1u);
-      atomicAdd(&sum[k >> 21], (double)v);
+      atomicAdd(&sum[k >> 21], quant(v));
     });
     __syncthreads();
-    double above;
-    const int b1 = crossing_bin(cnt, sum, LB, 0.0, thr, &above, scratch_d, &found);
+    u64 above;
+    const int b1 = crossing_bin(cnt, sum, LB, 0, thr, qinv, &above, scratch_q, &found);
     if (b1 < 0) {
       kthr = 0u;          // the sum never reaches the threshold: every positive entry
       cut = 0;
     } else {
       // pass 2: bits [20:10] within bin b1
-      for (int b = tid; b < LB; b += LT) { cnt[b] = 0; sum[b] = 0.0; }
+      for (int b = tid; b < LB; b += LT) { cnt[b] = 0; sum[b] = 0; }
       __syncthreads();
       for_each([&](int t, float v) {
         if (pin && pin[t]) return;
         const uint32_t k = __float_as_uint(v);
         if ((int)(k >> 21) == b1) {
           atomicAdd(&cnt[(k >> 10) & 2047u], 1u);
-          atomicAdd(&sum[(k >> 10) & 2047u], (double)v);
+          atomicAdd(&sum[(k >> 10) & 2047u], quant(v));
         }
       });
       __syncthreads();
-      double above2;
-      int b2 = crossing_bin(cnt, sum, LB, above, thr, &above2, scratch_d, &found);
-      // rounding of the float64 partial sums can only move the crossing by one
-      // bin; fall back to the lowest non-empty bin if it slipped past the end
+      u64 above2;
+      int b2 = crossing_bin(cnt, sum, LB, above, thr, qinv, &above2, scratch_q, &found);
+      // the sub-bins of b1 add up to b1's sum exactly, so the crossing is found; the
+      // fallback (the lowest non-empty bin) only guards the invariant
       if (b2 < 0) {
         b2 = 0;
-        above2 = above;
         for (int b = LB - 1; b >= 0; --b) {
           if (cnt[b]) { b2 = b; }
         }
-        double run = above;
+        u64 run = above;
         for (int b = LB - 1; b > b2; --b) run += sum[b];
         above2 = run;
       }
       // pass 3: bits [9:0] within (b1, b2)
       const uint32_t pre22 = ((uint32_t)b1 << 11) | (uint32_t)b2;
-      for (int b = tid; b < LB; b += LT) { cnt[b] = 0; sum[b] = 0.0; }
+      for (int b = tid; b < LB; b += LT) { cnt[b] = 0; sum[b] = 0; }
       __syncthreads();
       for_each([&](int t, float v) {
         if (pin && pin[t]) return;
         const uint32_t k = __float_as_uint(v);
         if ((k >> 10) == pre22) {
           atomicAdd(&cnt[k & 1023u], 1u);
-          atomicAdd(&sum[k & 1023u], (double)v);
+          atomicAdd(&sum[k & 1023u], quant(v));
         }
       });
       __syncthreads();
-      double above3;
-      int b3 = crossing_bin(cnt, sum, 1024, above2, thr, &above3, scratch_d, &found);
+      u64 above3;
+      int b3 = crossing_bin(cnt, sum, 1024, above2, thr, qinv, &above3, scratch_q, &found);
       if (b3 < 0) {
         b3 = 0;
         for (int b = 1023; b >= 0; --b) {
           if (cnt[b]) { b3 = b; }
         }
-        double run = above2;
+        u64 run = above2;
         for (int b = 1023; b > b3; --b) run += sum[b];
         above3 = run;
       }
       kthr = (pre22 << 10) | (uint32_t)b3;
       // ties at the crossing value: the j smallest indices, j = first count at which
-      // the running float64 sum, rounded to float32, reaches thr
+      // the running sum, rounded to float32, reaches thr
       const float vstar = __uint_as_float(kthr);
+      const u64 qstar = quant(vstar);
       const uint32_t ties = cnt[b3];
       uint32_t need = ties;
       {
-        double run = above3;
+        u64 run = above3;
         for (uint32_t j = 1; j <= ties; ++j) {
-          run += (double)vstar;
-          if ((float)run >= thr) { need = j; break; }
+          run += qstar;
+          if (fixed_to_f32(run, qinv) >= thr) { need = j; break; }
         }
       }
       // ordered scan for the index just past the need-th tie: round j covers tokens

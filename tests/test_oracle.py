@@ -160,20 +160,26 @@ def test_nfold_with_ragged_counts_and_causal_limits_matches_brute_force():
     assert n_seen.tolist() == [4, 2]
 
 
-@pytest.mark.parametrize("mutant", ["mean_over_group", "no_scale", "fold_denominator"])
+@pytest.mark.parametrize("mutant", ["mean_over_group", "sum_over_group", "no_lse", "no_scale",
+                                    "fold_denominator"])
 def test_a_planted_scoring_mistake_is_caught(monkeypatch, mutant):
     """Each mutant restates one plausible mistake; the brute-force check must reject it."""
     orig = ref._group_probs
 
-    def mean_over_group(q_r, k, lse_r, scale):
+    def group_probs(q_r, k, lse_r, scale, reduce="amax", use_lse=True):
         hkv = k.shape[1]
         g = q_r.shape[0] // hkv
         kk = k.float().repeat_interleave(g, dim=1)
-        p = torch.exp(torch.einsum("hd,shd->hs", q_r.float(), kk) * scale - lse_r.unsqueeze(-1))
-        return p.view(hkv, g, -1).mean(1)
+        logits = torch.einsum("hd,shd->hs", q_r.float(), kk) * scale
+        p = torch.exp(logits - lse_r.unsqueeze(-1) if use_lse else logits)
+        return getattr(p.view(hkv, g, -1), reduce)(1)
 
     if mutant == "mean_over_group":
-        monkeypatch.setattr(ref, "_group_probs", mean_over_group)
+        monkeypatch.setattr(ref, "_group_probs", lambda q, k, l, s: group_probs(q, k, l, s, "mean"))
+    elif mutant == "sum_over_group":
+        monkeypatch.setattr(ref, "_group_probs", lambda q, k, l, s: group_probs(q, k, l, s, "sum"))
+    elif mutant == "no_lse":
+        monkeypatch.setattr(ref, "_group_probs", lambda q, k, l, s: group_probs(q, k, l, s, use_lse=False))
     elif mutant == "no_scale":
         monkeypatch.setattr(ref, "_group_probs", lambda q, k, l, s: orig(q, k, l, 1.0))
     else:

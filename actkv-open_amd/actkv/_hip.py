@@ -110,6 +110,10 @@ def lib() -> ctypes.CDLL:
         for name, (res, args) in _SIGNATURES.items():
             fn = getattr(handle, name)
             fn.restype, fn.argtypes = res, args
+        # the HIP runtime the library links (torch's copy), reached through the library's own
+        # dependency scope; the upload ring queues its host-to-device copies with it
+        cp = handle.hipMemcpyAsync
+        cp.restype, cp.argtypes = _c_i32, [_c_p, _c_p, _c_sz, _c_i32, _c_p]
         _lib = handle
     return _lib
 
@@ -168,13 +172,16 @@ def stream(device: torch.device) -> int:
 
 
 _workspaces: dict = {}
+_HIP_MEMCPY_H2D = 1      # hipMemcpyHostToDevice
 
 
 class _PinnedRing:
     """Host-to-device int32 uploads through one pinned staging buffer, used as a ring.
 
-    Each upload copies into the next free span of the buffer and queues an asynchronous copy
-    from it.  The buffer is split in two halves: leaving a half records an event after its last
+    Each upload copies into the next free span of the buffer, takes a fresh device tensor from
+    torch's caching allocator and queues hipMemcpyAsync from the span into it (called directly:
+    torch's own non-blocking copy also records a host-allocator event per call, which the ring
+    makes unnecessary and which costs several microseconds).  The buffer is split in two halves: leaving a half records an event after its last
     copy, and coming back to that half waits for that event, so no span is rewritten before its
     copy has run.  One event per half-buffer of uploads (thousands of calls), instead of one per
     upload (an event record costs a current-stream lookup, several microseconds).  Uploads larger
@@ -219,7 +226,12 @@ class _PinnedRing:
             self.streams[h] = set()
         self.streams[h].add(cur)
         self.np[self.off:self.off + n] = arr
-        out = self.buf[self.off:self.off + n].to(device, non_blocking=True)
+        out = torch.empty(n, dtype=torch.int32, device=device)
+        if n:
+            rc = lib().hipMemcpyAsync(out.data_ptr(), self.buf.data_ptr() + 4 * self.off, 4 * n,
+                                      _HIP_MEMCPY_H2D, cur)
+            if rc != 0:
+                raise RuntimeError(f"hipMemcpyAsync (host to device, {4 * n} bytes) failed with HIP error {rc}")
         self.off += n
         return out
 

@@ -209,6 +209,7 @@ class PagedKVCache:
         self.device = device
         self._pin_count: dict[int, tuple] = {}      # req -> (tensor, version, count): avoids a sync
         self._dev_cache: dict = {}                  # device copies of unchanged block tables
+        self._const_cache: dict = {}                # device copies of budget / protected-count lists
 
     # ---------------------------------------------------------------- allocation
     @property
@@ -386,6 +387,17 @@ class PagedKVCache:
         self._dev_cache[key] = (tabs, stamp, seq, bt)
         return seq, bt
 
+    def _device_consts(self, values: tuple) -> torch.Tensor:
+        """int32 device tensor holding `values`, shared by every call with the same values.
+        Only for kernel inputs the kernels never write (budgets, protected counts): an
+        eviction loop with fixed budgets then uploads nothing per call."""
+        t = self._const_cache.get(values)
+        if t is None:
+            if len(self._const_cache) > 256:
+                self._const_cache.clear()
+            t = self._const_cache[values] = self._upload(np.array(values, dtype=np.int32))
+        return t
+
     def block_table(self, reqs: list[int]) -> torch.Tensor:
         host, mb = self._host_tables(reqs)
         return self._upload(host[len(reqs):]).view(len(reqs), mb)
@@ -472,9 +484,9 @@ class PagedKVCache:
         for i, r in enumerate(reqs):
             drop = ys[i] - math.ceil(kept[i] / bs)
             table = self.tables[r]
-            freed = table[:drop]
+            if drop > 0:                      # freed blocks pushed last-first: table[drop-1], ..., table[0]
+                self.free.extend(table[drop - 1::-1])
             self.tables[r] = table.tail(drop) if isinstance(table, _Table) else table[drop:]
-            self.free.extend(reversed(freed))
             self.seq_used[r] = kept[i]
         return perm, pin_out
 
@@ -609,9 +621,12 @@ class PagedKVCache:
         if sc.stride(-1) != 1:
             sc = sc.contiguous()
         L, _, H, _ = sc.shape
-        params = upload_i32(seqs + [max(budgets[i], 0) for i in active] + counts, dev)
+        # the lengths come with the block tables the compaction launch reads anyway; budgets and
+        # protected counts are the same from call to call in an eviction loop
+        seq_dev, _ = self._device_tables(a_reqs)
+        consts = self._device_consts(tuple(max(budgets[i], 0) for i in active) + tuple(counts))
         if all(p is None for p in pinneds):           # every request's pins are a prefix count
-            pin_mat, prot_count = None, params[2 * ra:]
+            pin_mat, prot_count = None, consts[ra:]
         else:
             prot_count = None
             if ra == 1:
@@ -624,7 +639,7 @@ class PagedKVCache:
                     else:
                         pin_mat[j, : p.numel()] = p
         _, bits = _keep_mask_launch(sc, L, H, sc.stride(0), sc.stride(1), sc.stride(2), ra,
-                                    params[:ra], params[ra:2 * ra], prot_count, pin_mat,
+                                    seq_dev, consts[:ra], prot_count, pin_mat,
                                     0 if pin_mat is None else pin_mat.stride(0),
                                     head_reduce, self.block_size, smax, dev, want_keep=False)
         perm, pin_out = self._compact_launch(a_reqs, bits, kept, pin_mat, prot_count)

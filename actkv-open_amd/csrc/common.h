@@ -65,6 +65,39 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Inclusive scan of a uint32 over the 64 lanes of a wave with DPP lane moves, which stay in
+// the VALU (a shuffle is an LDS-pipe permute with LDS latency per step): shifts by 1, 2, 4
+// and 8 lanes within each 16-lane row, then the last lane of rows 0 and 2 added into rows 1
+// and 3, then lane 31 added into rows 2 and 3.  Lanes whose source is outside the row, or
+// whose row the step leaves out, take `ident` (the identity of the associative `op`).
+// Lane 63 ends with the whole wave's result.  Every lane of the wave must be active.
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v, uint32_t ident, Op op) {
+  const int id = (int)ident;
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x111, 0xf, 0xf, false));  // row_shr:1
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x112, 0xf, 0xf, false));  // row_shr:2
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x114, 0xf, 0xf, false));  // row_shr:4
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x118, 0xf, 0xf, false));  // row_shr:8
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x142, 0xa, 0xf, false));  // row_bcast:15
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x143, 0xc, 0xf, false));  // row_bcast:31
+  return v;
+}
+
+struct OpAdd { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a + b; } };
+struct OpMin { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a < b ? a : b; } };
+struct OpMax { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; } };
+
+// The whole wave's sum / min / max, in every lane.
+__device__ __forceinline__ uint32_t wave_total_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)wave_scan_u32(v, 0u, OpAdd()), 63);
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)wave_scan_u32(v, 0xFFFFFFFFu, OpMin()), 63);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)wave_scan_u32(v, 0u, OpMax()), 63);
+}
+
 }  // namespace actkv
 
 // Returns ACTKV_ERR_LAUNCH if the last launch failed.

@@ -51,8 +51,8 @@ struct CompactArgs {
 };
 
 // Exclusive scan of popcounts of words[0..nw) into pre[0..nw]; pre[nw] = total.
-// Each thread sums a contiguous run of words; runs are scanned with wave
-// shuffles and one LDS pass over the CT/64 wave totals.
+// Each thread sums a contiguous run of words; runs are scanned with DPP wave
+// scans and one LDS pass over the CT/64 wave totals.
 __device__ void scan_words(const uint32_t *words, uint32_t *pre, int nw) {
   __shared__ uint32_t wsum[CT / 64];
   const int per = (nw + CT - 1) / CT;
@@ -60,11 +60,7 @@ __device__ void scan_words(const uint32_t *words, uint32_t *pre, int nw) {
   uint32_t s = 0;
   for (int w = lo; w < hi; ++w) s += __popc(words[w]);
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  uint32_t inc = s;
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t v = __shfl_up(inc, o, 64);
-    if (lane >= o) inc += v;
-  }
+  const uint32_t inc = wave_scan_u32(s, 0u, OpAdd());
   if (lane == 63) wsum[wv] = inc;
   __syncthreads();
   uint32_t run = inc - s;

@@ -9,8 +9,8 @@
 //   select : one 1024-thread block per request, its keys in LDS (chunks of
 //            32768 tokens beyond that).  Finds the exact k-th
 //            largest key by narrowing a window of key values (2048 bins per
-//            pass over the candidates' own range, the window's candidates in LDS
-//            once they fit), and the index cut among tied keys (lower index
+//            pass over the candidates' own range; past one chunk, the window's
+//            candidates in LDS once they fit), and the index cut among tied keys (lower index
 //            wins), then writes
 //            keep[t] = protected | key > thr | (key == thr & t < cut),
 //            packed LSB-first into 32-bit words for actkv_compact too.
@@ -29,6 +29,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 namespace actkv {
 
@@ -85,17 +86,16 @@ constexpr int KCHUNK = 32768;
 __device__ __forceinline__ void load_chunk(uint32_t *skeys, const uint32_t *keys, int c0, int n) {
   const int n4 = n >> 2;
   const uint4 *src = (const uint4 *)(keys + c0);   // c0 % 4 == 0, rows 16-byte aligned
-  constexpr int U = 4;                             // 16-byte loads in flight per thread (in-bounds
+  constexpr int U = 8;                             // 16-byte loads in flight per thread: 32768
+                                                   // keys in one round with 1024 threads (in-bounds
                                                    // clamped reads past n4 are not stored)
   for (int i = threadIdx.x; i < n4; i += U * blockDim.x) {
-    uint4 v0 = src[i];                                            // i < n4
-    uint4 v1 = src[min(i + (int)blockDim.x, n4 - 1)];
-    uint4 v2 = src[min(i + 2 * (int)blockDim.x, n4 - 1)];
-    uint4 v3 = src[min(i + 3 * (int)blockDim.x, n4 - 1)];
-    ((uint4 *)skeys)[i] = v0;
-    if (i + (int)blockDim.x < n4) ((uint4 *)skeys)[i + blockDim.x] = v1;
-    if (i + 2 * (int)blockDim.x < n4) ((uint4 *)skeys)[i + 2 * blockDim.x] = v2;
-    if (i + 3 * (int)blockDim.x < n4) ((uint4 *)skeys)[i + 3 * blockDim.x] = v3;
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = src[min(i + u * (int)blockDim.x, n4 - 1)];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i + u * (int)blockDim.x < n4) ((uint4 *)skeys)[i + u * blockDim.x] = v[u];
   }
   for (int i = 4 * n4 + threadIdx.x; i < n; i += blockDim.x) skeys[i] = keys[c0 + i];
 }
@@ -142,37 +142,68 @@ __device__ __forceinline__ void visit_keys(uint32_t *skeys, const uint32_t *keys
   }
 }
 
+// Count the keys of an LDS-resident request (S <= KCHUNK) that fall in the
+// window [base, base + 2^wbits), wbits <= 21, into hist[(key - base) >> sh].
+// For a narrow window: each thread tests its keys 32 at a time and issues LDS
+// atomics only for the few inside, so a wave makes a handful of atomic
+// instructions instead of one per key slot (each costs LDS pipe time however
+// few lanes it carries).  Called by every thread of the block.
+__device__ __forceinline__ void count_window_sparse(const uint32_t *skeys, int S, uint32_t base, int wbits,
+                                                    int sh, uint32_t *hist) {
+  const int n4 = S >> 2;
+  const uint4 *k4 = (const uint4 *)skeys;
+  const uint32_t width = 1u << wbits;
+  auto in = [&](uint32_t key) -> uint32_t { return (uint32_t)((key != 0u) & (key - base < width)); };
+  constexpr int U = 8;
+  for (int i0 = 0; i0 < n4; i0 += U * blockDim.x) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * blockDim.x + threadIdx.x;
+      const uint4 v = i < n4 ? k4[i] : make_uint4(0u, 0u, 0u, 0u);
+      m |= (in(v.x) | (in(v.y) << 1) | (in(v.z) << 2) | (in(v.w) << 3)) << (4 * u);
+    }
+    while (m) {
+      const int j = __builtin_ctz(m);
+      m &= m - 1;
+      const uint32_t key = skeys[4 * (i0 + (j >> 2) * blockDim.x + threadIdx.x) + (j & 3)];
+      atomicAdd(&hist[(key - base) >> sh], 1u);
+    }
+  }
+  for (int t = 4 * n4 + threadIdx.x; t < S; t += blockDim.x) {
+    const uint32_t key = skeys[t];
+    if (in(key)) atomicAdd(&hist[(key - base) >> sh], 1u);
+  }
+}
+
 // Bit width of x (0 for x == 0).
 __device__ __forceinline__ int bit_width(uint32_t x) { return x ? 32 - __clz(x) : 0; }
 
-// Inclusive scan over a wave.
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
-  const int lane = threadIdx.x & 63;
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint32_t u = __shfl_up(v, o, 64);
-    if (lane >= o) v += u;
-  }
-  return v;
-}
-
 // The bin holding the k-th largest element of hist[nbins] (LDS), 1 <= k <= total,
-// in two barriers; *need = k - (elements in the bins above it).  Thread i owns
-// nbins/blockDim bins from the top; wave scans and the per-wave totals give each
-// thread its exclusive count, and the one thread whose bins cross k resolves the
-// bin.  Between the barriers it clears clear[0, nclear) (the next pass's counts).
+// in two barriers; *need = k - (elements in the bins above it).  Thread i of the
+// NT-thread block owns nbins/NT bins from the top; DPP wave scans and the per-wave
+// totals (wtot, 16-byte aligned, NT/64 entries) give each thread its exclusive
+// count, and the one thread whose bins cross k resolves the bin.  Between the
+// barriers it clears clear[0, nclear) (the next pass's counts).
+template <int NT>
 __device__ int find_bin(const uint32_t *hist, int nbins, uint32_t k, uint32_t *need, uint32_t *wtot,
                         uint32_t *found, uint32_t *clear, int nclear) {
-  const int per = nbins / (int)blockDim.x;
+  static_assert(NT % 256 == 0 && NT <= 1024, "wave totals are read four at a time");
+  const int per = nbins / NT;
   const int top = nbins - 1 - (int)threadIdx.x * per;
   uint32_t c = 0;
   for (int j = 0; j < per; ++j) c += hist[top - j];
-  const uint32_t inc = wave_incl_scan(c);
+  const uint32_t inc = wave_scan_u32(c, 0u, OpAdd());
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   if (lane == 63) wtot[w] = inc;
-  for (int i = threadIdx.x; i < nclear; i += blockDim.x) clear[i] = 0;
+  for (int i = threadIdx.x; i < nclear; i += NT) clear[i] = 0;
   __syncthreads();
   uint32_t before = 0;
-  for (int i = 0; i < w; ++i) before += wtot[i];
+#pragma unroll
+  for (int q = 0; q < NT / 64; q += 4) {
+    const uint4 x = *(const uint4 *)(wtot + q);
+    before += (q < w ? x.x : 0u) + (q + 1 < w ? x.y : 0u) + (q + 2 < w ? x.z : 0u) + (q + 3 < w ? x.w : 0u);
+  }
   const uint32_t excl = before + inc - c;   // elements in the bins above my range
   if (excl < k && excl + c >= k) {
     uint32_t above = excl;
@@ -199,40 +230,68 @@ __device__ int find_bin(const uint32_t *hist, int nbins, uint32_t k, uint32_t *n
 // when the scores are concentrated (an average over many layers, heads and
 // queries), which keeps the LDS atomics of the counting pass apart.  Once the
 // window's candidates fit in LDS they are gathered there and the remaining
-// passes touch only them.  The passes are arranged for few block barriers: the
-// next pass's counts are cleared inside the bin search, counters are set before
-// the first barrier.
+// passes touch only them.
+//
+// A request of up to KCHUNK tokens is resident: thread i holds the keys of
+// tokens j*SEL_T + i (j < KPT) in registers, loaded while the statistics are
+// reduced, and a token-ordered copy in LDS for the walks that go by index (the
+// gather's read-back, ties, a window too wide to gather, the mask).  The first
+// pass and the gather test the register keys; the mask is written with one
+// ballot per 64 consecutive tokens, i.e. two whole words per wave.  The
+// selection is bound by the VALU work per key on one CU, so each key is tested
+// with as few operations as the case allows.  A longer request walks its keys
+// from memory in LDS chunks.  The passes are arranged for few block barriers:
+// the next pass's counts are cleared inside the bin search, counters are set
+// before the first barrier.
+constexpr int KPT = KCHUNK / SEL_T;     // keys per thread of a resident request
+
 __global__ void __launch_bounds__(SEL_T) keep_select_kernel(KeepArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t skeys[KCHUNK];
   __shared__ uint32_t hist_a[HIST_BINS], hist_b[HIST_BINS];
   __shared__ uint2 cand[CAND_CAP];
-  __shared__ uint32_t red[3][SEL_T / 64], wtot[SEL_T / 64], found[2];
+  __shared__ uint32_t red[3][SEL_T / 64], found[2];
+  __shared__ __attribute__((aligned(16))) uint32_t wtot[SEL_T / 64];
   __shared__ int ncand_s, ntie_s, cut_s;
   const int r = blockIdx.x;
   const int S = min(max(a.seq_used[r], 0), a.max_seq);
   if (S == 0) return;
   const uint32_t *keys = a.keys + (int64_t)r * a.keys_sr;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const bool resident = S <= KCHUNK;       // uniform over the block
   for (int b = threadIdx.x; b < HIST_BINS; b += blockDim.x) hist_a[b] = 0;
   if (threadIdx.x == 0) { ncand_s = 0; ntie_s = 0; cut_s = 0x7fffffff; }
-  if (S <= KCHUNK) load_chunk(skeys, keys, 0, S);
   // candidates (unprotected tokens): count, smallest and largest key, from the
-  // keys kernel's per-64-token figures, reduced in one barrier
-  uint32_t cnt = 0, kmin = 0xFFFFFFFFu, kmax = 0;
+  // keys kernel's per-64-token figures, reduced in one barrier; their loads go
+  // first, the keys' loads (clamped in bounds, zero past S) behind them
   const uint4 *st = a.stats + (int64_t)r * a.stats_sr;
-  for (int g = threadIdx.x; g < (S + 63) / 64; g += blockDim.x) {
+  const int ngroups = (S + 63) / 64;
+  const uint4 s0 = st[min((int)threadIdx.x, ngroups - 1)];
+  uint32_t kr[KPT];
+  if (resident) {
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) {
+      const int t = j * SEL_T + threadIdx.x;
+      const uint32_t v = keys[min(t, S - 1)];
+      kr[j] = t < S ? v : 0u;
+    }
+  }
+  uint32_t cnt = 0, kmin = 0xFFFFFFFFu, kmax = 0;
+  if ((int)threadIdx.x < ngroups) { cnt = s0.x; kmin = s0.y; kmax = s0.z; }
+  for (int g = threadIdx.x + blockDim.x; g < ngroups; g += blockDim.x) {
     const uint4 v = st[g];
     cnt += v.x;
     kmin = min(kmin, v.y);
     kmax = max(kmax, v.z);
   }
-  for (int o = 32; o > 0; o >>= 1) {
-    cnt += __shfl_xor(cnt, o, 64);
-    kmin = min(kmin, (uint32_t)__shfl_xor(kmin, o, 64));
-    kmax = max(kmax, (uint32_t)__shfl_xor(kmax, o, 64));
-  }
-  if (lane == 0) { red[0][wv] = cnt; red[1][wv] = kmin; red[2][wv] = kmax; }
+  cnt = wave_scan_u32(cnt, 0u, OpAdd());
+  kmin = wave_scan_u32(kmin, 0xFFFFFFFFu, OpMin());
+  kmax = wave_scan_u32(kmax, 0u, OpMax());
+  if (lane == 63) { red[0][wv] = cnt; red[1][wv] = kmin; red[2][wv] = kmax; }
   __syncthreads();
+  if (resident) {
+#pragma unroll
+    for (int j = 0; j < KPT; ++j) skeys[j * SEL_T + threadIdx.x] = kr[j];   // read after later barriers
+  }
   uint32_t cand_n = 0, lo = 0xFFFFFFFFu, hi = 0;
   for (int i = 0; i < SEL_T / 64; ++i) {
     cand_n += red[0][i];
@@ -252,6 +311,7 @@ __global__ void __launch_bounds__(SEL_T) keep_select_kernel(KeepArgs a) {
     bool in_lds = false;
     int nc = 0;
     uint32_t *cur = hist_a, *nxt = hist_b;   // cur is zero
+    bool first = true;
     while (true) {
       const int sh = max(0, wbits - 11);     // 2048 bins of 2^sh keys
       auto count = [&](uint32_t key, int) {
@@ -260,22 +320,54 @@ __global__ void __launch_bounds__(SEL_T) keep_select_kernel(KeepArgs a) {
       };
       if (in_lds) {
         for (int i = threadIdx.x; i < nc; i += blockDim.x) count(cand[i].x, (int)cand[i].y);
+      } else if (resident && first) {
+        // every candidate lies in [lo, hi]: only the protected tokens (key 0) are skipped
+#pragma unroll
+        for (int j = 0; j < KPT; ++j)
+          if (kr[j] != 0u) atomicAdd(&cur[(kr[j] - base) >> sh], 1u);
+      } else if (resident) {                 // a window too wide to gather (wbits <= 21)
+        count_window_sparse(skeys, S, base, wbits, sh, cur);
       } else {
         visit_keys(skeys, keys, S, count);
       }
       __syncthreads();
       uint32_t need2;
-      const int b = find_bin(cur, HIST_BINS, need, &need2, wtot, found, nxt, HIST_BINS);
+      const int b = find_bin<SEL_T>(cur, HIST_BINS, need, &need2, wtot, found, nxt, HIST_BINS);
       in_win = cur[b];
       need = need2;
       base += (uint32_t)b << sh;
       wbits = sh;
+      first = false;
       if (sh == 0) break;                    // the bin is one key value: the threshold
       if (!in_lds && in_win <= (uint32_t)CAND_CAP) {
         // gather the window's candidates (key, index) into LDS
-        visit_keys(skeys, keys, S, [&](uint32_t key, int t) {
-          if (key != 0 && key - base < (1u << wbits)) cand[atomicAdd(&ncand_s, 1)] = make_uint2(key, (uint32_t)t);
-        });
+        if (resident) {
+          // key - base < lim: in the window and not 0 (base >= lo >= 1); a thread's
+          // hits go to consecutive slots placed by a DPP scan, one shared-count
+          // update per wave, the keys read back from the LDS copy
+          const uint32_t lim = min(1u << wbits, 0u - base);
+          uint32_t m = 0;
+#pragma unroll
+          for (int j = 0; j < KPT; ++j) m |= (uint32_t)(kr[j] - base < lim) << j;
+          const uint32_t c = __popc(m);
+          const uint32_t inc = wave_scan_u32(c, 0u, OpAdd());
+          const uint32_t tot = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
+          if (tot != 0) {                    // uniform over the wave
+            uint32_t wb = 0;
+            if (lane == 0) wb = (uint32_t)atomicAdd(&ncand_s, (int)tot);
+            uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)wb, 0) + inc - c;
+            while (m) {
+              const int j = __builtin_ctz(m);
+              m &= m - 1;
+              const int t = j * SEL_T + threadIdx.x;
+              cand[o++] = make_uint2(skeys[t], (uint32_t)t);
+            }
+          }
+        } else {
+          visit_keys(skeys, keys, S, [&](uint32_t key, int t) {
+            if (key != 0 && key - base < (1u << wbits)) cand[atomicAdd(&ncand_s, 1)] = make_uint2(key, (uint32_t)t);
+          });
+        }
         __syncthreads();
         nc = ncand_s;
         in_lds = true;
@@ -285,12 +377,18 @@ __global__ void __launch_bounds__(SEL_T) keep_select_kernel(KeepArgs a) {
     thr = base;
     const uint32_t ties = in_win;            // candidates whose key == thr
     cut = 0x7fffffff;
-    if (need < ties && in_lds && ties <= (uint32_t)HIST_BINS) {
+    if (need < ties && (in_lds || resident) && ties <= (uint32_t)HIST_BINS) {
       // keep the `need` lowest-index tokens whose key == thr: the tied candidates'
       // indices are gathered from LDS and each finds its rank among them
       uint32_t *tie_t = nxt;
-      for (int i = threadIdx.x; i < nc; i += blockDim.x)
-        if (cand[i].x == thr) tie_t[atomicAdd(&ntie_s, 1)] = cand[i].y;
+      if (in_lds) {
+        for (int i = threadIdx.x; i < nc; i += blockDim.x)
+          if (cand[i].x == thr) tie_t[atomicAdd(&ntie_s, 1)] = cand[i].y;
+      } else {
+        visit_chunk(skeys, 0, S, [&](uint32_t key, int t) {
+          if (key == thr) tie_t[atomicAdd(&ntie_s, 1)] = (uint32_t)t;
+        });
+      }
       __syncthreads();
       const int nt = ntie_s;
       for (int i = threadIdx.x; i < nt; i += blockDim.x) {
@@ -326,56 +424,84 @@ __global__ void __launch_bounds__(SEL_T) keep_select_kernel(KeepArgs a) {
     }
   }
   // (k == cand_n: thr = 0, cut = 0 keeps every token)
-  // write: a thread's 4 consecutive tokens give one nibble of a 32-token word, the
-  // word's 8 nibbles sitting in 8 consecutive lanes; four wave ballots (token j of
-  // every lane's group) hold them, and the word's first lane interleaves its byte
-  // of each ballot into the word
+  // write: lane i of a wave tests token t0 + i of 64 consecutive tokens t0 (a
+  // multiple of 64); the wave's ballot is words t0/32 and t0/32 + 1, stored by
+  // lanes 0 and 1.  Without a tie cut and with thr >= 1 the test is one
+  // subtraction and one compare: key - 1 >= thr - 1 keeps key 0 (protected,
+  // wraps to the top) and every key >= thr.
   const int padded = ((S + a.BS - 1) / a.BS) * a.BS;
   const int nw = (padded + 31) >> 5;
   uint8_t *krow = a.keep ? a.keep + (int64_t)r * a.keep_sr : nullptr;
   uint32_t *brow = a.bits ? a.bits + (int64_t)r * a.bits_sr : nullptr;
-  for (int c0 = 0; c0 < padded; c0 += KCHUNK) {
-    const int n = min(KCHUNK, S - c0);       // keys of the chunk (n <= 0: padding only)
-    if (S > KCHUNK) {
-      __syncthreads();
-      if (n > 0) load_chunk(skeys, keys, c0, n);
-      __syncthreads();
-    }
-    const int groups = (min(KCHUNK, padded - c0) + 3) >> 2;
-    auto group = [&](int g) {                // 4-token group g of the chunk
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (4 * g + 3 < n) v = ((const uint4 *)skeys)[g];
-      else if (4 * g < n) {
-        v.x = skeys[4 * g];
-        if (4 * g + 1 < n) v.y = skeys[4 * g + 1];
-        if (4 * g + 2 < n) v.z = skeys[4 * g + 2];
+  auto write_mask = [&](auto simple) {
+    constexpr bool SIMPLE = decltype(simple)::value;
+    // t = this lane's token; whole = every token of the wave's 64 is < S (uniform)
+    auto one = [&](int t, uint32_t key, bool whole) {
+      bool kp = SIMPLE ? (key - 1u >= thr - 1u) : ((key == 0u) | (key > thr) | ((key == thr) & (t < cut)));
+      if (!whole) kp = kp & (t < S);
+      const unsigned long long bal = __ballot(kp);
+      if (krow && t < S) krow[t] = kp ? 1 : 0;
+      if (brow && lane < 2) {
+        const int w = ((t - lane) >> 5) + lane;
+        if (w < nw) brow[w] = lane ? (uint32_t)(bal >> 32) : (uint32_t)bal;
       }
-      return v;
     };
-    auto emit = [&](int g, uint4 v) {
-      const int t = c0 + 4 * g;
-      const uint32_t kk[4] = {v.x, v.y, v.z, v.w};
-      unsigned long long bal[4];
+    // the keys come from the LDS copy (a resident request's is whole), one chunk
+    // of KCHUNK tokens at a time
+    for (int c0 = 0; c0 < padded; c0 += KCHUNK) {
+      const int n = min(KCHUNK, S - c0);     // keys of the chunk (n <= 0: padding only)
+      if (!resident) {
+        __syncthreads();
+        if (n > 0) load_chunk(skeys, keys, c0, n);
+        __syncthreads();
+      }
+      for (int j = 0; j < KPT; ++j) {
+        const int tl = j * SEL_T + threadIdx.x;
+        one(c0 + tl, tl < n ? skeys[tl] : 0u, c0 + (j + 1) * SEL_T <= S);
+      }
+    }
+  };
+  if (resident && cut == 0x7fffffff && thr != 0u) {
+    // the common case, from the register keys: a wave's 64 tokens t0 + lane of
+    // slot j give words t0/32 (lane 0) and t0/32 + 1 (lane 1)
+    // the compare's lane mask is the ballot (no per-lane boolean); the lanes
+    // past S are masked off with a mask built from the wave's first token
+    const uint32_t thr1 = thr - 1u;
+    const int wu = __builtin_amdgcn_readfirstlane(wv);
+    const int bsh = 32 * (lane & 1);
+    static_assert(2 * KPT == 64, "one word per lane");
+    uint32_t myword = 0;
+    auto slots = [&](auto wb) {
+      constexpr bool WB = decltype(wb)::value;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t key = kk[j];
-        const bool kp = t + j < S && (key == 0 || key > thr || (key == thr && t + j < cut));
-        bal[j] = __ballot(kp);
-        if (krow && t + j < S) krow[t + j] = kp ? 1 : 0;
-      }
-      const int w = t >> 5;
-      if (brow && (lane & 7) == 0 && w < nw) {
-        const int sh = lane;                 // 8 * (lane / 8): this word's byte of the ballots
-        brow[w] = spread4((uint32_t)(bal[0] >> sh)) | (spread4((uint32_t)(bal[1] >> sh)) << 1) |
-                  (spread4((uint32_t)(bal[2] >> sh)) << 2) | (spread4((uint32_t)(bal[3] >> sh)) << 3);
+      for (int j = 0; j < KPT; ++j) {
+        const int rem = S - (j * SEL_T + 64 * wu);     // tokens of the wave's 64 that are < S
+        const unsigned long long valid = rem >= 64 ? ~0ull : rem <= 0 ? 0ull : (1ull << rem) - 1ull;
+        const unsigned long long bal = __builtin_amdgcn_uicmp(kr[j] - 1u, thr1, 35 /* unsigned >= */) & valid;
+        if (WB) {
+          const int t = j * SEL_T + threadIdx.x;
+          if (t < S) krow[t] = (uint8_t)((bal >> lane) & 1ull);
+        }
+        // lanes 2j and 2j + 1 keep slot j's two words: one store per wave at the end
+        // (a store instruction costs the memory pipeline about as much for two
+        // lanes as for 64)
+        const uint32_t word = (uint32_t)(bal >> bsh);    // even lanes: low half, odd lanes: high half
+        myword = (lane >> 1) == j ? word : myword;
       }
     };
-    for (int g0 = 0; g0 < groups; g0 += 2 * blockDim.x) {
-      const int g = g0 + threadIdx.x, g2 = g + blockDim.x;
-      const uint4 v0 = group(g), v1 = group(g2);
-      emit(g, v0);
-      if (g0 + blockDim.x < groups) emit(g2, v1);   // uniform over the block
+    if (brow) {
+      if (krow) slots(std::integral_constant<bool, true>());
+      else slots(std::integral_constant<bool, false>());
+      const int w = (lane >> 1) * (SEL_T / 32) + 2 * wv + (lane & 1);
+      if (w < nw) brow[w] = myword;
+      for (int w = KCHUNK / 32 + threadIdx.x; w < nw; w += blockDim.x) brow[w] = 0u;   // past the resident
+    } else {                                                                            // span (a block size
+      write_mask(std::integral_constant<bool, true>());                                 // not dividing it)
     }
+  } else if (cut == 0x7fffffff && thr != 0u) {
+    write_mask(std::integral_constant<bool, true>());
+  } else {
+    write_mask(std::integral_constant<bool, false>());
   }
 }
 
@@ -396,11 +522,7 @@ __device__ __forceinline__ void write_keys(const KeepArgs &a, int r, int S, int 
     a.keys[(int64_t)r * a.keys_sr + t] = key;
   }
   const bool c = key != 0;                 // candidate keys are never 0
-  uint32_t mn = c ? key : 0xFFFFFFFFu, mx = key;
-  for (int o = 32; o > 0; o >>= 1) {
-    mn = min(mn, (uint32_t)__shfl_xor(mn, o, 64));
-    mx = max(mx, (uint32_t)__shfl_xor(mx, o, 64));
-  }
+  const uint32_t mn = wave_min_u32(c ? key : 0xFFFFFFFFu), mx = wave_max_u32(key);
   const uint32_t n = (uint32_t)__popcll(__ballot(c));
   if ((tok & 63) == 0 && t < S) a.stats[(int64_t)r * a.stats_sr + t / 64] = make_uint4(n, mn, mx, 0u);
 }

@@ -409,11 +409,13 @@ def test_keep_mask_ties_keep_the_lower_index():
     assert keep[:3].all() and keep[3000:3050].all() and keep[100:400].all() and not keep[400:1100].any()
 
 
-@pytest.mark.parametrize("n_tied,spread", [(5000, True), (3000, False), (40, True)])
-def test_keep_mask_many_ties_keep_the_lower_index(n_tied, spread):
+@pytest.mark.parametrize("n_tied,spread,S", [(5000, True, 40000), (3000, False, 40000), (40, True, 40000),
+                                             (5000, True, 30000), (40, True, 30000)])
+def test_keep_mask_many_ties_keep_the_lower_index(n_tied, spread, S):
     """More tied scores at the boundary than the selection ranks in LDS (2048), scattered over
-    the request or in one run, and a few ties among distinct scores: lowest indices first."""
-    S = 40000
+    the request or in one run, and a few ties among distinct scores: lowest indices first.
+    40000 tokens exceed the select block's LDS chunk of keys (candidates gathered), 30000 do not
+    (ties found among the keys in LDS)."""
     g = torch.Generator().manual_seed(n_tied)
     scores = torch.rand(3, 2, S, generator=g) * 0.4            # distinct, below the tie value
     pos = torch.randperm(S - 8, generator=g)[:n_tied] + 8 if spread else torch.arange(1000, 1000 + n_tied)

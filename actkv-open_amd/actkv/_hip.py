@@ -205,6 +205,10 @@ class _PinnedRing:
         if self.buf is None:
             self.buf = torch.empty(self.SIZE, dtype=torch.int32, pin_memory=True)
             self.np = self.buf.numpy()
+            # touch every page now: a first write to a page of the fresh buffer costs a fault
+            # of several microseconds, which would otherwise land on the uploads of the first
+            # pass through the ring
+            self.np[:] = 0
         h = self.off // half
         cur = stream(device)
         if self.off + n > (h + 1) * half:

@@ -145,17 +145,19 @@ __device__ __forceinline__ void copy_rows(unsigned char *kv, int64_t sp, int64_t
   }
 }
 
-// Pinned flag of old logical position pos of request r.
-__device__ __forceinline__ uint8_t pin_of(const CompactArgs &a, int r, int pos) {
-  return a.pin_in ? a.pin_in[(int64_t)r * a.pin_sr + pos] : (uint8_t)(pos < a.pin_count[r]);
+// Pinned flag of old logical position pos of request r (pcount: pin_count[r]).
+__device__ __forceinline__ uint8_t pin_of(const CompactArgs &a, int r, int pos, int pcount) {
+  return a.pin_in ? a.pin_in[(int64_t)r * a.pin_sr + pos] : (uint8_t)(pos < pcount);
 }
 
-// grid (tiles, plane groups, R), CT threads, dynamic LDS 2*(max_words+1) words.
+// grid (tiles, plane groups, R), CT threads, dynamic LDS 2*max_words words.  The
+// length and the pin count are read together at the start.
 template <typename U>
 __global__ void __launch_bounds__(CT) compact_kernel(CompactArgs a) {
   extern __shared__ uint32_t sm[];
   __shared__ int64_t src_slot[MAX_PAIRS], dst_slot[MAX_PAIRS];
   const int r = blockIdx.z;
+  const int pcount = a.pin_count ? a.pin_count[r] : 0;
   const int S = max(a.seq_used[r], 0);
   const int Y = (S + a.BS - 1) / a.BS;
   const int nw = (Y * a.BS + 31) >> 5;
@@ -169,11 +171,11 @@ __global__ void __launch_bounds__(CT) compact_kernel(CompactArgs a) {
   uint32_t *words = sm;
   uint32_t *pre = sm + a.max_words;
   const uint32_t *brow = a.bits + (int64_t)r * a.bits_sr;
+  const int32_t *btr = a.bt + (int64_t)r * a.bt_sr;
   for (int w = threadIdx.x; w < nw; w += CT) words[w] = brow[w];
   __syncthreads();
   scan_words(words, pre, nw);
   const int B = (int)pre[nw];
-  const int32_t *btr = a.bt + (int64_t)r * a.bt_sr;
   const int X = (B + a.BS - 1) / a.BS;
   const int drop = Y - X;
   const int start = drop * a.BS, end = start + B;
@@ -203,7 +205,7 @@ __global__ void __launch_bounds__(CT) compact_kernel(CompactArgs a) {
       }
       if (lead) {
         if (a.perm) a.perm[(int64_t)r * a.perm_sr + (dst - start)] = src;
-        if (a.pin_out) a.pin_out[(int64_t)r * a.pout_sr + (dst - start)] = pin_of(a, r, src);
+        if (a.pin_out) a.pin_out[(int64_t)r * a.pout_sr + (dst - start)] = pin_of(a, r, src, pcount);
         if (a.src_out) a.src_out[(int64_t)r * a.pairs_sr + i] = sslot;
         if (a.dst_out) a.dst_out[(int64_t)r * a.pairs_sr + i] = dslot;
       }
@@ -216,7 +218,7 @@ __global__ void __launch_bounds__(CT) compact_kernel(CompactArgs a) {
       const int pos = start + j;
       if ((words[pos >> 5] >> (pos & 31)) & 1u) {
         if (a.perm) a.perm[(int64_t)r * a.perm_sr + j] = pos;
-        if (a.pin_out) a.pin_out[(int64_t)r * a.pout_sr + j] = pin_of(a, r, pos);
+        if (a.pin_out) a.pin_out[(int64_t)r * a.pout_sr + j] = pin_of(a, r, pos, pcount);
       }
     }
   }

@@ -5,8 +5,9 @@ The one-layer 2k fp16 and 32k bf16 workloads fit the CPU oracle: scores are comp
 every K-V byte bit-exactly with the oracle's evict on the GPU's own scores.
 The 36-layer ragged batch and the 36-layer 131k sequence (tens of GB of K/V) are checked at full size through size-independent
 properties -- the oracle's keep mask and plan on the GPU's scores, sequential allocator
-semantics, survivors == pre-compaction rows at perm, untouched rows unchanged -- plus oracle
-spot checks of the scores on the smallest request."""
+semantics, survivors == pre-compaction rows at perm on every layer, untouched rows unchanged --
+with every layer's and request's scores against a float32 torch reference on the GPU and
+oracle spot checks of the scores on the smallest request."""
 import math
 
 import numpy as np
@@ -38,6 +39,26 @@ def _exact_lse_gpu(kv_layer, table, seq_used, q):
         qh = q[:, h * g:(h + 1) * g].float().reshape(-1, d)
         lse[:, h * g:(h + 1) * g] = torch.logsumexp((qh @ kt) * d ** -0.5, -1).view(n_q, g)
     return lse
+
+
+def _scores_fp32_gpu(kv_layer, table, seq_used, q, lse):
+    """Float32 torch reference of one request's scores on the GPU (every layer and request of
+    a large case, where the CPU oracle covers a sample): mean over the N action queries of
+    max over the GQA group of exp(scale q.k - lse).  q [N, Hq, D], lse [N, Hq] (device);
+    returns [Hkv, seq_used]."""
+    bs, hkv, d = kv_layer.shape[2], kv_layer.shape[3], kv_layer.shape[4]
+    n_q, hq, _ = q.shape
+    g = hq // hkv
+    nblk = math.ceil(seq_used / bs)
+    blocks = torch.tensor(table[:nblk], device=q.device, dtype=torch.long)
+    k = kv_layer[0].index_select(0, blocks).reshape(-1, hkv, d)[:seq_used].float()
+    out = torch.empty(hkv, seq_used, device=q.device)
+    for h in range(hkv):
+        kt = k[:, h].t().contiguous()
+        qh = q[:, h * g:(h + 1) * g].float().reshape(-1, d)
+        p = torch.exp((qh @ kt) * d ** -0.5 - lse[:, h * g:(h + 1) * g].reshape(-1, 1))
+        out[h] = p.view(n_q, g, seq_used).amax(1).mean(0)
+    return out
 
 
 def _single_layer_case(S, n_q, dtype, budget, sinks, seed):
@@ -161,7 +182,12 @@ def test_36_layers_8_ragged_sequences_one_evict_call():
     n_valid = torch.tensor(n_qs, dtype=torch.int32, device="cuda")
     cache.cal_attn(reqs, q, lse, out, n_seen, layer=None, n_valid=n_valid)
     assert n_seen.tolist() == n_qs
-    # oracle spot check of the scores: smallest request, two layers
+    # every layer and request against the float32 torch reference on the GPU ...
+    for l in range(layers):
+        for r in reqs:
+            want = _scores_fp32_gpu(cache.kv[l], cache.tables[r], lens[r], q[l, r, :n_qs[r]], lse[l, r, :n_qs[r]])
+            torch.testing.assert_close(out[l, r, :, :lens[r]], want, rtol=1e-3, atol=1e-9, msg=f"layer {l} request {r}")
+    # ... and the oracle's reference folds on the smallest request, two layers
     r0 = int(np.argmin(lens))
     for l in (0, layers - 1):
         want = torch.zeros(1, 8, width)
@@ -184,7 +210,7 @@ def test_36_layers_8_ragged_sequences_one_evict_call():
         plans[r] = (src, dst)
     free_o, tables_o, seq_o = _allocator_after(free0, tables0, seq0, reqs, keeps, 16)
     assert cache.free == free_o and cache.tables == tables_o and cache.seq_used == seq_o
-    _check_moves(cache, before, slots_before, {r: perms[r] for r in reqs}, plans, layers_to_check=(0, 17, 35))
+    _check_moves(cache, before, slots_before, {r: perms[r] for r in reqs}, plans, layers_to_check=range(layers))
 
 
 def test_36_layers_131k_tokens_clustered_runs_compaction():
@@ -212,4 +238,4 @@ def test_36_layers_131k_tokens_clustered_runs_compaction():
     free_o, tables_o, seq_o = _allocator_after(free0, tables0, seq0, [0], [keep], 16)
     assert cache.free == free_o and cache.tables == tables_o and cache.seq_used == seq_o
     assert drop == math.ceil(S / 16) - math.ceil(int(keep.sum()) / 16)
-    _check_moves(cache, before, slots_before, {0: perm}, {0: (src, dst)}, layers_to_check=(0, 1, 20, 35))
+    _check_moves(cache, before, slots_before, {0: perm}, {0: (src, dst)}, layers_to_check=range(layers))

@@ -192,7 +192,8 @@ class _PinnedRing:
     def __init__(self):
         self.buf = None
         self.np = None
-        self.off = 0
+        self.half = 0                    # the half the next span is taken from
+        self.off = 0                     # the next free entry (inside that half)
         self.events = [None, None]       # per half: event after its last copy, or "sync"
         self.streams = [set(), set()]    # per half: the streams its copies were queued on
 
@@ -209,7 +210,10 @@ class _PinnedRing:
             # of several microseconds, which would otherwise land on the uploads of the first
             # pass through the ring
             self.np[:] = 0
-        h = self.off // half
+        # the current half is tracked, not derived from the offset: a half filled to its last
+        # entry leaves the offset on the next half's first entry (or one past the buffer), and
+        # the next upload must still go through the change of halves below
+        h = self.half
         cur = stream(device)
         if self.off + n > (h + 1) * half:
             # leave half h (its copies are all queued): an event on the stream that queued them
@@ -221,6 +225,7 @@ class _PinnedRing:
             else:
                 self.events[h] = "sync"
             h = 1 - h
+            self.half = h
             self.off = h * half
             if self.events[h] == "sync":
                 torch.cuda.synchronize(device)

@@ -494,3 +494,25 @@ def test_pinned_uploads_survive_ring_wraps_and_side_streams():
     torch.cuda.synchronize()
     for vals, t in outs:
         assert t.cpu().tolist() == vals
+
+
+def test_pinned_uploads_that_fill_a_half_exactly():
+    """Uploads whose sizes divide half the ring fill each half to its last entry: the next upload
+    must change halves (waiting for the other half's copies) instead of running past the buffer
+    or into the other half unchecked.  Three whole passes of the ring, then single uploads of
+    exactly half the ring; every uploaded tensor holds its values."""
+    from actkv import _hip
+    dev = torch.device("cuda")
+    ring = _hip._PinnedRing()
+    half = _hip._PinnedRing.SIZE // 2
+    n = 2048
+    outs = []
+    for i in range(3 * 2 * half // n + 5):
+        vals = np.arange(i * n, (i + 1) * n, dtype=np.int32)
+        outs.append((vals, ring.upload_i32(vals, dev)))
+    for i in range(3):
+        vals = np.full(half, i, dtype=np.int32)
+        outs.append((vals, ring.upload_i32(vals, dev)))
+    torch.cuda.synchronize()
+    for vals, t in outs:
+        assert np.array_equal(t.cpu().numpy(), vals)

@@ -139,19 +139,29 @@ def dtype_code(dtype: torch.dtype) -> int:
     return _DTYPES[dtype]
 
 
+_GPU_DEVICES: dict = {}
+
+
 def require_gpu(what: str, *tensors) -> torch.device:
-    """All tensors must live on one ROCm GPU: the kernels have no CPU path."""
-    dev = None
+    """All tensors must live on one ROCm GPU: the kernels have no CPU path.  (Device indices
+    are compared as ints: building a torch.device per tensor costs a call's host time.)"""
+    idx = None
     for t in tensors:
         if t is None:
             continue
-        if t.device.type != "cuda":
+        if not t.is_cuda:
             raise RuntimeError(f"{what} runs HIP kernels and needs tensors on a ROCm GPU, got {t.device}; "
                                "the *_ref functions are the CPU formulations")
-        if dev is None:
-            dev = t.device
-        elif t.device != dev:
-            raise RuntimeError(f"{what}: tensors on different devices ({dev}, {t.device})")
+        i = t.get_device()
+        if idx is None:
+            idx = i
+        elif i != idx:
+            raise RuntimeError(f"{what}: tensors on different devices (cuda:{idx}, cuda:{i})")
+    if idx is None:
+        return None
+    dev = _GPU_DEVICES.get(idx)
+    if dev is None:
+        dev = _GPU_DEVICES[idx] = torch.device("cuda", idx)
     return dev
 
 

@@ -101,7 +101,7 @@ def action_scores_ref(q, kv, block_table, seq_used, lse, out, n_seen, scale=None
 # ----------------------------------------------------------------------------- HIP path
 
 def _as_i32(t: torch.Tensor, device) -> torch.Tensor:
-    if t.dtype != torch.int32 or t.device != device:
+    if t.dtype is not torch.int32 or t.get_device() != device.index:
         t = t.to(device=device, dtype=torch.int32)
     return t
 
@@ -124,6 +124,10 @@ def action_scores(q, kv, block_table, seq_used, lse, out, n_seen, scale=None, *,
                          "allocate it as [R, Hkv, max_blocks * block_size]")
     dev = _hip.require_gpu("action_scores", q, kv, block_table, seq_used, lse, out, n_seen,
                            n_valid, kv_len)
+    # strides are read as tuples and the K plane is addressed through the cache's own
+    # pointer and strides (plane 0 starts at the cache's first element): each view or
+    # per-dimension query would cost host time on every call
+    kvs = kv.stride()
     multi_layer = kv.dim() == 6
     if multi_layer:
         L, _, nb, bs, hkv, d = kv.shape
@@ -131,8 +135,8 @@ def action_scores(q, kv, block_table, seq_used, lse, out, n_seen, scale=None, *,
             raise ValueError("a [L, 2, NB, BS, Hkv, D] cache takes q [L, R, N, Hq, D], "
                              "lse [L, R, N, Hq] and out [L, R, Hkv, W]")
         q5, lse4, out4 = q, lse, out
-        kv_sl = kv.stride(0)
-        kv_k = kv[:, 0]
+        qs, ls, os_ = q.stride(), lse.stride(), out.stride()
+        kv_sl = kvs[0]
     else:
         _, nb, bs, hkv, d = kv.shape
         L = 1
@@ -143,17 +147,17 @@ def action_scores(q, kv, block_table, seq_used, lse, out, n_seen, scale=None, *,
         else:
             raise ValueError(f"q must be [R, Hq, D] or [R, N, Hq, D] for a one-layer cache, got {tuple(q.shape)}")
         out4 = out.unsqueeze(0)
+        qs, ls, os_ = q5.stride(), lse4.stride(), out4.stride()
         kv_sl = 0
-        kv_k = kv[0]
     _, r_n, n_q, hq, dq = q5.shape
     assert hq % hkv == 0
     assert dq == d
-    assert kv.stride(-1) == 1 and q.stride(-1) == 1
-    if lse4.dtype != torch.float32 or out4.dtype != torch.float32:
+    assert kvs[-1] == 1 and qs[-1] == 1
+    if lse4.dtype is not torch.float32 or out4.dtype is not torch.float32:
         raise TypeError("lse and out must be float32")
-    if lse4.stride(-1) != 1 or out4.stride(-1) != 1:
+    if ls[-1] != 1 or os_[-1] != 1:
         raise ValueError("lse and out need a unit stride in their last dimension")
-    if n_seen.dtype != torch.int32:
+    if n_seen.dtype is not torch.int32:
         raise TypeError("n_seen must be int32 (it is updated in place)")
     if tuple(lse4.shape) != (L, r_n, n_q, hq) or tuple(out4.shape[:3]) != (L, r_n, hkv):
         raise ValueError(f"shape mismatch: q {tuple(q.shape)}, lse {tuple(lse.shape)}, out {tuple(out.shape)}")
@@ -168,13 +172,13 @@ def action_scores(q, kv, block_table, seq_used, lse, out, n_seen, scale=None, *,
         raise ValueError(f"kv_len must be [R, N] = {(r_n, n_q)}")
     lib = _hip.lib()
     rc = lib.actkv_action_scores(
-        q5.data_ptr(), _hip.dtype_code(q5.dtype), q5.stride(0), q5.stride(1), q5.stride(2), q5.stride(3),
-        kv_k.data_ptr(), _hip.dtype_code(kv.dtype), kv_sl, kv_k.stride(-4), kv_k.stride(-3), kv_k.stride(-2),
+        q5.data_ptr(), _hip.dtype_code(q5.dtype), qs[0], qs[1], qs[2], qs[3],
+        kv.data_ptr(), _hip.dtype_code(kv.dtype), kv_sl, kvs[-4], kvs[-3], kvs[-2],
         nb,
         bt.data_ptr(), bt.stride(0), bt.shape[1],
         seq.data_ptr(),
-        lse4.data_ptr(), lse4.stride(0), lse4.stride(1), lse4.stride(2),
-        out4.data_ptr(), out4.stride(0), out4.stride(1), out4.stride(2), out4.shape[-1],
+        lse4.data_ptr(), ls[0], ls[1], ls[2],
+        out4.data_ptr(), os_[0], os_[1], os_[2], out4.shape[-1],
         n_seen.data_ptr(), _hip.ptr(nv), _hip.ptr(kl),
         L, r_n, n_q, hq, hkv, d, bs, float(scale), _hip.stream(dev))
     _hip.check(rc, "actkv_action_scores")

@@ -467,9 +467,14 @@ class PagedKVCache:
             dst = torch.full((r_n, smax), -1, dtype=torch.int64, device=dev)
         es = self.kv.element_size()
         row = self.n_kv_heads * self.head_dim
-        flat = self.kv.view(self.n_layers * 2, -1, row)
+        if self.kv.is_contiguous():     # [L*2 planes, NB*BS slots, row] from the cache's own strides
+            kvs = self.kv.stride()
+            planes, plane_b, slot_b = self.n_layers * 2, kvs[1] * es, kvs[3] * es
+        else:
+            flat = self.kv.view(self.n_layers * 2, -1, row)
+            planes, plane_b, slot_b = flat.shape[0], flat.stride(0) * es, flat.stride(1) * es
         rc = _hip.lib().actkv_compact(
-            flat.data_ptr(), flat.shape[0], flat.stride(0) * es, flat.stride(1) * es, row * es, self.num_blocks,
+            self.kv.data_ptr(), planes, plane_b, slot_b, row * es, self.num_blocks,
             bits.data_ptr(), bits.stride(0), r_n, seq_dev.data_ptr(),
             bt_dev.data_ptr(), mb, bs,
             perm.data_ptr(), bmax, _hip.ptr(pinned_in), 0 if pinned_in is None else pinned_in.stride(0),

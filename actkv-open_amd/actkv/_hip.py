@@ -101,7 +101,7 @@ _lib = None
 
 def lib() -> ctypes.CDLL:
     """Load the library once; raise if it has not been built."""
-    global _lib
+    global _lib, _glue_mod
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} is missing: build it with `python actkv-open_amd/build_lib.py` "
@@ -114,8 +114,28 @@ def lib() -> ctypes.CDLL:
         # dependency scope; the upload ring queues its host-to-device copies with it
         cp = handle.hipMemcpyAsync
         cp.restype, cp.argtypes = _c_i32, [_c_p, _c_p, _c_sz, _c_i32, _c_p]
+        try:
+            from . import _glue as g
+        except ImportError as e:
+            raise RuntimeError("the CPython call module actkv/_glue*.so is missing: build it with "
+                               "`python actkv-open_amd/build_lib.py`") from e
+        addr = lambda f: ctypes.cast(f, ctypes.c_void_p).value
+        g.bind(addr(handle.actkv_action_scores), addr(handle.actkv_keep_mask), addr(handle.actkv_compact),
+               addr(cp))
         _lib = handle
+        _glue_mod = g
     return _lib
+
+
+_glue_mod = None
+
+
+def glue():
+    """The bound _glue module: the scoring, keep-mask and compaction entry points and
+    hipMemcpyAsync, called without ctypes' per-argument conversion (same arguments)."""
+    if _glue_mod is None:
+        lib()
+    return _glue_mod
 
 
 def available() -> bool:
@@ -247,7 +267,7 @@ class _PinnedRing:
         self.np[self.off:self.off + n] = arr
         out = torch.empty(n, dtype=torch.int32, device=device)
         if n:
-            rc = lib().hipMemcpyAsync(out.data_ptr(), self.buf.data_ptr() + 4 * self.off, 4 * n,
+            rc = glue().memcpy_async(out.data_ptr(), self.buf.data_ptr() + 4 * self.off, 4 * n,
                                       _HIP_MEMCPY_H2D, cur)
             if rc != 0:
                 raise RuntimeError(f"hipMemcpyAsync (host to device, {4 * n} bytes) failed with HIP error {rc}")
@@ -280,10 +300,17 @@ def scratch(device: torch.device, key, nbytes: int) -> torch.Tensor:
     return buf
 
 
+_ws_sizes: dict = {}
+
+
 def workspace(device: torch.device, kind: int, r: int, max_seq: int) -> torch.Tensor:
     """Cached per (device, kind) and grown on demand; the kernels need no initialised
     contents.  Calls sharing it are ordered on the current stream."""
-    need = int(lib().actkv_workspace_size(kind, r, max_seq))
+    need = _ws_sizes.get((kind, r, max_seq))
+    if need is None:                # the size is a pure function of its arguments
+        if len(_ws_sizes) > 4096:
+            _ws_sizes.clear()
+        need = _ws_sizes[(kind, r, max_seq)] = int(lib().actkv_workspace_size(kind, r, max_seq))
     key = (device, kind)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < need:

@@ -170,8 +170,7 @@ def action_scores(q, kv, block_table, seq_used, lse, out, n_seen, scale=None, *,
     kl = None if kv_len is None else _as_i32(kv_len, dev).contiguous()
     if kl is not None and tuple(kl.shape) != (r_n, n_q):
         raise ValueError(f"kv_len must be [R, N] = {(r_n, n_q)}")
-    lib = _hip.lib()
-    rc = lib.actkv_action_scores(
+    rc = _hip.glue().action_scores(
         q5.data_ptr(), _hip.dtype_code(q5.dtype), qs[0], qs[1], qs[2], qs[3],
         kv.data_ptr(), _hip.dtype_code(kv.dtype), kv_sl, kvs[-4], kvs[-3], kvs[-2],
         nb,

@@ -87,12 +87,32 @@ def _as_i32(table) -> np.ndarray:
 _REDUCE = {"mean": _hip.REDUCE_MEAN, "max": _hip.REDUCE_MAX}
 
 
+_SCORE_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+
+
 def _scores_layout(scores: torch.Tensor, seq_used: int):
-    """[..., H, W] / [H, W] / [W] -> (tensor, L, H, s_sl, s_sh) with a unit last stride."""
-    if scores.shape[-1] < seq_used:
-        raise ValueError(f"scores cover {scores.shape[-1]} tokens, seq_used is {seq_used}")
+    """[..., H, W] / [H, W] / [W] -> (tensor, L, H, s_sl, s_sh) with a unit last stride.
+
+    The kernels read columns [0, seq_used) of each row through the strides, so a tensor of a
+    kernel dtype with a unit last stride, whose leading dims collapse into one layer stride, is
+    used as it is: no view is built (each costs host time on every eviction).  Other dtypes and
+    layouts are copied first, their seq_used columns only."""
+    shape = scores.shape
+    nd = len(shape)
+    if shape[-1] < seq_used:
+        raise ValueError(f"scores cover {shape[-1]} tokens, seq_used is {seq_used}")
+    st = scores.stride()
+    if scores.dtype in _SCORE_DTYPES and st[-1] == 1:
+        if nd == 1:
+            return scores, 1, 1, 0, 0
+        if nd == 2:
+            return scores, 1, shape[0], 0, st[0]
+        if nd == 3:
+            return scores, shape[0], shape[1], st[0], st[1]
+        if all(st[i] == st[i + 1] * shape[i + 1] for i in range(nd - 3)):
+            return scores, math.prod(shape[:-2]), shape[-2], st[nd - 3], st[-2]
     s = scores[..., :seq_used]
-    if s.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+    if s.dtype not in _SCORE_DTYPES:
         s = s.float()
     if s.stride(-1) != 1:
         s = s.contiguous()
@@ -115,7 +135,7 @@ def _keep_mask_launch(s, L, H, s_sl, s_sr, s_sh, R, seq_dev, budget_dev, prot_co
     nw = keep_words(max_seq, block_size)
     bits = torch.empty(R, max(nw, 1), dtype=torch.int32, device=device)
     ws = _hip.workspace(device, _hip.WS_KEEP_MASK, R, max_seq)
-    rc = _hip.lib().actkv_keep_mask(
+    rc = _hip.glue().keep_mask(
         s.data_ptr(), _hip.dtype_code(s.dtype), s_sl, s_sr, s_sh, L, H, R,
         seq_dev.data_ptr(), budget_dev.data_ptr(), _hip.ptr(prot_count_dev), _hip.ptr(prot_mask), pm_sr,
         _REDUCE[head_reduce], _hip.ptr(keep), 0 if keep is None else keep.shape[1], bits.data_ptr(),
@@ -371,20 +391,26 @@ class PagedKVCache:
         """(seq_used [R], block_table [R, MB]) int32 on the device, reused while the requests'
         tables and lengths are unchanged (the device copy is never handed to callers)."""
         key = tuple(reqs), tuple(ys) if ys is not None else None
-        tabs = tuple(self.tables[r] for r in reqs)
-        stamp = tuple((getattr(t, "version", None), len(t), self.seq_used[r]) for t, r in zip(tabs, reqs))
         hit = self._dev_cache.get(key)
-        # the entry holds the table objects themselves: identity, not id(), decides a hit
-        if (hit is not None and hit[1] == stamp and all(isinstance(t, _Table) for t in tabs)
-                and all(a is b for a, b in zip(hit[0], tabs))):
-            return hit[2], hit[3]
+        if hit is not None:
+            # the entry holds the table objects themselves: identity, not id(), decides a hit,
+            # then each table's mutation count, length and the request's length
+            tables, seq_used = self.tables, self.seq_used
+            for r, t, (ver, n, s) in zip(reqs, hit[0], hit[1]):
+                if tables[r] is not t or t.version != ver or len(t) != n or seq_used[r] != s:
+                    break
+            else:
+                return hit[2], hit[3]
         host, mb = self._host_tables(reqs, ys)
         dev = self._upload(host)
         r_n = len(reqs)
         seq, bt = dev[:r_n], dev[r_n:].view(r_n, mb)
-        if len(self._dev_cache) > 64:
-            self._dev_cache.clear()
-        self._dev_cache[key] = (tabs, stamp, seq, bt)
+        tabs = tuple(self.tables[r] for r in reqs)
+        if all(isinstance(t, _Table) for t in tabs):   # plain lists carry no mutation count
+            if len(self._dev_cache) > 64:
+                self._dev_cache.clear()
+            self._dev_cache[key] = (tabs, tuple((t.version, len(t), self.seq_used[r]) for t, r in zip(tabs, reqs)),
+                                    seq, bt)
         return seq, bt
 
     def _device_consts(self, values: tuple) -> torch.Tensor:
@@ -439,26 +465,31 @@ class PagedKVCache:
         self._pin_count[req] = (pinned, pinned._version, cnt)
         return cnt
 
-    def _compact_launch(self, reqs, bits, kept, pinned_in=None, pin_count=None, pin_out=None):
+    def _compact_launch(self, reqs, bits, kept, pinned_in=None, pin_count=None, pin_out=None, *,
+                        tables=None, flat=False):
         """One actkv_compact launch over `reqs` with packed keep bits [R, words] and host-known
         kept counts; then the host allocator updates in request order (sequential semantics).
         pinned_in [R, >=S] bool or pin_count [R] int32 (device) gives the pinned tokens;
         pin_out (optional, bool [R, >=max(kept)]) receives the survivors' pins.
+        tables: the requests' (seq_used, block_table) device copies when the caller holds them.
         The kernel always reports each request's {B, M, drop, X} into a device buffer; with
         ACTKV_DEBUG=1 in the environment that report and the plan are read back and checked
         against the host's counts (one synchronisation per call).
-        Returns perm [R, max(kept)] int64 and pinned_out [R, max(kept)] bool (or None)."""
+        Returns perm [R, max(kept)] int64 and pinned_out [R, max(kept)] bool (or None); with
+        flat=True and one request, perm [kept] and pinned_out [kept] (no per-request view)."""
         dev = self.kv.device
         bs = self.block_size
         r_n = len(reqs)
         seqs = [self.seq_used[r] for r in reqs]
-        ys = [math.ceil(s / bs) for s in seqs]
-        seq_dev, bt_dev = self._device_tables(reqs)
+        ys = [-(-s // bs) for s in seqs]
+        seq_dev, bt_dev = self._device_tables(reqs) if tables is None else tables
         mb = bt_dev.shape[1]
         bmax = max(max(kept), 1)
-        perm = torch.empty(r_n, bmax, dtype=torch.int64, device=dev)
+        flat = flat and r_n == 1 and pin_out is None
+        shape = (bmax,) if flat else (r_n, bmax)
+        perm = torch.empty(shape, dtype=torch.int64, device=dev)
         if pin_out is None and (pinned_in is not None or pin_count is not None):
-            pin_out = torch.empty(r_n, bmax, dtype=torch.bool, device=dev)
+            pin_out = torch.empty(shape, dtype=torch.bool, device=dev)
         counts = _hip.scratch(dev, "compact_counts", 16 * r_n)
         debug = _hip.debug()
         if debug:
@@ -473,12 +504,12 @@ class PagedKVCache:
         else:
             flat = self.kv.view(self.n_layers * 2, -1, row)
             planes, plane_b, slot_b = flat.shape[0], flat.stride(0) * es, flat.stride(1) * es
-        rc = _hip.lib().actkv_compact(
+        rc = _hip.glue().compact(
             self.kv.data_ptr(), planes, plane_b, slot_b, row * es, self.num_blocks,
             bits.data_ptr(), bits.stride(0), r_n, seq_dev.data_ptr(),
             bt_dev.data_ptr(), mb, bs,
             perm.data_ptr(), bmax, _hip.ptr(pinned_in), 0 if pinned_in is None else pinned_in.stride(0),
-            _hip.ptr(pin_count), _hip.ptr(pin_out), bmax if pin_out is None else pin_out.stride(0),
+            _hip.ptr(pin_count), _hip.ptr(pin_out), bmax if pin_out is None or flat else pin_out.stride(0),
             None, 0, None, 0, _hip.ptr(src) if debug else None, _hip.ptr(dst) if debug else None,
             src.shape[1] if debug else 0, counts.data_ptr(),
             1, max(seqs), max(kept), _hip.stream(dev))
@@ -487,12 +518,14 @@ class PagedKVCache:
             _check_compaction(reqs, seqs, kept, bs, bits, counts.view(torch.int32)[: 4 * r_n].view(r_n, 4),
                               src, dst)
         for i, r in enumerate(reqs):
-            drop = ys[i] - math.ceil(kept[i] / bs)
+            drop = ys[i] - -(-kept[i] // bs)
             table = self.tables[r]
             if drop > 0:                      # freed blocks pushed last-first: table[drop-1], ..., table[0]
                 self.free.extend(table[drop - 1::-1])
             self.tables[r] = table.tail(drop) if isinstance(table, _Table) else table[drop:]
             self.seq_used[r] = kept[i]
+        if flat and kept[0] < bmax:     # nothing kept: empty results
+            return perm[:0], None if pin_out is None else pin_out[:0]
         return perm, pin_out
 
     def compact(self, req: int, keep_mask: torch.Tensor) -> torch.Tensor:
@@ -593,7 +626,7 @@ class PagedKVCache:
         seqs = [self.seq_used[r] for r in a_reqs]
         smax = max(seqs)
         ra = len(active)
-        # scores -> one [L, R, H, W] view
+        # scores -> (tensor, L, H, layer / request / head strides), read in place where possible
         if isinstance(scores, torch.Tensor):
             _hip.require_gpu("PagedKVCache.evict", scores)
             if scores.dim() < 3:
@@ -603,6 +636,19 @@ class PagedKVCache:
                 raise ValueError(f"scores {tuple(scores.shape)} do not have {r_n} requests at dim -3")
             sc = sc.reshape(-1, *sc.shape[-3:]) if sc.dim() != 4 else sc
             sc = sc[:, active] if ra != r_n else sc
+            if sc.shape[-1] < smax:
+                raise ValueError(f"scores cover {sc.shape[-1]} tokens, a request holds {smax}")
+            if sc.dtype not in _SCORE_DTYPES:
+                sc = sc.float()
+            if sc.stride(-1) != 1:
+                sc = sc.contiguous()
+            L, _, H, _ = sc.shape
+            s_sl, s_sr, s_sh, _ = sc.stride()
+        elif ra == 1:
+            s_i = scores[active[0]]
+            _hip.require_gpu("PagedKVCache.evict", s_i)
+            sc, L, H, s_sl, s_sh = _scores_layout(s_i, seqs[0])
+            s_sr = 0
         else:
             per = []
             for i in active:
@@ -610,25 +656,16 @@ class PagedKVCache:
                 _hip.require_gpu("PagedKVCache.evict", s_i)
                 s3, L_i, H_i, _, _ = _scores_layout(s_i, self.seq_used[reqs[i]])
                 per.append(s3.reshape(L_i, H_i, -1))
-            L0, H0 = per[0].shape[0], per[0].shape[1]
-            if any(p.shape[0] != L0 or p.shape[1] != H0 for p in per):
+            L, H = per[0].shape[0], per[0].shape[1]
+            if any(p.shape[0] != L or p.shape[1] != H for p in per):
                 raise ValueError("every request's scores need the same layer and head counts")
-            if ra == 1:                                   # no copy: a strided view
-                sc = per[0].unsqueeze(1)
-            else:
-                sc = torch.zeros(L0, ra, H0, smax, dtype=per[0].dtype, device=dev)
-                for j, p in enumerate(per):
-                    sc[:, j, :, : p.shape[-1]] = p
-        if sc.shape[-1] < smax:
-            raise ValueError(f"scores cover {sc.shape[-1]} tokens, a request holds {smax}")
-        if sc.dtype not in (torch.float32, torch.float16, torch.bfloat16):
-            sc = sc.float()
-        if sc.stride(-1) != 1:
-            sc = sc.contiguous()
-        L, _, H, _ = sc.shape
+            sc = torch.zeros(L, ra, H, smax, dtype=per[0].dtype, device=dev)
+            for j, p in enumerate(per):
+                sc[:, j, :, : seqs[j]] = p[..., : seqs[j]]
+            s_sl, s_sr, s_sh, _ = sc.stride()
         # the lengths come with the block tables the compaction launch reads anyway; budgets and
         # protected counts are the same from call to call in an eviction loop
-        seq_dev, _ = self._device_tables(a_reqs)
+        tables = self._device_tables(a_reqs)
         consts = self._device_consts(tuple(max(budgets[i], 0) for i in active) + tuple(counts))
         if all(p is None for p in pinneds):           # every request's pins are a prefix count
             pin_mat, prot_count = None, consts[ra:]
@@ -643,11 +680,18 @@ class PagedKVCache:
                         pin_mat[j, : counts[j]] = True
                     else:
                         pin_mat[j, : p.numel()] = p
-        _, bits = _keep_mask_launch(sc, L, H, sc.stride(0), sc.stride(1), sc.stride(2), ra,
-                                    seq_dev, consts[:ra], prot_count, pin_mat,
+        _, bits = _keep_mask_launch(sc, L, H, s_sl, s_sr, s_sh, ra,
+                                    tables[0], consts[:ra], prot_count, pin_mat,
                                     0 if pin_mat is None else pin_mat.stride(0),
                                     head_reduce, self.block_size, smax, dev, want_keep=False)
-        perm, pin_out = self._compact_launch(a_reqs, bits, kept, pin_mat, prot_count)
+        perm, pin_out = self._compact_launch(a_reqs, bits, kept, pin_mat, prot_count, tables=tables,
+                                             flat=True)
+        if ra == 1:                                   # flat results: no per-request views
+            i = active[0]
+            out[i] = perm
+            self.pinned[reqs[i]] = pin_out
+            self._pin_count[reqs[i]] = (pin_out, pin_out._version, counts[0])
+            return out
         for j, i in enumerate(active):
             b = kept[j]
             out[i] = perm[j, :b]

@@ -3,7 +3,8 @@
     python actkv-open_amd/build_lib.py          # compile every csrc/*.hip, link the .so
 
 Objects go to actkv-open_amd/_build/, the library to actkv-open_amd/actkv/libactkv_hip.so,
-where actkv/_hip.py loads it.  hipcc cross-compiles for gfx950 without a GPU.
+where actkv/_hip.py loads it.  hipcc cross-compiles for gfx950 without a GPU.  gcc builds
+csrc/pyglue.c into actkv/_glue*.so, the CPython module _hip.py calls the hot entry points through.
 """
 from __future__ import annotations
 
@@ -12,12 +13,14 @@ import glob
 import os
 import subprocess
 import sys
+import sysconfig
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "actkv", "libactkv_hip.so")
+GLUE = os.path.join(HERE, "actkv", "_glue" + sysconfig.get_config_var("EXT_SUFFIX"))
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -49,7 +52,18 @@ def build(verbose: bool = False) -> str:
     tmp = LIB + ".tmp"
     _run([HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, LIB)
+    build_glue()
     return LIB
+
+
+def build_glue() -> str:
+    """The CPython module that calls the library's hot entry points (host code only: gcc)."""
+    tmp = GLUE + ".tmp"
+    _run(["gcc", "-O2", "-shared", "-fPIC", "-Wall", "-Wextra", "-Wconversion", "-Werror",
+          "-Wno-unused-parameter", "-I" + sysconfig.get_paths()["include"],
+          "-I" + os.path.join(ROOT, "include"), os.path.join(CSRC, "pyglue.c"), "-o", tmp])
+    os.replace(tmp, GLUE)
+    return GLUE
 
 
 if __name__ == "__main__":

@@ -120,6 +120,35 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.actkv_slot_map(fake, 1, -1, 4, 16, fake, None) == 1
 
 
+def test_glue_takes_the_ctypes_arguments():
+    """The CPython call module (actkv/_glue*.so) takes each wrapped entry point's arguments with
+    the C types of the ctypes declarations, rejects a wrong count or an out-of-range value, and
+    returns what the ctypes call returns (validation failures here: nothing is launched)."""
+    lib, g = _hip.lib(), _hip.glue()
+    letter = {ctypes.c_void_p: "p", ctypes.c_int: "i", ctypes.c_int64: "l", ctypes.c_size_t: "z",
+              ctypes.c_float: "f"}
+    sigs = g.signatures()
+    assert set(sigs) == {"actkv_action_scores", "actkv_keep_mask", "actkv_compact", "hipMemcpyAsync"}
+    for name, letters in sigs.items():
+        argtypes = lib.hipMemcpyAsync.argtypes if name == "hipMemcpyAsync" else _hip._SIGNATURES[name][1]
+        assert "".join(letter[t] for t in argtypes) == letters, name
+    # null q, k/v, tables: rejected by the library's validation, the same code both ways
+    args = [None, 2, 0, 0, 0, 0, None, 2, 0, 0, 0, 0, 10, None, 0, 1, None, None, 0, 0, 0,
+            None, 0, 0, 0, 16, None, None, None, 1, 1, 1, 4, 2, 128, 16, 0.1, None]
+    assert g.action_scores(*args) == lib.actkv_action_scores(*args) == 1
+    km = [None, 0, 0, 0, 0, 1, 1, 1, None, None, None, None, 0, 0, None, 0, None, 0, 16, 100, None, 0, None]
+    assert g.keep_mask(*km) == lib.actkv_keep_mask(*km) == 1
+    cp = [None, 2, 0, 0, 16, 10, None, 1, 1, None, None, 1, 16, None, 0, None, 0, None, None, 0,
+          None, 0, None, 0, None, None, 0, None, 1, 16, 16, None]
+    assert g.compact(*cp) == lib.actkv_compact(*cp) == 1
+    with pytest.raises(TypeError, match="takes 38 arguments"):
+        g.action_scores(*args[:-1])
+    with pytest.raises(OverflowError, match="does not fit a C int"):
+        g.keep_mask(*km[:5], 1 << 40, *km[6:])
+    with pytest.raises(TypeError, match="argument 2"):
+        g.compact(*cp[:2], "x", *cp[3:])
+
+
 @pytest.mark.parametrize("bad", ["missing"])
 def test_python_layer_fails_loudly_without_the_library(monkeypatch, bad):
     monkeypatch.setattr(_hip, "LIB_PATH", "/nonexistent/libactkv_hip.so")

@@ -473,6 +473,40 @@ def test_launches_follow_torch_current_stream():
     assert torch.equal(a, b) and na.tolist() == nb.tolist() == [1, 1]
 
 
+@pytest.mark.parametrize("n_q", [128, 8])
+def test_scoring_interleaved_over_streams_counts_every_query_once(n_q):
+    """Scoring calls interleaved over three streams (free to run concurrently, each with its own
+    out and n_seen) count each call's queries once and leave the same running means, bit for
+    bit, as the same calls on the default stream.  n_q = 128 runs the query-tile kernel
+    (512 rows), 8 the K-slice kernel (32 rows)."""
+    dev = torch.device("cuda")
+    cache = _filled_cache([3000, 1700], hkv=8, d=128, layers=1, seed=21, dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(22)
+    q = torch.randn(2, n_q, 32, 128, generator=g).to(torch.bfloat16).to(dev)
+    lse = (6.0 + torch.rand(2, n_q, 32, generator=g)).to(dev)
+    width = max(len(cache.tables[r]) for r in (0, 1)) * cache.block_size
+    rounds = 4
+    want = torch.zeros(2, 8, width, device=dev)
+    n_want = torch.zeros(2, dtype=torch.int32, device=dev)
+    for _ in range(rounds):
+        cache.cal_attn([0, 1], q, lse, want, n_want)
+    streams = [torch.cuda.Stream() for _ in range(3)]
+    outs = [torch.zeros(2, 8, width, device=dev) for _ in streams]
+    seen = [torch.zeros(2, dtype=torch.int32, device=dev) for _ in streams]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    for _ in range(rounds):
+        for st, o, n in zip(streams, outs, seen):
+            with torch.cuda.stream(st):
+                cache.cal_attn([0, 1], q, lse, o, n)
+    for st in streams:
+        st.synchronize()
+    assert n_want.tolist() == [rounds * n_q] * 2
+    for o, n in zip(outs, seen):
+        assert n.tolist() == [rounds * n_q] * 2
+        assert torch.equal(o, want)
+
+
 def test_pinned_uploads_survive_ring_wraps_and_side_streams():
     """Host-to-device uploads through the pinned staging ring: enough of them to wrap the ring
     several times, every third queued on a side stream, and one larger than half the ring;

@@ -173,11 +173,12 @@ class Workload:
         self.n_seen.zero_()
 
     def step(self, ev=None):
-        """One eviction pass; ev = (start, scored, end) events recorded on the current stream."""
+        """One eviction pass; ev = (start, scored, end) events recorded on the current stream
+        (scored may be None: no marker between the scoring call and the eviction)."""
         if ev:
             ev[0].record()
         self.cache.cal_attn([0], self.q, self.lse, self.out, self.n_seen, layer=None)
-        if ev:
+        if ev and ev[1] is not None:
             ev[1].record()
         perm = self.cache.evict(0, self.out[:, 0], self.budget, protected=self.args.sinks)
         if ev:
@@ -203,13 +204,16 @@ def measure(w, steps, warmup):
     Each step starts from a restored cache.  The restore (a device copy of the whole cache) is
     queued first and the step's launches are queued behind it with no synchronisation, so the
     host prepares the step while the GPU copies, as a serving loop prepares step i+1 while step
-    i runs.  Events on the launch stream bracket each step (start, after scoring, end): the step
-    interval is the GPU's time for the step, and the scoring interval is the scoring call itself
-    (kernel + n_seen bump) with no host gap in it.
+    i runs.  Events on the launch stream at the step's start and end give the GPU's time for
+    the step.  An event is a marker packet that itself holds the queue for several
+    microseconds, so the split into the scoring call (kernel + n_seen bump) and the eviction
+    comes from a second pass of the same steps with a third event between them (its two
+    intervals add up to a little more than the step).
 
     The same steps are then timed once more with a synchronisation before each step, so the
     host's launch work is exposed; that figure is reported beside the first."""
     import torch
+    E = lambda: torch.cuda.Event(enable_timing=True)
     for _ in range(warmup):
         w.restore()
         w.step()
@@ -218,19 +222,26 @@ def measure(w, steps, warmup):
     wall0 = time.perf_counter()
     for _ in range(steps):
         w.restore()
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        ev = [E(), None, E()]
         w.step(ev)
         evs.append(ev)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     t_step = [e[0].elapsed_time(e[2]) * 1e3 for e in evs]
+    evs = []
+    for _ in range(steps):
+        w.restore()
+        ev = [E() for _ in range(3)]
+        w.step(ev)
+        evs.append(ev)
+    torch.cuda.synchronize()
     t_score = [e[0].elapsed_time(e[1]) * 1e3 for e in evs]
     t_evict = [e[1].elapsed_time(e[2]) * 1e3 for e in evs]
     t_sync = []
     for _ in range(steps):
         w.restore()
         torch.cuda.synchronize()
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        ev = [E(), None, E()]
         w.step(ev)
         torch.cuda.synchronize()
         t_sync.append(ev[0].elapsed_time(ev[2]) * 1e3)

@@ -21,7 +21,10 @@
 //   so the running max / sum of a row are lane-local plus one v_permlane32_swap;
 //   O^T += V^T . P^T (A = V^T from LDS, B = P^T: the lane's own 16 probabilities,
 //   taken in the token order tau(kb, lh, j) = 16kb + 8(j/4) + 4lh + j%4 that
-//   matches the S^T register layout, so no shuffle is needed).
+//   matches the S^T register layout, so no shuffle is needed).  P is split into
+//   hi = P rounded to the cache dtype and lo = (P - hi) rounded again, and both
+//   terms go through the matrix core: P then carries about 16 significant bits
+//   (bf16) instead of 8, so out is within ~1e-5 of the float32 softmax @ v.
 // K and V stages go straight from HBM into an LDS ring (buffer loads with the LDS
 // bit, several stages ahead), rows XOR-swizzled; V is read back transposed
 // (ds_read_b64_tr_b16).  Described at attn_ring_kernel.
@@ -301,12 +304,14 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
     const float msafe = m_new == -INFINITY ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m2 - msafe);
     float ps = 0.f;
-    V8 pb[2];
+    V8 pb[2], pbl[2];  // P = hi + lo, both in the cache dtype (hi/lo split below)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const float pe = __builtin_amdgcn_exp2f(fmaf(st[e], c2, -msafe));
       ps += pe;
-      pb[e >> 3][e & 7] = (T)pe;
+      const T hi = (T)pe;
+      pb[e >> 3][e & 7] = hi;
+      pbl[e >> 3][e & 7] = (T)(pe - (float)hi);
     }
     {
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ps), __float_as_uint(ps), false, false);
@@ -340,10 +345,13 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
         // (inserting the 16-bit elements one by one compiled to a wrong operand)
         const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
         const V8 va = __builtin_bit_cast(V8, make_uint4(l2.x, l2.y, h2.x, h2.y));
-        if constexpr (__is_same(T, __bf16))
+        if constexpr (__is_same(T, __bf16)) {
           oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[kb], oacc[dt], 0, 0, 0);
-        else
+          oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pbl[kb], oacc[dt], 0, 0, 0);
+        } else {
           oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[kb], oacc[dt], 0, 0, 0);
+          oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pbl[kb], oacc[dt], 0, 0, 0);
+        }
       }
     }
   };
@@ -652,7 +660,7 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
   // online softmax of each tile's rows over the slice, then O^T += V^T . P^T with each V^T
   // fragment read once for all tiles
   auto softmax_pv = [&](Tiles &st, const unsigned char *vl, int t0) {
-    V8 pb[RT][2];
+    V8 pb[RT][2], pbl[RT][2];  // P = hi + lo, both in the cache dtype
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       f32x16 &x = st.s[rt];
@@ -678,7 +686,9 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
       for (int e = 0; e < 16; ++e) {
         const float pe = __builtin_amdgcn_exp2f(fmaf(x[e], c2, -msafe));
         ps += pe;
-        pb[rt][e >> 3][e & 7] = (T)pe;
+        const T hi = (T)pe;
+        pb[rt][e >> 3][e & 7] = hi;
+        pbl[rt][e >> 3][e & 7] = (T)(pe - (float)hi);
       }
       {
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(ps), __float_as_uint(ps), false, false);
@@ -709,10 +719,13 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
         const V8 va = __builtin_bit_cast(V8, make_uint4(l2.x, l2.y, h2.x, h2.y));
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
-          if constexpr (__is_same(T, __bf16))
+          if constexpr (__is_same(T, __bf16)) {
             oacc[rt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb[rt][kb], oacc[rt][dt], 0, 0, 0);
-          else
+            oacc[rt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pbl[rt][kb], oacc[rt][dt], 0, 0, 0);
+          } else {
             oacc[rt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[rt][kb], oacc[rt][dt], 0, 0, 0);
+            oacc[rt][dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pbl[rt][kb], oacc[rt][dt], 0, 0, 0);
+          }
         }
       }
     }

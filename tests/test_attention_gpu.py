@@ -4,9 +4,11 @@ oracle's float64 restatement of lse_attn.py:42-60.
 
 Tolerances:
 - lse: absolute 1e-4. The logits are float32 MFMA dot products; the oracle is float64.
-- out, matrix-core path: the probabilities are rounded to the cache dtype for the P.V
-  product, a relative error of at most 2^-9 (bf16) or 2^-12 (fp16) per term. So out is within
-  that fraction of max|v|: atol 1e-2 (bf16) and 2e-3 (fp16).
+- out, matrix-core path: the probabilities enter the P.V product as two cache-dtype terms,
+  hi = P rounded and lo = (P - hi) rounded, a relative error of about 2^-17 (bf16) or 2^-22
+  (fp16) per term; with the float32 logits and exp, out is within ~1e-5 of the float64 oracle
+  for |v| of a few units: atol 2e-4 for both dtypes (the reference's own outputs_match
+  criterion is 1e-3, bench_kernels.py:129-131).
 - out, float32 path: 1e-4.
 """
 import math
@@ -43,7 +45,7 @@ def _oracle(cache, reqs, q, layer, kv_len=None, n_valid=None):
 
 
 def _atol(dtype):
-    return {torch.bfloat16: 1e-2, torch.float16: 2e-3, torch.float32: 1e-4}[dtype]
+    return {torch.bfloat16: 2e-4, torch.float16: 2e-4, torch.float32: 1e-4}[dtype]
 
 
 @pytest.mark.parametrize("lens,hq,hkv,n_q,dtype,causal", [
@@ -81,7 +83,7 @@ def test_reference_signature_one_query_per_request():
     assert tuple(out.shape) == (3, 32, 128) and tuple(lse.shape) == (3, 32)
     want_out, want_lse = _oracle(cache, [0, 1, 2], q.unsqueeze(1), 0)
     torch.testing.assert_close(lse.cpu(), want_lse[:, 0], rtol=0, atol=1e-4)
-    torch.testing.assert_close(out.cpu(), want_out[:, 0], rtol=0, atol=1e-2)
+    torch.testing.assert_close(out.cpu(), want_out[:, 0], rtol=0, atol=_atol(cache.kv.dtype))
 
 
 def test_all_layers_with_ragged_query_counts():
@@ -97,7 +99,7 @@ def test_all_layers_with_ragged_query_counts():
     for l in range(layers):
         want_out, want_lse = _oracle(cache, [0, 1], q[l], l, n_valid=n_valid.tolist())
         torch.testing.assert_close(lse[l].cpu(), want_lse, rtol=0, atol=1e-4)
-        torch.testing.assert_close(out[l].cpu(), want_out, rtol=0, atol=1e-2)
+        torch.testing.assert_close(out[l].cpu(), want_out, rtol=0, atol=_atol(cache.kv.dtype))
     assert torch.equal(out[:, 1, 9:].cpu(), torch.zeros(layers, n_q - 9, 32, 128))
 
 
@@ -177,7 +179,7 @@ def test_token_split_and_single_pass_agree(monkeypatch, n_q):
     want_out, want_lse = _oracle(cache, [0, 1], q, 0, kv_len=kv_len.tolist())
     for out, lse in ((split_out, split_lse), (one_out, one_lse)):
         torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
-        torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-2)
+        torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=_atol(cache.kv.dtype))
 
 
 @pytest.mark.parametrize("bs,lens,n_q,causal,split", [
@@ -207,7 +209,7 @@ def test_block_sizes_and_chunking(monkeypatch, bs, lens, n_q, causal, split):
     out, lse = cache.decode_attention(reqs, q.cuda(), kv_len=None if kv_len is None else kv_len.cuda())
     want_out, want_lse = _oracle(cache, reqs, q, 0, kv_len=None if kv_len is None else kv_len.tolist())
     torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
-    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-2)
+    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=_atol(cache.kv.dtype))
 
 
 def test_block_table_window_refill(monkeypatch):
@@ -221,7 +223,7 @@ def test_block_table_window_refill(monkeypatch):
     out, lse = cache.decode_attention([0], q.cuda())
     want_out, want_lse = _oracle(cache, [0], q, 0)
     torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
-    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-2)
+    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=_atol(cache.kv.dtype))
 
 
 @pytest.mark.parametrize("lens,hq,hkv,widen,causal", [
@@ -251,7 +253,7 @@ def test_decode_split_follows_the_longest_sequence(lens, hq, hkv, widen, causal)
                                       kv_len=None if kv_len is None else kv_len.cuda())
     want_out, want_lse = _oracle(cache, reqs, q, 0, kv_len=None if kv_len is None else kv_len.tolist())
     torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
-    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-2)
+    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=_atol(cache.kv.dtype))
     # the split does not depend on the table's width: the tight table gives the same bits
     tight_out, tight_lse = paged_decode_attention(q.cuda(), cache.kv[0], bt, seq,
                                                   kv_len=None if kv_len is None else kv_len.cuda())
@@ -269,7 +271,7 @@ def test_split_calls_of_different_shapes_share_the_workspace():
         out, lse = cache.decode_attention(reqs, q.cuda())
         want_out, want_lse = _oracle(cache, reqs, q, 0)
         torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
-        torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-2)
+        torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=_atol(cache.kv.dtype))
 
 
 def test_many_pairs_take_one_pass_without_a_workspace():
@@ -287,4 +289,4 @@ def test_many_pairs_take_one_pass_without_a_workspace():
     for l in (0, layers - 1):
         want_out, want_lse = _oracle(cache, reqs, q[l], l)
         torch.testing.assert_close(lse[l].cpu(), want_lse, rtol=0, atol=1e-4)
-        torch.testing.assert_close(out[l].cpu(), want_out, rtol=0, atol=1e-2)
+        torch.testing.assert_close(out[l].cpu(), want_out, rtol=0, atol=_atol(cache.kv.dtype))

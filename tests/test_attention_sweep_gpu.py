@@ -5,8 +5,8 @@ Each case draws: 1-5 requests of 0-6000 tokens, the GQA shape (Hq/Hkv 32/8, 16/8
 16/4), 1-80 queries per request (so both matrix-core kernels: one 32-row tile or several),
 bf16 or fp16, block 16/32/64, causal limits or none, a partial query count per request or
 none, and a block table as wide as the longest request or twice that.  Tolerances as in
-test_attention_gpu.py: lse atol 1e-4; out atol 1e-2 (bf16) / 2e-3 (fp16), the rounding of
-the probabilities to the cache dtype for the P.V product.
+test_attention_gpu.py: lse atol 1e-4; out atol 2e-4 (the probabilities enter the P.V
+product as a hi and a lo term in the cache dtype, about 16 significant bits).
 """
 import math
 import random
@@ -63,4 +63,4 @@ def test_random_shapes_match_the_oracle(seed):
         q.float(), cache.kv[0].cpu().float(), [cache.tables[r] for r in reqs], [cache.seq_used[r] for r in reqs],
         kv_len=None if kv_len is None else kv_len.tolist(), n_valid=None if n_valid is None else n_valid.tolist())
     torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
-    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-2 if dtype == torch.bfloat16 else 2e-3)
+    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=2e-4)   # P as hi + lo terms

@@ -207,3 +207,30 @@ def test_debug_compaction_check_accepts_a_correct_plan_and_catches_a_wrong_one()
         clash[0, 1] = src[0, 0]
         with pytest.raises(RuntimeError, match="disjoint"):
             _check_compaction([0, 1], seqs, kept, bs, args[0], args[1], args[2], torch.from_numpy(clash))
+
+
+@pytest.mark.parametrize("shape,perm,dtype,seq", [
+    ((300,), None, torch.float32, 257),                      # [W]
+    ((8, 300), None, torch.float32, 300),                    # [Hkv, W]
+    ((3, 8, 300), None, torch.bfloat16, 290),                # [L, Hkv, W]
+    ((2, 3, 8, 300), None, torch.float16, 111),              # [L1, L2, Hkv, W]: the leading dims collapse
+    ((3, 8, 300), (1, 0, 2), torch.float32, 200),            # heads outermost in memory: still a stride pair
+    ((8, 300, 3), (2, 0, 1), torch.float32, 300),            # [L, Hkv, W] view of a W-major buffer: copied
+    ((2, 3, 8, 300), (1, 0, 2, 3), torch.float32, 64),       # leading dims that do not collapse: copied
+    ((3, 8, 300), None, torch.float64, 150),                 # not a kernel dtype: converted
+])
+def test_scores_layout_addresses_the_same_scores(shape, perm, dtype, seq):
+    """The eviction reads scores in place through (L, H, layer stride, head stride) with a unit
+    last stride: the geometry it derives must address exactly scores[..., h, t] for t < seq,
+    whether the tensor is used as it is or copied first."""
+    from actkv.paged import _scores_layout
+    g = torch.Generator().manual_seed(len(shape) * 1000 + seq)
+    base = torch.rand(*shape, generator=g).to(dtype)
+    scores = base.permute(*perm) if perm else base
+    t, L, H, s_sl, s_sh = _scores_layout(scores, seq)
+    assert t.dtype in (torch.float32, torch.float16, torch.bfloat16) and t.stride(-1) == 1
+    want = scores[..., :seq].reshape(L, H, seq).to(t.dtype)
+    got = torch.as_strided(t, (L, H, seq), (s_sl, s_sh, 1), t.storage_offset())
+    assert torch.equal(got, want)
+    with pytest.raises(ValueError):
+        _scores_layout(scores, scores.shape[-1] + 1)

@@ -229,6 +229,7 @@ class PagedKVCache:
         self.device = device
         self._pin_count: dict[int, tuple] = {}      # req -> (tensor, version, count): avoids a sync
         self._dev_cache: dict = {}                  # device copies of unchanged block tables
+        self._dev_rows: dict = {}                   # req -> (batch entry key, row) of _dev_cache
         self._const_cache: dict = {}                # device copies of budget / protected-count lists
 
     # ---------------------------------------------------------------- allocation
@@ -387,20 +388,37 @@ class PagedKVCache:
             return torch.from_numpy(host.copy()).to(self.device)
         return _hip.upload_i32(host, torch.device(self.device))
 
-    def _device_tables(self, reqs, ys=None):
+    def _device_tables(self, reqs, ys=None, shared_rows=False):
         """(seq_used [R], block_table [R, MB]) int32 on the device, reused while the requests'
-        tables and lengths are unchanged (the device copy is never handed to callers)."""
+        tables and lengths are unchanged (the device copy is never handed to callers).
+        shared_rows: one request may also be served by its row of a batch's device copy (the
+        row keeps the batch's MB columns), as when the reference's loop evicts requests one by
+        one after one cal_attn over all of them; callers whose checks depend on MB leave it off."""
         key = tuple(reqs), tuple(ys) if ys is not None else None
         hit = self._dev_cache.get(key)
+        tables, seq_used = self.tables, self.seq_used
         if hit is not None:
             # the entry holds the table objects themselves: identity, not id(), decides a hit,
             # then each table's mutation count, length and the request's length
-            tables, seq_used = self.tables, self.seq_used
             for r, t, (ver, n, s) in zip(reqs, hit[0], hit[1]):
                 if tables[r] is not t or t.version != ver or len(t) != n or seq_used[r] != s:
                     break
             else:
                 return hit[2], hit[3]
+        if shared_rows and ys is None and len(reqs) == 1:
+            r = reqs[0]
+            t = tables[r]
+            row_key = (key[0], "row")   # apart from the request's own copy: its MB differs
+            for ent, j, own in ((self._dev_cache.get(row_key), 0, True), (*self._batch_row(r), False)):
+                if ent is None:
+                    continue
+                ver, n, s = ent[1][j]
+                if ent[0][j] is t and t.version == ver and len(t) == n and seq_used[r] == s:
+                    if own:
+                        return ent[2], ent[3]
+                    seq, bt = ent[2][j:j + 1], ent[3][j:j + 1]
+                    self._dev_cache[row_key] = ((t,), ((ver, n, s),), seq, bt)
+                    return seq, bt
         host, mb = self._host_tables(reqs, ys)
         dev = self._upload(host)
         r_n = len(reqs)
@@ -409,9 +427,20 @@ class PagedKVCache:
         if all(isinstance(t, _Table) for t in tabs):   # plain lists carry no mutation count
             if len(self._dev_cache) > 64:
                 self._dev_cache.clear()
+                self._dev_rows.clear()
             self._dev_cache[key] = (tabs, tuple((t.version, len(t), self.seq_used[r]) for t, r in zip(tabs, reqs)),
                                     seq, bt)
+            if r_n > 1 and ys is None:
+                for j, r in enumerate(reqs):
+                    self._dev_rows[r] = (key, j)
         return seq, bt
+
+    def _batch_row(self, r):
+        """(cache entry, row) of the last batch device copy that holds request r, or (None, 0)."""
+        row = self._dev_rows.get(r)
+        if row is None:
+            return None, 0
+        return self._dev_cache.get(row[0]), row[1]
 
     def _device_consts(self, values: tuple) -> torch.Tensor:
         """int32 device tensor holding `values`, shared by every call with the same values.
@@ -665,7 +694,7 @@ class PagedKVCache:
             s_sl, s_sr, s_sh, _ = sc.stride()
         # the lengths come with the block tables the compaction launch reads anyway; budgets and
         # protected counts are the same from call to call in an eviction loop
-        tables = self._device_tables(a_reqs)
+        tables = self._device_tables(a_reqs, shared_rows=True)
         consts = self._device_consts(tuple(max(budgets[i], 0) for i in active) + tuple(counts))
         if all(p is None for p in pinneds):           # every request's pins are a prefix count
             pin_mat, prot_count = None, consts[ra:]

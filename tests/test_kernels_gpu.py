@@ -448,6 +448,37 @@ def test_batched_evict_mixes_first_and_repeated_evictions():
     _assert_same_state(cache, model)
 
 
+def test_per_request_evicts_after_one_batched_cal_attn_match_the_oracle():
+    """The reference bench's step (benchmarks/bench_kernels.py:81-89): one cal_attn over every
+    request, then evict of each request in a Python loop.  The evictions read their tables from
+    the rows of the batch's device copy; the whole state still matches oracle evicts, also when
+    a request grew after the batch's tables were uploaded (its row is stale and is not used)
+    and when the loop runs a second time on the compacted cache."""
+    lens = [300, 41, 517, 160]
+    cache = _filled_cache(lens, hkv=2, d=32, layers=1, seed=31)
+    model = _model_of(cache)
+    g = torch.Generator().manual_seed(32)
+    reqs = list(range(len(lens)))
+    for rnd in range(2):
+        q = torch.randn(len(reqs), 4, 32, generator=g).cuda()
+        lse = torch.full((len(reqs), 4), 3.0, device="cuda")
+        width = (max(len(cache.tables[r]) for r in reqs) + 4) * cache.block_size
+        out = torch.zeros(len(reqs), 2, width, device="cuda")
+        n_seen = torch.zeros(len(reqs), dtype=torch.int32, device="cuda")
+        cache.cal_attn(reqs, q, lse, out, n_seen)
+        if rnd == 1:   # request 2 grows after the batch's tables were uploaded (scores 0 there)
+            k = torch.randn(1, 20, 2, 32, generator=g)
+            cache.append(2, k.cuda(), k.cuda())
+            model.append(2, _bits(k), _bits(k))
+        scores = out.cpu()
+        for r in reqs:
+            budget = max(cache.seq_used[r] // 3, 1)
+            perm = cache.evict(r, out[r], budget, protected=2)
+            want = model.evict(r, scores[r, :, : model.seq_used[r]], budget, protected=2, tie_rule="lowest")
+            assert np.array_equal(perm.cpu().numpy(), want), (rnd, r)
+        _assert_same_state(cache, model)
+
+
 def test_launches_follow_torch_current_stream():
     """The library launches on torch's current stream, including inside `torch.cuda.stream`."""
     from actkv import _hip

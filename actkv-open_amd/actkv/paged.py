@@ -231,6 +231,7 @@ class PagedKVCache:
         self._dev_cache: dict = {}                  # device copies of unchanged block tables
         self._dev_rows: dict = {}                   # req -> (batch entry key, row) of _dev_cache
         self._const_cache: dict = {}                # device copies of budget / protected-count lists
+        self._kv_dev = self.kv.device               # keys the two device caches by stream
 
     # ---------------------------------------------------------------- allocation
     @property
@@ -393,8 +394,13 @@ class PagedKVCache:
         tables and lengths are unchanged (the device copy is never handed to callers).
         shared_rows: one request may also be served by its row of a batch's device copy (the
         row keeps the batch's MB columns), as when the reference's loop evicts requests one by
-        one after one cal_attn over all of them; callers whose checks depend on MB leave it off."""
-        key = tuple(reqs), tuple(ys) if ys is not None else None
+        one after one cal_attn over all of them; callers whose checks depend on MB leave it off.
+
+        Entries are kept per stream: an upload is queued on the stream current at the time, so
+        only work on that stream is ordered after it, and only that stream's later allocations
+        can reuse the memory once the entry is dropped."""
+        cur = self._stream_key()
+        key = cur, tuple(reqs), tuple(ys) if ys is not None else None
         hit = self._dev_cache.get(key)
         tables, seq_used = self.tables, self.seq_used
         if hit is not None:
@@ -408,8 +414,8 @@ class PagedKVCache:
         if shared_rows and ys is None and len(reqs) == 1:
             r = reqs[0]
             t = tables[r]
-            row_key = (key[0], "row")   # apart from the request's own copy: its MB differs
-            for ent, j, own in ((self._dev_cache.get(row_key), 0, True), (*self._batch_row(r), False)):
+            row_key = (cur, key[1], "row")   # apart from the request's own copy: its MB differs
+            for ent, j, own in ((self._dev_cache.get(row_key), 0, True), (*self._batch_row(r, cur), False)):
                 if ent is None:
                     continue
                 ver, n, s = ent[1][j]
@@ -435,22 +441,30 @@ class PagedKVCache:
                     self._dev_rows[r] = (key, j)
         return seq, bt
 
-    def _batch_row(self, r):
-        """(cache entry, row) of the last batch device copy that holds request r, or (None, 0)."""
+    def _stream_key(self) -> int:
+        """The current stream of the cache's device (0 on the CPU)."""
+        dev = self._kv_dev
+        return _hip.stream(dev) if dev.type == "cuda" else 0
+
+    def _batch_row(self, r, cur):
+        """(cache entry, row) of the last batch device copy that holds request r, uploaded on
+        stream `cur`, or (None, 0)."""
         row = self._dev_rows.get(r)
-        if row is None:
+        if row is None or row[0][0] != cur:
             return None, 0
         return self._dev_cache.get(row[0]), row[1]
 
     def _device_consts(self, values: tuple) -> torch.Tensor:
         """int32 device tensor holding `values`, shared by every call with the same values.
         Only for kernel inputs the kernels never write (budgets, protected counts): an
-        eviction loop with fixed budgets then uploads nothing per call."""
-        t = self._const_cache.get(values)
+        eviction loop with fixed budgets then uploads nothing per call.  Kept per stream, as
+        the device tables are."""
+        key = (self._stream_key(), values)
+        t = self._const_cache.get(key)
         if t is None:
             if len(self._const_cache) > 256:
                 self._const_cache.clear()
-            t = self._const_cache[values] = self._upload(np.array(values, dtype=np.int32))
+            t = self._const_cache[key] = self._upload(np.array(values, dtype=np.int32))
         return t
 
     def block_table(self, reqs: list[int]) -> torch.Tensor:

@@ -2,7 +2,8 @@
 //
 // Reference: actkv/paged.py:23-46 (keep_mask_from_scores).  Two launches,
 // batched over requests:
-//   keys   : grid (ceil(max_seq/128), R), 512 threads.  Per token, reduce KV
+//   keys   : grid (ceil(max_seq/TOK), R), 512 threads, TOK = 128 tokens per
+//            block up to 120 layers, 64 up to 256.  Per token, reduce KV
 //            heads (mean|max) then average layers, with the float32 order of
 //            torch's CPU `mean` so s[t] is bit-identical to the reference, and
 //            write an order-preserving uint32 key (0 marks a protected token).
@@ -35,10 +36,12 @@ namespace actkv {
 
 constexpr int HIST_BINS = 2048;
 constexpr int KT = 512;                 // threads per keys block
-constexpr int TOK = 128;                // tokens per keys block
+constexpr int TOK_WIDE = 128;           // tokens per keys block up to MAX_LAYERS_WIDE layers
+constexpr int TOK_NARROW = 64;          // ... and up to MAX_LAYERS (one wave of tokens)
 constexpr int SEL_T = 1024;             // threads per select block
 constexpr int CAND_CAP = 1536;          // window candidates the select block holds in LDS
-constexpr int MAX_LAYERS = 120;         // [L][TOK] layer values fit 60 KiB of LDS
+constexpr int MAX_LAYERS_WIDE = 120;    // [L][TOK] layer values fit 64 KiB of LDS:
+constexpr int MAX_LAYERS = 256;         // 120 x 128 and 256 x 64 floats
 
 struct KeepArgs {
   const void *scores;
@@ -509,6 +512,7 @@ __global__ void __launch_bounds__(SEL_T) keep_select_kernel(KeepArgs a) {
 // tokens (one wave) the candidate count and the smallest and largest candidate
 // key, which the select kernel reduces instead of passing over the keys.  lvals
 // [L][TOK] holds the head-reduced score of each (layer, token) of the block.
+template <int TOK>
 __device__ __forceinline__ void write_keys(const KeepArgs &a, int r, int S, int t0, const float *lvals) {
   const int tok = threadIdx.x;
   if (tok >= TOK) return;                  // the first TOK / 64 waves, whole
@@ -527,19 +531,20 @@ __device__ __forceinline__ void write_keys(const KeepArgs &a, int r, int S, int 
   if ((tok & 63) == 0 && t < S) a.stats[(int64_t)r * a.stats_sr + t / 64] = make_uint4(n, mn, mx, 0u);
 }
 
-// float32 scores with 16-byte aligned token rows: thread (layer group tid/32,
-// quad tid%32) reduces the HH heads of 4 consecutive tokens with 16-byte loads,
+// float32 scores with 16-byte aligned token rows: thread (layer group tid/(TOK/4),
+// quad tid%(TOK/4)) reduces the HH heads of 4 consecutive tokens with 16-byte loads,
 // up to three layers' loads in flight at once.  Same per-token float order as the
 // generic kernel (a 4-token quad lies wholly in or out of the torch body:
 // torch_body_end is a multiple of 4).
-template <int HH>
+template <int HH, int TOK>
 __global__ void __launch_bounds__(KT) keep_vec4_kernel(KeepArgs a) {
+  constexpr int QUADS = TOK / 4, LGROUPS = KT / QUADS;
   extern __shared__ __attribute__((aligned(16))) float lvals[];  // [L][TOK]
   const int r = blockIdx.y;
   const int S = min(max(a.seq_used[r], 0), a.max_seq);
   const int t0 = blockIdx.x * TOK;
   if (t0 >= S) return;
-  const int quad = threadIdx.x & 31, lg = threadIdx.x >> 5;  // 16 layer groups
+  const int quad = threadIdx.x % QUADS, lg = threadIdx.x / QUADS;
   const int tq = t0 + 4 * quad;
   const bool body4 = tq < torch_body_end(S);
   const float *sbase = (const float *)a.scores + (int64_t)r * a.s_sr + tq;
@@ -553,11 +558,11 @@ __global__ void __launch_bounds__(KT) keep_vec4_kernel(KeepArgs a) {
   // layers whose loads are in flight together (16 heads: one, within the registers)
   constexpr int LIF = HH <= 8 ? 3 : 1;
   if (tq < S) {
-    for (int l0 = lg; l0 < a.L; l0 += 16 * LIF) {
+    for (int l0 = lg; l0 < a.L; l0 += LGROUPS * LIF) {
       f32x4 hv[LIF][HH];
 #pragma unroll
       for (int it = 0; it < LIF; ++it) {
-        const int l = l0 + 16 * it;
+        const int l = l0 + LGROUPS * it;
         if (l < a.L) {
 #pragma unroll
           for (int hh = 0; hh < HH; ++hh) hv[it][hh] = load4(sbase + (int64_t)l * a.s_sl + (int64_t)hh * a.s_sh);
@@ -565,7 +570,7 @@ __global__ void __launch_bounds__(KT) keep_vec4_kernel(KeepArgs a) {
       }
 #pragma unroll
       for (int it = 0; it < LIF; ++it) {
-        const int l = l0 + 16 * it;
+        const int l = l0 + LGROUPS * it;
         if (l >= a.L) continue;
         f32x4 v;
         if (a.head_reduce == ACTKV_REDUCE_MAX) {
@@ -587,12 +592,12 @@ __global__ void __launch_bounds__(KT) keep_vec4_kernel(KeepArgs a) {
     }
   }
   __syncthreads();
-  write_keys(a, r, S, t0, lvals);
+  write_keys<TOK>(a, r, S, t0, lvals);
 }
 
 // Any score dtype, head count and stride: thread (layer group tid/128, token
-// tid%128), one element per load.
-template <typename SCT>
+// tid%TOK), one element per load.
+template <typename SCT, int TOK>
 __global__ void __launch_bounds__(KT) keep_generic_kernel(KeepArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lvals[];  // [L][TOK]
   const int r = blockIdx.y;
@@ -618,7 +623,7 @@ __global__ void __launch_bounds__(KT) keep_generic_kernel(KeepArgs a) {
     }
   }
   __syncthreads();
-  write_keys(a, r, S, t0, lvals);
+  write_keys<TOK>(a, r, S, t0, lvals);
 }
 
 // grid R, 1024 threads: pack bool [S] -> bits (zero-padded to whole blocks)
@@ -696,21 +701,29 @@ static int keep_mask_impl(const void *scores, int scores_dtype, int64_t s_sl, in
 
   const bool vec4 = scores_dtype == ACTKV_F32 && ((uintptr_t)scores & 15) == 0 && s_sl % 4 == 0 &&
                     s_sr % 4 == 0 && s_sh % 4 == 0 && (H == 1 || H == 2 || H == 4 || H == 8 || H == 16);
-  const dim3 grid((unsigned)((max_seq + TOK - 1) / TOK), (unsigned)R);
-  const size_t shm = (size_t)L * TOK * sizeof(float);
-  if (vec4) {
-    switch (H) {
-      case 1: hipLaunchKernelGGL(keep_vec4_kernel<1>, grid, dim3(KT), shm, st, a); break;
-      case 2: hipLaunchKernelGGL(keep_vec4_kernel<2>, grid, dim3(KT), shm, st, a); break;
-      case 4: hipLaunchKernelGGL(keep_vec4_kernel<4>, grid, dim3(KT), shm, st, a); break;
-      case 8: hipLaunchKernelGGL(keep_vec4_kernel<8>, grid, dim3(KT), shm, st, a); break;
-      default: hipLaunchKernelGGL(keep_vec4_kernel<16>, grid, dim3(KT), shm, st, a); break;
+  // [L][TOK] floats of LDS per block: 128 tokens up to 120 layers, 64 beyond
+  const bool wide = L <= MAX_LAYERS_WIDE;
+  const int tok = wide ? TOK_WIDE : TOK_NARROW;
+  const dim3 grid((unsigned)((max_seq + tok - 1) / tok), (unsigned)R);
+  const size_t shm = (size_t)L * tok * sizeof(float);
+  auto launch = [&](auto tokc) {
+    constexpr int TK = decltype(tokc)::value;
+    if (vec4) {
+      switch (H) {
+        case 1: hipLaunchKernelGGL((keep_vec4_kernel<1, TK>), grid, dim3(KT), shm, st, a); break;
+        case 2: hipLaunchKernelGGL((keep_vec4_kernel<2, TK>), grid, dim3(KT), shm, st, a); break;
+        case 4: hipLaunchKernelGGL((keep_vec4_kernel<4, TK>), grid, dim3(KT), shm, st, a); break;
+        case 8: hipLaunchKernelGGL((keep_vec4_kernel<8, TK>), grid, dim3(KT), shm, st, a); break;
+        default: hipLaunchKernelGGL((keep_vec4_kernel<16, TK>), grid, dim3(KT), shm, st, a); break;
+      }
+    } else switch (scores_dtype) {
+      case ACTKV_F32: hipLaunchKernelGGL((keep_generic_kernel<float, TK>), grid, dim3(KT), shm, st, a); break;
+      case ACTKV_F16: hipLaunchKernelGGL((keep_generic_kernel<_Float16, TK>), grid, dim3(KT), shm, st, a); break;
+      default: hipLaunchKernelGGL((keep_generic_kernel<__bf16, TK>), grid, dim3(KT), shm, st, a); break;
     }
-  } else switch (scores_dtype) {
-    case ACTKV_F32: hipLaunchKernelGGL(keep_generic_kernel<float>, grid, dim3(KT), shm, st, a); break;
-    case ACTKV_F16: hipLaunchKernelGGL(keep_generic_kernel<_Float16>, grid, dim3(KT), shm, st, a); break;
-    default: hipLaunchKernelGGL(keep_generic_kernel<__bf16>, grid, dim3(KT), shm, st, a); break;
-  }
+  };
+  if (wide) launch(std::integral_constant<int, TOK_WIDE>());
+  else launch(std::integral_constant<int, TOK_NARROW>());
   int rc = actkv_check_launch();
   if (rc) return rc;
   hipLaunchKernelGGL(keep_select_kernel, dim3(R), dim3(SEL_T), 0, st, a);

@@ -12,12 +12,14 @@
 //   ks[t]   = decay * ks[t], then + act[t] where hit (two roundings, as
 //             ks.mul_(decay); ks[hit] += a[hit])
 // The nucleus is found without sorting: three radix passes (11/11/10 bits of
-// the float key) over LDS histograms holding, per bin, the count and the
-// float64 sum of the values; walking the bins from the top finds the bin where
-// the running sum crosses the threshold, the last pass fixes the exact value,
-// and the tied entries at that value are taken in index order.  Sums are
-// float64 and compared after rounding to float32, as torch's cumsum stores
-// float64 running sums as float32.
+// the float key) over LDS histograms holding, per bin, the count and the sum
+// of the values; walking the bins from the top finds the bin where the running
+// sum crosses the threshold, the last pass fixes the exact value, and the tied
+// entries at that value are taken in index order.  The bin sums are fixed-point
+// integers (each value scaled by 2^(61-E), E the total's exponent), so 64-bit
+// integer atomics give the same bits in any order; running sums are compared
+// after rounding to float32, as torch's cumsum stores its float64 running sums
+// as float32.
 #include "common.h"
 #include "torch_order.h"
 

@@ -363,7 +363,9 @@ score_kslice_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
       const float v = psum[tt] + __shfl_xor(psum[tt], 32, 64);
       mine = (TT == 1 || lh == tt) ? v : mine;
     }
-    if (t_own < t_end && (TT == 2 || lh == 0)) obase[t_own] = (old * fn0 + mine) / fden;
+    // a token in a block the table marks invalid keeps its score, as in the other kernels
+    if (t_own < t_end && (TT == 2 || lh == 0) && bts[(t_own >> bs_shift) - b0] >= 0)
+      obase[t_own] = (old * fn0 + mine) / fden;
   };
 
   const int step = NW * SLICE;

@@ -129,7 +129,7 @@ int actkv_copy_slots(void *kv_flat, int64_t planes, int64_t stride_plane_bytes,
  * input of actkv_compact.  Either may be NULL, not both.
  * workspace must hold actkv_workspace_size(ACTKV_WS_KEEP_MASK, R, max_seq)
  * bytes (the per-token keys); it needs no initialisation.  Calls that share a
- * workspace must be stream-ordered.  Limits: L <= 120 (ACTKV_ERR_UNSUPPORTED
+ * workspace must be stream-ordered.  Limits: L <= 256 (ACTKV_ERR_UNSUPPORTED
  * beyond).
  */
 int actkv_keep_mask(const void *scores, int scores_dtype, int64_t s_sl, int64_t s_sr,
@@ -145,8 +145,8 @@ int actkv_keep_mask(const void *scores, int scores_dtype, int64_t s_sl, int64_t 
  *
  * No counterpart in the reference: an addition for callers that cannot allocate device
  * memory (code under HIP graph capture, serving loops that forbid allocation).  Same
- * arguments, results and errors as actkv_keep_mask, minus the workspace: the keys,
- * histogram and selection live in a file-scope device array of
+ * arguments, results and errors as actkv_keep_mask, minus the workspace: the per-token
+ * keys and the per-64-token candidate statistics live in a file-scope device array of
  * ACTKV_KEEP_MASK_SCRATCH_BYTES bytes per GPU, held from the library's load until the
  * process ends.  Calls whose actkv_workspace_size(ACTKV_WS_KEEP_MASK, R, max_seq) exceeds
  * it return ACTKV_ERR_WORKSPACE and launch nothing.  The array's address is looked up on
@@ -294,8 +294,9 @@ size_t actkv_lrfu_workspace_size(int L, int R, int max_seq);
  * out : float32 [L, R, N, Hq, D], strides o_sl o_sr o_sn o_sh, unit last
  * lse : float32 [L, R, N, Hq], strides lse_sl lse_sr lse_sn, unit last
  * bf16/fp16 with D = 128 and Hq/Hkv in {1, 2, 4} run on the matrix cores
- * (probabilities rounded to the cache dtype for the P.V product, float32
- * accumulation); every other case uses float32 dot products.  D <= 512.
+ * (each probability enters the P.V product as a hi and a lo term in the cache
+ * dtype, P = hi + lo to about 2^-16 relative, float32 accumulation); every other
+ * case uses float32 dot products.  D <= 512.
  * workspace: optional, actkv_paged_attention_workspace_size(...) bytes, any
  * contents.  With it, long sequences are split into token chunks attended in
  * parallel and merged by a second launch (flash-decoding); without it (NULL or

@@ -242,6 +242,33 @@ def test_evict_keeps_the_protected_prefix_and_the_top_scored_tokens():
     assert np.array_equal(cache.pinned[0].cpu().numpy(), model.pinned[0])
 
 
+def test_evictions_on_two_side_streams_match_the_oracle():
+    """Evictions with equal budgets on two side streams (ordered by a stream wait, as calls that
+    share the keep-mask workspace must be): the budget and table uploads of one stream are not
+    read by the other stream's kernels, and the final state equals the oracle's."""
+    cache = _filled_cache([300, 500, 260], hkv=2, d=16, seed=41)
+    model = _model_of(cache)
+    g = torch.Generator().manual_seed(42)
+    sc = [torch.rand(2, n, generator=g) for n in (300, 500, 260)]
+    dev_sc = [s.cuda() for s in sc]
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Stream(), torch.cuda.Stream()
+    perms = []
+    with torch.cuda.stream(a):
+        perms.append(cache.evict(0, dev_sc[0], budget=100, protected=4))
+    b.wait_stream(a)
+    with torch.cuda.stream(b):
+        perms.append(cache.evict(1, dev_sc[1], budget=100, protected=4))
+    a.wait_stream(b)
+    with torch.cuda.stream(a):
+        perms.append(cache.evict(2, dev_sc[2], budget=100, protected=4))
+    torch.cuda.synchronize()
+    for r in range(3):
+        want = model.evict(r, sc[r], budget=100, protected=4)
+        assert np.array_equal(perms[r].cpu().numpy(), want)
+    _assert_same_state(cache, model)
+
+
 def test_evict_within_budget_is_a_no_op():
     cache = _filled_cache([20])
     table = list(cache.tables[0])
@@ -285,7 +312,9 @@ def test_evict_keeps_the_protected_tokens_across_repeated_evictions():
     # query tiles of 385..512 rows (query tile in registers) and 257..384 rows (K slices)
     (torch.bfloat16, 32, 8, 128, 16, 100), (torch.float16, 16, 8, 128, 16, 150),
     (torch.bfloat16, 8, 8, 128, 16, 300), (torch.float16, 32, 8, 128, 16, 128),
-    (torch.bfloat16, 16, 8, 128, 64, 200)])
+    (torch.bfloat16, 16, 8, 128, 64, 200),
+    # G = 1 with 400 query rows: the query-register kernel's per-row causal limits
+    (torch.bfloat16, 8, 8, 128, 16, 400)])
 def test_action_scores_causal_region_and_ragged_query_counts(dtype, hq, hkv, d, bs, n_q):
     """kv_len (query n sees tokens t < kv_len[r, n]) and n_valid (request r folds its first
     n_valid[r] queries): the causal action region of an agent round (additive extension)."""
@@ -311,6 +340,50 @@ def test_action_scores_causal_region_and_ragged_query_counts(dtype, hq, hkv, d, 
     rtol = 1e-4 if dtype == torch.float32 else 1e-3
     torch.testing.assert_close(out_k.cpu(), out_o, rtol=rtol, atol=1e-6)
     assert torch.equal(n_k.cpu(), n_o)
+
+
+@pytest.mark.parametrize("dtype,hq,hkv,d,n_q", [
+    (torch.float32, 8, 2, 32, 5),            # generic kernel
+    (torch.bfloat16, 32, 8, 128, 80),        # 320 query rows: K-slice kernel
+    (torch.bfloat16, 32, 8, 128, 100),       # 400 query rows: query-register kernel
+    (torch.float16, 16, 8, 128, 24),         # 48 rows, causal below
+])
+def test_action_scores_leave_tokens_of_out_of_pool_blocks_untouched(dtype, hq, hkv, d, n_q):
+    """A block-table entry outside [0, num_blocks) inside seq_used: every kernel reads in bounds
+    and leaves that block's score columns as they were; every other column is scored."""
+    lens = [600, 333]
+    bs = 16
+    cache = _filled_cache(lens, bs=bs, hkv=hkv, d=d, dtype=dtype, seed=21)
+    reqs = [0, 1]
+    bt, seq = cache.block_table(reqs), cache.seq_tensor(reqs)
+    width = bt.shape[1] * bs
+    g = torch.Generator().manual_seed(22)
+    q = torch.randn(2, n_q, hq, d, generator=g).to(dtype)
+    kv0 = cache.kv[0].cpu()
+    tables = [cache.tables[r] for r in reqs]
+    lse = torch.stack([ref.decode_lse(q[:, n], kv0, tables, lens) for n in range(n_q)], 1)
+    out0 = torch.rand(2, hkv, width, generator=g)
+    kv_len = None
+    if n_q == 24:
+        kv_len = torch.stack([torch.randint(1, s + 1, (n_q,), generator=g) for s in lens]).to(torch.int32)
+    bad = bt.clone()
+    bad[0, 3] = -1                       # tokens 48..63 of request 0
+    bad[1, 10] = cache.num_blocks + 7    # tokens 160..175 of request 1
+    out_k = out0.cuda()
+    action_scores(q.cuda(), cache.kv[0], bad, seq, lse.cuda(), out_k,
+                  torch.zeros(2, dtype=torch.int32, device="cuda"),
+                  kv_len=None if kv_len is None else kv_len.cuda())
+    out_o = out0.clone()
+    ref.action_scores_nfold(q, kv0, tables, lens, lse, out_o, torch.zeros(2, dtype=torch.int32), kv_len=kv_len)
+    got = out_k.cpu()
+    untouched = torch.zeros(2, width, dtype=torch.bool)
+    untouched[0, 48:64] = True
+    untouched[1, 160:176] = True
+    for r in range(2):
+        assert torch.equal(got[r][:, untouched[r]], out0[r][:, untouched[r]])
+        keep = ~untouched[r]
+        rtol = 1e-4 if dtype == torch.float32 else 1e-3
+        torch.testing.assert_close(got[r][:, keep], out_o[r][:, keep], rtol=rtol, atol=1e-6)
 
 
 def test_action_scores_every_layer_in_one_launch():
@@ -345,6 +418,10 @@ def test_action_scores_every_layer_in_one_launch():
     (40, 16, 513, 520, 64, 2, "mean"),       # 16 heads: a full cascade block per layer
     (5, 8, 1001, 1001, 99, 3, "mean"),       # rows not 16-byte aligned: the 4-byte load path
     (2, 4, 2050, 2052, 200, 0, "max"),       # 4 heads, a last quad with 2 tokens
+    # more than 120 layers: 64-token key blocks
+    (121, 8, 1500, 1504, 150, 4, "mean"),
+    (256, 2, 700, 704, 70, 0, "max"),
+    (200, 3, 333, 333, 33, 2, "mean"),       # unaligned rows: the one-element load path
 ])
 def test_keep_mask_bit_exact_with_the_oracle(L, H, S, W, budget, prot, reduce):
     """The device reduction reproduces torch's CPU mean bit for bit, so the keep mask equals

@@ -23,6 +23,8 @@
 #include "common.h"
 
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 
 namespace actkv {
@@ -58,6 +60,34 @@ struct ScoreArgs {
 // IEEE maximum (NaN-propagating, as torch's amax): lowers to v_maximum3_f32 on
 // gfx950 without the operand canonicalisation fmaxf needs.
 __device__ __forceinline__ float vmax(float x, float y) { return __builtin_elementwise_maximum(x, y); }
+
+// Workgroup barrier for LDS hand-overs that leaves VM loads in flight: this wave's LDS
+// reads and writes complete (lgkmcnt(0)) and at most VM of its vector memory operations
+// are outstanding, then s_barrier; the empty asm statements keep the compiler from moving
+// memory accesses across it.  __syncthreads() would fence every address space, and its
+// fence waits vmcnt(0) (loads into LDS write LDS too), draining every K chunk in flight.
+// Loads from global memory into LDS (lane i writes bytes [i*W, i*W + W) at lds_addr,
+// W = 16 or 4).  Issued as assembly so the compiler's wait insertion does not track them:
+// it cannot tell which LDS array such a load writes, and waits for all of them (vmcnt(0))
+// before any later LDS access.  Every wait for these loads is explicit in the kernel.
+__device__ __forceinline__ void load_lds16(const void *gptr, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(gptr), "s"(lds_addr) : "memory", "m0");
+}
+__device__ __forceinline__ void load_lds4(const void *gptr, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" :: "v"(gptr), "s"(lds_addr) : "memory", "m0");
+}
+__device__ __forceinline__ uint32_t lds_address(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+
+template <int VM>
+__device__ __forceinline__ void lds_barrier() {
+  static_assert(VM >= 0 && VM < 16, "vmcnt low bits");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0070 | VM);   // vmcnt(VM) expcnt(7) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 __device__ __forceinline__ int seq_len_of(const ScoreArgs &a, int r) {
   int s = a.seq_used[r];
@@ -386,13 +416,15 @@ score_kslice_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
 }
 
 // ------------------------------------------------------------------ MFMA, query tile in registers
-// For query tiles of 385..512 rows.  One workgroup of 8 waves (2 per SIMD) owns
-// a (layer, request, KV head) pair and a token range.  The pair's action-query
-// tile -- rows (query n, group head g), nq*G <= 512 of them, head_dim 128,
-// bf16/fp16 -- is split over 8 row groups of 64 rows: each wave keeps its two
-// 32-row tiles as MFMA A operands in registers for the whole range, with their
-// accumulator seeds -lse/scale (-inf for padding rows, which then add
-// exp2(-inf) = 0) as the C operand of each chain's first MFMA.
+// One workgroup of 8 waves (2 per SIMD) owns a (layer, request, KV head) pair and
+// a token range.  The pair's action-query tile -- rows (query n, group head g),
+// nq*G <= 64*RG of them, head_dim 128, bf16/fp16 -- is split over RG row groups
+// of 64 rows, and the 8 waves over RG row groups x 8/RG token groups: wave
+// (rg, tg) keeps row group rg's two 32-row tiles as MFMA A operands in registers
+// for the whole range, with their accumulator seeds -lse/scale (-inf for padding
+// rows, which then add exp2(-inf) = 0) as the C operand of each chain's first
+// MFMA, and multiplies the 32-token tiles tg, tg + 8/RG, ... of every chunk.
+// RG = 8 for 385..512 rows, 4 up to 256 and 2 up to 128: every wave has rows.
 //
 // K streams through LDS in chunks of CH tokens, double buffered: the waves load
 // chunk c+1 straight from HBM into LDS (global_load_lds_dwordx4) while they
@@ -414,21 +446,26 @@ score_kslice_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
 // tile.  Per-token partial sums (one per row group and lane half) go to LDS at
 // the end of the chunk; after the next barrier the first CH threads add them in
 // a fixed order and write the running means.
-template <typename T, typename V8, int G, bool CAUSAL>
+template <typename T, typename V8, int G, bool CAUSAL, int RG, int NBUF, bool SWZ>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
-  constexpr int NW = 8, RG = 8, TG = NW / RG, KS = 8, QG = 4 / G;
+  constexpr int NW = 8, TG = NW / RG, KS = 8, QG = 4 / G;
+  static_assert(RG == 2 || RG == 4 || RG == 8, "row groups");
+  static_assert(NBUF >= 2 && NBUF <= 4, "K chunk buffers");
   constexpr int TPC = QREG_CHUNK / 32;  // 32-token tiles per chunk
   constexpr int CH = QREG_CHUNK;        // tokens per chunk
   constexpr int NT = TPC / TG;          // tiles per wave per chunk
   constexpr int LPW = TPC * KS / NW;    // fragment loads per wave per chunk
   constexpr int NRED = 2 * RG;          // partial sums per token
   static_assert(KS % LPW == 0, "a wave's loads stay within one tile");
-  // the two K buffers are distinct arrays: the compiler then knows that reads of
-  // one need not wait for the loads in flight into the other
+  // the K buffers are distinct arrays: the compiler then knows that reads of one
+  // need not wait for the loads in flight into the others
   __shared__ __attribute__((aligned(16))) unsigned char kbuf_a[TPC * KS * 1024];
   __shared__ __attribute__((aligned(16))) unsigned char kbuf_b[TPC * KS * 1024];
+  __shared__ __attribute__((aligned(16))) unsigned char kbuf_c[NBUF >= 3 ? TPC * KS * 1024 : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char kbuf_d[NBUF >= 4 ? TPC * KS * 1024 : 16];
   __shared__ float red[2][NRED][CH];
+  __shared__ float oldm[8][CH];   // running means of the chunks in flight, ring of 8 >= NBUF + 1
   __shared__ int bts[MFMA_MAX_TOKENS / 16];
 
   // XCD-aware work mapping: all token ranges of one (layer, request, head)
@@ -501,35 +538,76 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
     }
   }
   if (tid < nbt) bts[tid] = (bt_own >= 0 && bt_own < a.num_blocks) ? bt_own : -1;
+  // every set-up load has landed: the chunk loop's counts of vector memory operations
+  // start from zero, and no later wait for the query tile drains the chunk loads
+  __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();
 
-  const T *kbase = (const T *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh + lh * 8;
+  const T *krow0 = (const T *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh;
   const float c2 = a.scale * 1.4426950408889634f;
   float *obase = a.out + (int64_t)l * a.out_sl + (int64_t)r * a.out_sr + (int64_t)h * a.out_sh;
   const float fn0 = (float)n0, fden = (float)(n0 + nq);
   const int ld_tile = (wave * LPW) / KS, ld_ks = (wave * LPW) % KS;
 
-  // This wave's share of a chunk: LPW B fragments of tile ld_tile, HBM -> LDS
-  // (lane i of a global_load_lds_dwordx4 writes bytes [16i, 16i+16) of the 1 KiB
-  // fragment).  A token past t_end, or in a block the table marks invalid, reads
-  // row 0 of block 0 instead; its score is never written.
+  // A chunk in LDS is CH token rows of 256 bytes (the head's 128 elements), each row's
+  // 16-byte columns stored XOR-swizzled: LDS column c of token t holds the row's column
+  // c ^ (t % 16).  This wave's share: tokens [16 wave, 16 wave + 16) of the chunk, as LPW
+  // loads of four whole rows (lane i writes bytes [16i, 16i + 16) of its 1 KiB: row i/16,
+  // LDS column i%16), so every load reads 256 contiguous bytes per row.  A token past
+  // t_end, or in a block the table marks invalid, reads row 0 of block 0 instead; its
+  // score is never written.
+  static_assert(LPW * 4 * NW == CH, "four rows per load");
   auto load_chunk = [&](int cbase, unsigned char *kb) {
-    const int t = cbase + ld_tile * 32 + lcol;
-    const int bi = min((t >> bs_shift) - b0, nbt - 1);
-    int phys = bts[bi];
-    const bool ok = t < t_end && phys >= 0;
-    phys = ok ? phys : 0;
-    const int slot = ok ? (t & (BS - 1)) : 0;
-    const T *kp = kbase + (int64_t)phys * a.kv_sb + (int64_t)slot * a.kv_ss + ld_ks * 16;
+    const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_address(&kb[wave * LPW * 1024]));
+    if constexpr (!SWZ) {
+      // fragment layout: LPW B fragments of tile ld_tile, [tile][k step][lane] x 16 bytes
+      const int t = cbase + ld_tile * 32 + lcol;
+      const int bi = min((t >> bs_shift) - b0, nbt - 1);
+      int phys = bts[bi];
+      const bool ok = t < t_end && phys >= 0;
+      phys = ok ? phys : 0;
+      const int slot = ok ? (t & (BS - 1)) : 0;
+      const T *kp = krow0 + (int64_t)phys * a.kv_sb + (int64_t)slot * a.kv_ss + lh * 8 + ld_ks * 16;
 #pragma unroll
-    for (int i = 0; i < LPW; ++i)
-      __builtin_amdgcn_global_load_lds((const void *)(kp + i * 16),
-                                       (__attribute__((address_space(3))) void *)&kb[(wave * LPW + i) * 1024],
-                                       16, 0, 0);
+      for (int i = 0; i < LPW; ++i) load_lds16(kp + i * 16, dst + i * 1024);
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int tl = wave * 16 + i * 4 + (lane >> 4);   // token of the chunk (tl % 16 = 4i + lane/16)
+      const int t = cbase + tl;
+      const int bi = min((t >> bs_shift) - b0, nbt - 1);
+      int phys = bts[bi];
+      const bool ok = t < t_end && phys >= 0;
+      phys = ok ? phys : 0;
+      const int slot = ok ? (t & (BS - 1)) : 0;
+      const int col = (lane & 15) ^ (tl & 15);
+      load_lds16(krow0 + (int64_t)phys * a.kv_sb + (int64_t)slot * a.kv_ss + col * 8, dst + i * 1024);
+    }
   };
-  auto read_b = [&](V8 (&b8)[KS], const unsigned char *kb, int tile) {
+  // The running means of the CH tokens at cbase -> oldm[slot] (wave 0: two loads into
+  // LDS of 4 bytes per lane, at clamped in-range tokens; those past t_end are not used).
+  auto load_old = [&](int cbase, int slot) {
+    if (wave == 0) {
+      const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_address(&oldm[slot][0]));
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) b8[ks] = *(const V8 *)(&kb[((tile * KS + ks) * 64 + lane) * 16]);
+      for (int i = 0; i < CH / 64; ++i) load_lds4(obase + min(cbase + i * 64 + lane, t_end - 1), dst + i * 256);
+    }
+  };
+  // B operand of k step ks: lane (lcol, lh) takes token lcol's column 2 ks + lh, at LDS
+  // column (2 ks + lh) ^ (lcol % 16) of its row; any 16 consecutive lanes read 16
+  // distinct columns (no bank conflict)
+  int roff[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) roff[ks] = lcol * 256 + (((2 * ks + lh) ^ (lcol & 15)) << 4);
+  auto read_b = [&](V8 (&b8)[KS], const unsigned char *kb, int tile) {
+    if constexpr (SWZ) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) b8[ks] = *(const V8 *)(&kb[tile * 32 * 256 + roff[ks]]);
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) b8[ks] = *(const V8 *)(&kb[((tile * KS + ks) * 64 + lane) * 16]);
+    }
   };
   auto mfma8 = [&](const V8 (&a8)[KS], const V8 (&b8)[KS], const f32x16 &c) {
     f32x16 acc = c;
@@ -609,40 +687,63 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
 #pragma unroll
     for (int k = 0; k < NT; ++k) red[buf][2 * rg + lh][(tg + k * TG) * 32 + lcol] = part[k];
   };
-  auto reduce_chunk = [&](int cbase, int buf, float old) {
+  auto reduce_chunk = [&](int cbase, int buf, int slot) {
     if (tid < CH) {
       const int t = cbase + tid;
       if (t < t_end && bts[(t >> bs_shift) - b0] >= 0) {
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < NRED; ++i) s += red[buf][i][tid];
-        obase[t] = (old * fn0 + s) / fden;
+        obase[t] = (oldm[slot][tid] * fn0 + s) / fden;
       }
     }
   };
 
+  // NBUF - 1 chunks in flight: step c waits for chunk c, hands it over with one barrier
+  // and issues the loads of chunk c + NBUF - 1 (K into the buffer chunk c - 1 used, the
+  // old means into ring slot (c + NBUF - 1) % 8, which no chunk still to be reduced
+  // holds).  After the set-up every vector memory operation of the loop is a load into
+  // LDS or a store: a wave issues LPW K loads per chunk, and wave 0 two more for the old
+  // means, after them.  So at most (NBUF - 2) * LPW of a wave's operations issued after
+  // chunk c's loads are outstanding when chunk c's are: vmcnt((NBUF - 2) * LPW) means
+  // chunk c's share of this wave is in LDS.
   const int nch = (t_end - t_begin + CH - 1) / CH;
-  const int otid = tid % CH;
-  float old = 0.f;  // running means of the chunk being multiplied (read one chunk ahead)
+  constexpr int VMW = (NBUF - 2) * LPW;
   auto step = [&](int c, const unsigned char *kcur, unsigned char *knext) {
     const int cbase = t_begin + c * CH;
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's share of chunk c is in LDS
-    __syncthreads();                     // ... and every wave's; chunk c-1 is finished
-    if (c >= 1) reduce_chunk(cbase - CH, (c - 1) & 1, old);
-    old = obase[min(cbase + otid, t_end - 1)];
-    load_chunk(cbase + CH, knext);       // past the end: harmless in-bounds rows
+    lds_barrier<VMW>();   // chunk c is in LDS, every wave's share; chunk c-1 is finished
+    if (c >= 1) reduce_chunk(cbase - CH, (c - 1) & 1, (c - 1) & 7);
+    load_chunk(cbase + (NBUF - 1) * CH, knext);   // past the end: harmless in-bounds rows
+    load_old(cbase + (NBUF - 1) * CH, (c + NBUF - 1) & 7);
     __builtin_amdgcn_sched_barrier(0);
     compute_chunk(kcur, c & 1, cbase);
     __builtin_amdgcn_sched_barrier(0);
   };
   load_chunk(t_begin, kbuf_a);
-  for (int c = 0; c < nch; c += 2) {
-    step(c, kbuf_a, kbuf_b);
-    if (c + 1 < nch) step(c + 1, kbuf_b, kbuf_a);
+  load_old(t_begin, 0);
+  if constexpr (NBUF >= 3) { load_chunk(t_begin + CH, kbuf_b); load_old(t_begin + CH, 1); }
+  if constexpr (NBUF >= 4) { load_chunk(t_begin + 2 * CH, kbuf_c); load_old(t_begin + 2 * CH, 2); }
+  if constexpr (NBUF == 2) {
+    for (int c = 0; c < nch; c += 2) {
+      step(c, kbuf_a, kbuf_b);
+      if (c + 1 < nch) step(c + 1, kbuf_b, kbuf_a);
+    }
+  } else if constexpr (NBUF == 3) {
+    for (int c = 0; c < nch; c += 3) {
+      step(c, kbuf_a, kbuf_c);
+      if (c + 1 < nch) step(c + 1, kbuf_b, kbuf_a);
+      if (c + 2 < nch) step(c + 2, kbuf_c, kbuf_b);
+    }
+  } else {
+    for (int c = 0; c < nch; c += 4) {
+      step(c, kbuf_a, kbuf_d);
+      if (c + 1 < nch) step(c + 1, kbuf_b, kbuf_a);
+      if (c + 2 < nch) step(c + 2, kbuf_c, kbuf_b);
+      if (c + 3 < nch) step(c + 3, kbuf_d, kbuf_c);
+    }
   }
-  __builtin_amdgcn_s_waitcnt(0x0F70);    // no load into LDS outlives the workgroup
-  __syncthreads();
-  reduce_chunk(t_begin + (nch - 1) * CH, (nch - 1) & 1, old);
+  lds_barrier<0>();     // no load into LDS outlives the workgroup; the last chunk is finished
+  reduce_chunk(t_begin + (nch - 1) * CH, (nch - 1) & 1, (nch - 1) & 7);
 }
 
 __global__ void bump_n_seen_kernel(int32_t *n_seen, const int32_t *n_valid, int R, int N) {
@@ -707,31 +808,60 @@ static int qreg_tokens_per_wg(int pairs, int span) {
   return best * chunk;
 }
 
+// Which MFMA kernel scores a launch of `rows` query rows.  ACTKV_SCORE_KERNEL=qreg or
+// kslice forces one of the two (both are exact; for timing and tests), read once.
+enum MfmaChoice { MFMA_AUTO = 0, MFMA_QREG = 1, MFMA_KSLICE = 2 };
+static int mfma_choice() {
+  static const int c = [] {
+    const char *e = getenv("ACTKV_SCORE_KERNEL");
+    if (!e) return (int)MFMA_AUTO;
+    if (!strcmp(e, "qreg")) return (int)MFMA_QREG;
+    if (!strcmp(e, "kslice")) return (int)MFMA_KSLICE;
+    return (int)MFMA_AUTO;
+  }();
+  return c;
+}
+
 template <typename T, typename V8, int G>
 static int launch_mfma(const ScoreArgs &a0, int bs_shift, hipStream_t st) {
   const int pairs = a0.L * a0.R * a0.Hkv;
   const int span = a0.max_blocks * a0.BS;
   const int q_per_launch = 512 / G;  // both kernels take at most 512 query rows
   const bool causal = a0.kv_len != nullptr;
+  const int choice = mfma_choice();
   for (int qc0 = 0; qc0 < a0.N; qc0 += q_per_launch) {
     ScoreArgs a = a0;
     a.qc0 = qc0;
     a.qcn = std::min(q_per_launch, a0.N - qc0);
     const int rows = a.qcn * G;
-    if (rows > 384) {
-      // the matrix cores bound the call: query tile in registers, K shared through LDS
+    // measured on 36 layers x 4 x 8k (causal) and 36 x 32k: the query-register kernel
+    // is faster up to 128 rows (whole-row loads: 4.4-4.7 TB/s of K against 3.5-4.4) and
+    // above 384 (the matrix cores bound it); the K-slice kernel from 129 to 384 rows
+    const bool qreg = choice == MFMA_QREG || (choice == MFMA_AUTO && (rows <= 128 || rows > 384));
+    if (qreg) {
+      // query tile in registers, K shared through LDS; RG row groups of 64 rows
       const int tpw = qreg_tokens_per_wg(pairs, span);
       const int cpp = (span + tpw - 1) / tpw;
       const int grid = ((pairs + 7) / 8) * 8 * cpp;
-      if (causal)
-        hipLaunchKernelGGL((score_qreg_kernel<T, V8, G, true>), dim3(grid), dim3(512), 0, st, a, tpw, cpp,
-                           pairs, bs_shift);
-      else
-        hipLaunchKernelGGL((score_qreg_kernel<T, V8, G, false>), dim3(grid), dim3(512), 0, st, a, tpw, cpp,
-                           pairs, bs_shift);
+#define ACTKV_QREG(RGV, NB, SW)                                                                    \
+  do {                                                                                             \
+    if (causal)                                                                                    \
+      hipLaunchKernelGGL((score_qreg_kernel<T, V8, G, true, RGV, NB, SW>), dim3(grid), dim3(512), 0, \
+                         st, a, tpw, cpp, pairs, bs_shift);                                        \
+    else                                                                                           \
+      hipLaunchKernelGGL((score_qreg_kernel<T, V8, G, false, RGV, NB, SW>), dim3(grid), dim3(512),  \
+                         0, st, a, tpw, cpp, pairs, bs_shift);                                     \
+  } while (0)
+      // up to 256 rows the call streams K at the HBM rate: whole-row loads into swizzled
+      // rows and three chunks in flight; above, the matrix cores bound it: fragment
+      // layout (fewer address instructions) and two chunks in flight
+      if (rows <= 128) ACTKV_QREG(2, 3, true);
+      else if (rows <= 256) ACTKV_QREG(4, 3, true);
+      else ACTKV_QREG(8, 2, false);
+#undef ACTKV_QREG
     } else {
-      // fewer rows: 12 waves stream their own K slices against the tile in LDS,
-      // which keeps more K in flight (measured faster up to 384 rows)
+      // 12 waves stream their own K slices against the tile in LDS, which keeps
+      // more K in flight
       constexpr int NW = 12, TT = 1;
       const int tpw = kslice_tokens_per_wg(pairs, span, NW);
       const int cpp = (span + tpw - 1) / tpw;

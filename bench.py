@@ -19,8 +19,16 @@ the scoring call the roofline uses.  The same steps timed with the host's launch
 (a synchronisation before each step) are reported beside it.
 
 The single JSON line also carries the same numbers for one layer (the 32k-token one-layer
-workload), the CPU baseline (the oracle's reference-style torch path timed on a bounded sample
-of the same workload on this host) and checks of the step's results.
+workload), the CPU baseline (the oracle's reference-style torch path on this host: the one
+32k-token layer in full, median of --cpu-runs runs, scaled linearly to 36 layers for the whole
+step), checks of the step's results and, under `configs`, the other workloads of the metric:
+  cfg1 : one fp16 layer of 2048 tokens, 64 action queries, keep 25% + 4 sinks (with its CPU
+         baseline in full)
+  cfg3 : 36 layers x 8 ragged sequences of 8k-64k tokens, 64-256 action queries, keep 5-30%
+         + 4 sinks, one shared shuffled pool; one cal_attn + one evict_batch
+  cfg4 : 131072 tokens x 36 layers, keep mask of clustered runs, compaction only
+each with its step time, algorithmic bytes and flops, GB/s, its floor and checks against the
+oracle.  The agent loop (`ora`) runs all 50 rounds of its schedule.
 """
 from __future__ import annotations
 
@@ -62,7 +70,7 @@ def parse(argv=None):
     ap.add_argument("--keep", type=float, default=0.10)
     ap.add_argument("--sinks", type=int, default=4)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU baseline sample")
+    ap.add_argument("--cpu-runs", type=int, default=3, help="runs of each CPU baseline (median reported)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-single-layer", action="store_true", help="skip the one-layer measurement")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "score_kernel_traffic.json"),
@@ -72,7 +80,9 @@ def parse(argv=None):
                     help="run the agent-loop workload instead (rounds of append + causal action scoring + "
                          "LRFU keep + compaction on a 36-layer batch of 4) and print its own JSON line")
     ap.add_argument("--ora-rounds", type=int, default=50)
-    ap.add_argument("--ora-short", type=int, default=10,
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the 2k fp16, 36-layer ragged batch and 131k compaction legs")
+    ap.add_argument("--ora-short", type=int, default=50,
                     help="rounds of the agent-loop workload reported in the default JSON line (0: none)")
     ap.add_argument("--no-table1", action="store_true", help="skip the reference bench's Table-1 cases")
     ap.add_argument("--no-power", action="store_true", help="skip the power and clock reading")
@@ -117,25 +127,31 @@ def run_info(torch, dev):
 
 
 class Workload:
-    """Seeded synthetic cache + action queries with exact lse, and a restorable snapshot."""
+    """Seeded synthetic cache + action queries with exact lse, and a restorable snapshot.
+    One sequence of `seq` tokens (default --seq) in `layers` layers; `queries` action queries
+    (default --queries), keep ratio `keep` (default --keep) + --sinks, cache dtype `dtype`
+    (default bf16); the physical blocks are drawn from a shuffled pool."""
 
-    def __init__(self, args, layers, device):
+    def __init__(self, args, layers, device, *, seq=None, queries=None, keep=None, dtype=None):
         import torch
         from actkv.paged import PagedKVCache
 
         self.args, self.L, self.dev = args, layers, device
-        S, bs, hkv, hq, d = args.seq, args.block_size, args.kv_heads, args.q_heads, args.head_dim
-        self.S, self.bs, self.hkv, self.hq, self.d, self.N = S, bs, hkv, hq, d, args.queries
+        S = args.seq if seq is None else seq
+        bs, hkv, hq, d = args.block_size, args.kv_heads, args.q_heads, args.head_dim
+        self.dtype = torch.bfloat16 if dtype is None else dtype
+        self.S, self.bs, self.hkv, self.hq, self.d = S, bs, hkv, hq, d
+        self.N = args.queries if queries is None else queries
         self.nb = math.ceil(S / bs) + 64
         gcpu = torch.Generator().manual_seed(args.seed)
-        self.cache = PagedKVCache(self.nb, bs, hkv, d, n_layers=layers, dtype=torch.bfloat16, device=device)
+        self.cache = PagedKVCache(self.nb, bs, hkv, d, n_layers=layers, dtype=self.dtype, device=device)
         self.cache.free = torch.randperm(self.nb, generator=gcpu).tolist()
         gdev = torch.Generator(device=device).manual_seed(args.seed + 1)
-        k = torch.randn(layers, S, hkv, d, generator=gdev, device=device, dtype=torch.bfloat16)
-        v = torch.randn(layers, S, hkv, d, generator=gdev, device=device, dtype=torch.bfloat16)
+        k = torch.randn(layers, S, hkv, d, generator=gdev, device=device, dtype=self.dtype)
+        v = torch.randn(layers, S, hkv, d, generator=gdev, device=device, dtype=self.dtype)
         self.cache.append(0, k, v)
         del k, v
-        self.q = torch.randn(layers, 1, self.N, hq, d, generator=gdev, device=device, dtype=torch.bfloat16)
+        self.q = torch.randn(layers, 1, self.N, hq, d, generator=gdev, device=device, dtype=self.dtype)
         self.lse = self._exact_lse()
         self.kv0 = self.cache.kv.clone()
         self.host0 = (list(self.cache.free), {0: list(self.cache.tables[0])}, dict(self.cache.seq_used))
@@ -143,7 +159,7 @@ class Workload:
         self.width = math.ceil(S / bs) * bs
         self.out = torch.zeros(layers, 1, hkv, self.width, device=device)
         self.n_seen = torch.zeros(1, dtype=torch.int32, device=device)
-        self.budget = int(args.keep * S)
+        self.budget = int((args.keep if keep is None else keep) * S)
 
     def _exact_lse(self):
         """lse[l, 0, n, h] = logsumexp_t scale * q . k_t over the whole prefix, float32 on the GPU."""
@@ -187,7 +203,8 @@ class Workload:
 
     # ---------------------------------------------------------------- algorithmic work
     def algorithmic(self, moved_pairs, drop):
-        L, S, hkv, hq, d, N, bs, e = self.L, self.S, self.hkv, self.hq, self.d, self.N, self.bs, 2
+        L, S, hkv, hq, d, N, bs = self.L, self.S, self.hkv, self.hq, self.d, self.N, self.bs
+        e = self.cache.kv.element_size()
         nblk = math.ceil(S / bs)
         per_layer_score = S * hkv * d * e + N * hq * d * e + N * hq * 4 + 2 * hkv * S * 4 + nblk * 4
         score = L * per_layer_score
@@ -339,7 +356,7 @@ def outputs_match(w, slots_before, keep):
     from actkv.kernels.compaction import gather_compaction
     from actkv.kernels.lse_attn import paged_decode_attention, paged_decode_attention_ref
     g = torch.Generator(device=w.dev).manual_seed(w.args.seed + 7)
-    q2 = torch.randn(1, w.hq, w.d, generator=g, device=w.dev, dtype=torch.bfloat16)
+    q2 = torch.randn(1, w.hq, w.d, generator=g, device=w.dev, dtype=w.dtype)
     seq, bt = w.cache._device_tables([0])
     got, _ = paged_decode_attention(q2, w.cache.kv[0], bt, seq)
     keep_slots = slots_before[torch.from_numpy(keep.numpy()).to(w.dev)]
@@ -487,39 +504,382 @@ def run_table1(torch, dev, seed=0, warmup=1, iters=5):
             "cases": rows}
 
 
-def cpu_baseline(w, layers):
-    """The oracle's reference-style torch CPU path on a bounded sample of the step: all N
-    action-query folds (one query per fold, as the reference) of the first `layers` layers, then
-    the keep mask over those layers and the compaction of their K/V planes; extrapolated
-    linearly in the layer count to the whole step."""
+class RaggedWorkload:
+    """A batch of ragged sequences in one shared, shuffled block pool: R requests of S_r ~
+    U[8192, 65536] tokens in L layers, N_r ~ U[64, 256] action queries each (bf16, exact
+    lse), keep ratio r_r ~ U[0.05, 0.30] + --sinks, all drawn from the seed.  One step scores
+    every layer and request in one cal_attn (n_valid = N_r) and evicts every request in one
+    evict_batch call."""
+
+    def __init__(self, args, device, R=8, L=36):
+        import torch
+        from actkv.paged import PagedKVCache
+
+        seed = args.seed + 3
+        rng = np.random.default_rng(seed)
+        bs, hkv, hq, d = args.block_size, args.kv_heads, args.q_heads, args.head_dim
+        self.args, self.R, self.L, self.dev = args, R, L, device
+        self.bs, self.hkv, self.hq, self.d, self.sinks = bs, hkv, hq, d, args.sinks
+        self.S = [int(x) for x in rng.integers(8192, 65537, R)]
+        self.Nq = [int(x) for x in rng.integers(64, 257, R)]
+        self.ratio = [float(x) for x in rng.uniform(0.05, 0.30, R)]
+        self.budgets = [int(r * s) for r, s in zip(self.ratio, self.S)]
+        self.nb = sum(math.ceil(s / bs) for s in self.S) + 64
+        self.cache = PagedKVCache(self.nb, bs, hkv, d, n_layers=L, dtype=torch.bfloat16, device=device)
+        self.cache.free = torch.randperm(self.nb, generator=torch.Generator().manual_seed(seed)).tolist()
+        gdev = torch.Generator(device=device).manual_seed(seed + 1)
+        self.reqs = list(range(R))
+        for r, n in enumerate(self.S):
+            k = torch.randn(L, n, hkv, d, generator=gdev, device=device, dtype=torch.bfloat16)
+            v = torch.randn(L, n, hkv, d, generator=gdev, device=device, dtype=torch.bfloat16)
+            self.cache.append(r, k, v)
+            del k, v
+        nmax = max(self.Nq)
+        self.q = torch.randn(L, R, nmax, hq, d, generator=gdev, device=device, dtype=torch.bfloat16)
+        self.n_valid = torch.tensor(self.Nq, dtype=torch.int32, device=device)
+        self.lse = self._exact_lse(nmax)
+        self.kv0 = self.cache.kv.clone()
+        self.host0 = (list(self.cache.free), {r: list(self.cache.tables[r]) for r in self.reqs},
+                      dict(self.cache.seq_used))
+        self.tables0_i32 = {r: np.array(self.host0[1][r], dtype=np.int32) for r in self.reqs}
+        self.width = max(math.ceil(n / bs) for n in self.S) * bs
+        self.out = torch.zeros(L, R, hkv, self.width, device=device)
+        self.n_seen = torch.zeros(R, dtype=torch.int32, device=device)
+
+    def _exact_lse(self, nmax):
+        """lse[l, r, n, h] = logsumexp_t scale * q . k_t over request r's tokens (n < N_r),
+        float32 on the GPU; rows n >= N_r are never read."""
+        import torch
+        g, scale = self.hq // self.hkv, self.d ** -0.5
+        lse = torch.zeros(self.L, self.R, nmax, self.hq, device=self.dev)
+        for r in self.reqs:
+            slots, n = self.cache.slot_map(r), self.Nq[r]
+            for l in range(self.L):
+                kflat = self.cache.kv[l, 0].reshape(-1, self.hkv, self.d)[slots]
+                for h in range(self.hkv):
+                    kt = kflat[:, h].float().t().contiguous()
+                    qh = self.q[l, r, :n, h * g:(h + 1) * g].float().reshape(-1, self.d)
+                    lse[l, r, :n, h * g:(h + 1) * g] = torch.logsumexp((qh @ kt) * scale, -1).view(n, g)
+        return lse
+
+    def restore(self):
+        from actkv.paged import _Table
+        self.cache.kv.copy_(self.kv0)
+        free, tables, seq = self.host0
+        self.cache.free = list(free)
+        self.cache.tables = {r: _Table(tables[r], self.tables0_i32[r].copy()) for r in self.reqs}
+        self.cache.seq_used = dict(seq)
+        self.cache.pinned.clear()
+        self.n_seen.zero_()
+
+    def step(self, ev=None):
+        if ev:
+            ev[0].record()
+        self.cache.cal_attn(self.reqs, self.q, self.lse, self.out, self.n_seen, layer=None, n_valid=self.n_valid)
+        if ev and ev[1] is not None:
+            ev[1].record()
+        perms = self.cache.evict_batch(self.reqs, self.out, self.budgets, protected=self.sinks)
+        if ev:
+            ev[2].record()
+        return perms
+
+    def algorithmic(self, moved, drops):
+        L, hkv, hq, d, bs, e = self.L, self.hkv, self.hq, self.d, self.bs, 2
+        score = keep = compact = flops = 0
+        for S, N, m, dr in zip(self.S, self.Nq, moved, drops):
+            nblk = math.ceil(S / bs)
+            score += L * (S * hkv * d * e + N * hq * d * e + N * hq * 4 + 2 * hkv * S * 4 + nblk * 4)
+            keep += L * hkv * S * 4 + S
+            compact += m * 2 * L * hkv * d * e * 2 + S + 2 * nblk * 4 + dr * 4
+            flops += 2 * N * hq * S * d * L
+        return {"bytes_score": score, "bytes_keep": keep, "bytes_compact": compact, "flops_score": flops}
+
+
+def check_ragged(w):
+    """One step of the ragged batch against the oracle, request by request in order: keep mask
+    (the oracle's on the GPU's own scores), perm (its compaction plan), the allocator (tables,
+    the free list's order, lengths: paged.py:135-138 applied sequentially) and the survivors'
+    K/V rows of the first and last layer at perm."""
     import torch
     from oracle import reference as ref
 
-    ls = max(1, min(layers, w.L))
+    w.restore()
+    slots_before = {r: w.cache.slot_map(r) for r in w.reqs}
+    perms = w.step()
+    torch.cuda.synchronize()
+    scores = w.out.cpu()
+    free, tables, seq = list(w.host0[0]), {r: list(t) for r, t in w.host0[1].items()}, {}
+    ok_mask = ok_perm = ok_rows = True
+    moved, drops = [], []
+    for i, r in enumerate(w.reqs):
+        S = w.S[i]
+        keep_o = ref.keep_mask_from_scores(scores[:, i, :, :S], S, w.budgets[i], protected=w.sinks)
+        src, _, perm_o, drop = ref.plan_compaction(keep_o.numpy(), S, tables[r], w.bs)
+        moved.append(int(src.size))
+        drops.append(int(drop))
+        p = perms[i].cpu()
+        ok_mask = ok_mask and bool(torch.equal(torch.sort(p).values, torch.nonzero(keep_o).flatten()))
+        ok_perm = ok_perm and bool(np.array_equal(p.numpy(), perm_o))
+        free.extend(reversed(tables[r][:drop]))
+        tables[r] = tables[r][drop:]
+        seq[r] = int(keep_o.sum())
+        pd = perms[i]
+        after_slots = w.cache.slot_map(r)
+        for l in (0, w.L - 1):
+            before = w.kv0[l].view(2, -1, w.hkv, w.d)[:, slots_before[r][pd]]
+            after = w.cache.kv[l].view(2, -1, w.hkv, w.d)[:, after_slots]
+            ok_rows = ok_rows and bool(torch.equal(before.view(torch.int16), after.view(torch.int16)))
+    ok_host = (w.cache.free == free and {r: list(w.cache.tables[r]) for r in w.reqs} == tables
+               and w.cache.seq_used == seq)
+    return {"keep_masks_match_oracle": ok_mask, "perms_match_oracle": ok_perm,
+            "first_last_layer_rows_match": ok_rows, "allocator_state_matches_oracle": ok_host}, moved, drops
+
+
+class ClusteredWorkload:
+    """One sequence of S tokens in L layers (bf16, shuffled pool) and a keep mask drawn as
+    alternating runs: kept runs Geom(mean 32), dropped runs Geom(mean 128), overall keep about
+    0.2.  One step is PagedKVCache.compact with that mask (paged.py:125-139): plan, row moves of
+    every layer's K and V, block reclaim."""
+
+    def __init__(self, args, device, S=131072, L=36):
+        import torch
+        from actkv.paged import PagedKVCache
+
+        seed = args.seed + 5
+        bs, hkv, d = args.block_size, args.kv_heads, args.head_dim
+        self.args, self.S, self.L, self.dev, self.bs, self.hkv, self.d = args, S, L, device, bs, hkv, d
+        self.nb = math.ceil(S / bs) + 64
+        self.cache = PagedKVCache(self.nb, bs, hkv, d, n_layers=L, dtype=torch.bfloat16, device=device)
+        self.cache.free = torch.randperm(self.nb, generator=torch.Generator().manual_seed(seed)).tolist()
+        gdev = torch.Generator(device=device).manual_seed(seed + 1)
+        k = torch.randn(L, S, hkv, d, generator=gdev, device=device, dtype=torch.bfloat16)
+        v = torch.randn(L, S, hkv, d, generator=gdev, device=device, dtype=torch.bfloat16)
+        self.cache.append(0, k, v)
+        del k, v
+        rng = np.random.default_rng(seed)
+        mask = np.zeros(S, dtype=bool)
+        t, kept_run = 0, True
+        while t < S:
+            n = int(rng.geometric(1 / 32 if kept_run else 1 / 128))
+            if kept_run:
+                mask[t:t + n] = True
+            t += n
+            kept_run = not kept_run
+        self.keep_host = torch.from_numpy(mask)
+        self.keep = self.keep_host.to(device)
+        self.kv0 = self.cache.kv.clone()
+        self.host0 = (list(self.cache.free), {0: list(self.cache.tables[0])}, dict(self.cache.seq_used))
+        self.table0_i32 = np.array(self.host0[1][0], dtype=np.int32)
+
+    def restore(self):
+        from actkv.paged import _Table
+        self.cache.kv.copy_(self.kv0)
+        free, tables, seq = self.host0
+        self.cache.free = list(free)
+        self.cache.tables = {0: _Table(tables[0], self.table0_i32.copy())}
+        self.cache.seq_used = dict(seq)
+        self.cache.pinned.clear()
+
+    def step(self, ev=None):
+        if ev:
+            ev[0].record()
+        perm = self.cache.compact(0, self.keep)
+        if ev:
+            ev[2].record()
+        return perm
+
+    def algorithmic(self, moved, drop):
+        nblk = math.ceil(self.S / self.bs)
+        return {"bytes_compact": moved * 2 * self.L * self.hkv * self.d * 2 * 2 + self.S + 2 * nblk * 4 + drop * 4}
+
+
+def check_clustered(w):
+    """The compaction against the oracle: perm (its plan), the allocator, and the first and last
+    layers' survivors at perm."""
+    import torch
+    from oracle import reference as ref
+
+    w.restore()
+    slots_before = w.cache.slot_map(0)
+    perm = w.step()
+    torch.cuda.synchronize()
+    src, _, perm_o, drop = ref.plan_compaction(w.keep_host.numpy(), w.S, w.host0[1][0], w.bs)
+    ok_perm = bool(np.array_equal(perm.cpu().numpy(), perm_o))
+    table = w.host0[1][0]
+    free = list(w.host0[0]) + list(reversed(table[:drop]))
+    ok_host = (w.cache.free == free and list(w.cache.tables[0]) == table[drop:]
+               and w.cache.seq_used[0] == int(w.keep_host.sum()))
+    after_slots = w.cache.slot_map(0)
+    ok_rows = True
+    for l in (0, w.L - 1):
+        before = w.kv0[l].view(2, -1, w.hkv, w.d)[:, slots_before[perm]]
+        after = w.cache.kv[l].view(2, -1, w.hkv, w.d)[:, after_slots]
+        ok_rows = ok_rows and bool(torch.equal(before.view(torch.int16), after.view(torch.int16)))
+    return {"perm_matches_oracle": ok_perm, "allocator_state_matches_oracle": ok_host,
+            "first_last_layer_rows_match": ok_rows}, int(src.size), int(drop)
+
+
+def time_steps(w, steps, warmup):
+    """Events at each step's start and end, every step from a restored copy (as measure())."""
+    import torch
+    for _ in range(warmup):
+        w.restore()
+        w.step()
+    torch.cuda.synchronize()
+    evs = []
+    for _ in range(steps):
+        w.restore()
+        ev = [torch.cuda.Event(enable_timing=True), None, torch.cuda.Event(enable_timing=True)]
+        w.step(ev)
+        evs.append(ev)
+    torch.cuda.synchronize()
+    t = [e[0].elapsed_time(e[2]) * 1e3 for e in evs]
+    return {"step_us": statistics.mean(t), "step_us_median": statistics.median(t)}
+
+
+def roof(bytes_hbm, flops=0):
+    """Floor of a phase: its HBM bytes at 8 TB/s or its dense bf16 flops at 2.5 PFLOP/s."""
+    return max(bytes_hbm / (HBM_PEAK_GBS * 1e9), flops / (BF16_PEAK_TFLOPS * 1e12)) * 1e6
+
+
+def run_cfg1(args, dev, cpu=True):
+    """The reference's CPU-runnable case on the GPU: one fp16 layer, one 2048-token sequence,
+    64 action queries with exact lse, keep 25% (budget 512) + 4 sinks, shuffled blocks; scoring
+    then evict.  Checks as the headline step's; the CPU baseline times the same case in full."""
+    import torch
+    w = Workload(args, 1, dev, seq=2048, queries=64, keep=0.25, dtype=torch.float16)
+    checks, moved, drop = check_step(w)
+    work = w.algorithmic(moved, drop)
+    m = measure(w, max(args.steps, 10), max(args.warmup, 2))
+    nbytes = work["bytes_score"] + work["bytes_keep"] + work["bytes_compact"]
+    floor = roof(work["bytes_score"], work["flops_score"]) + roof(work["bytes_keep"] + work["bytes_compact"])
+    res = {"workload": "1 layer x 1 sequence x 2048 tokens, Hq 32 / Hkv 8, head_dim 128, block 16, fp16, "
+                       "64 action queries, keep 25% (budget 512) + 4 sinks, shuffled blocks",
+           "step_us": round(m["step_us"], 2), "step_us_median": round(m["step_us_median"], 2),
+           "score_us": round(m["score_us"], 2), "evict_us": round(m["evict_us"], 2),
+           "algorithmic": work, "GBps": round(nbytes / (m["step_us"] * 1e-6) / 1e9, 1),
+           "pct_of_hbm_peak": round(100 * nbytes / (m["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 3),
+           "bound": "hbm", "floor_us": round(floor, 2), "frac_of_floor": round(floor / m["step_us"], 4),
+           "checks": checks}
+    if cpu:
+        res["cpu_baseline"] = cpu_summary(cpu_runs(w, 3), nbytes, "the whole case (config 1)")
+    del w
+    return res
+
+
+def run_cfg3(args, dev, steps=5):
+    """36 layers x 8 ragged sequences scored and evicted in one cal_attn + one evict_batch."""
+    w = RaggedWorkload(args, dev)
+    checks, moved, drops = check_ragged(w)
+    work = w.algorithmic(moved, drops)
+    m = measure(w, steps, 1)
+    nbytes = work["bytes_score"] + work["bytes_keep"] + work["bytes_compact"]
+    floor_score = roof(work["bytes_score"], work["flops_score"])
+    floor = floor_score + roof(work["bytes_keep"] + work["bytes_compact"])
+    res = {"workload": f"{w.L} layers x {w.R} ragged sequences of {min(w.S)}-{max(w.S)} tokens "
+                       f"(sum {sum(w.S)}), Hq 32 / Hkv 8, head_dim 128, block 16, bf16, "
+                       f"{min(w.Nq)}-{max(w.Nq)} action queries, keep {min(w.ratio):.1%}-{max(w.ratio):.1%} "
+                       f"+ {w.sinks} sinks, one shared shuffled block pool; one cal_attn + one evict_batch",
+           "seq_lens": w.S, "action_queries": w.Nq, "budgets": w.budgets,
+           "step_us": round(m["step_us"], 1), "step_us_median": round(m["step_us_median"], 1),
+           "score_us": round(m["score_us"], 1), "evict_us": round(m["evict_us"], 1),
+           "evict_us_per_layer": round(m["step_us"] / w.L, 2),
+           "algorithmic": work, "GBps": round(nbytes / (m["step_us"] * 1e-6) / 1e9, 1),
+           "pct_of_hbm_peak": round(100 * nbytes / (m["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
+           "score_TFLOPs": round(work["flops_score"] / (m["score_us"] * 1e-6) / 1e12, 1),
+           "bound": ("mfma" if work["flops_score"] / (BF16_PEAK_TFLOPS * 1e12)
+                     > work["bytes_score"] / (HBM_PEAK_GBS * 1e9) else "hbm"),
+           "floor_us": round(floor, 1), "frac_of_floor": round(floor / m["step_us"], 4),
+           "moved_rows": sum(moved), "blocks_freed": sum(drops), "checks": checks}
+    del w
+    return res
+
+
+def run_cfg4(args, dev, steps=5):
+    """131072 tokens x 36 layers, clustered keep runs, compaction only."""
+    w = ClusteredWorkload(args, dev)
+    checks, moved, drop = check_clustered(w)
+    work = w.algorithmic(moved, drop)
+    m = time_steps(w, steps, 1)
+    floor = roof(work["bytes_compact"])
+    res = {"workload": f"1 sequence x {w.S} tokens x {w.L} layers, Hkv 8, head_dim 128, block 16, bf16, "
+                       f"keep mask of alternating runs (kept Geom(mean 32), dropped Geom(mean 128)): "
+                       f"{int(w.keep_host.sum())} kept; PagedKVCache.compact",
+           "step_us": round(m["step_us"], 1), "step_us_median": round(m["step_us_median"], 1),
+           "evict_us_per_layer": round(m["step_us"] / w.L, 2), "algorithmic": work,
+           "GBps": round(work["bytes_compact"] / (m["step_us"] * 1e-6) / 1e9, 1),
+           "pct_of_hbm_peak": round(100 * work["bytes_compact"] / (m["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
+           "bound": "hbm", "floor_us": round(floor, 1), "frac_of_floor": round(floor / m["step_us"], 4),
+           "moved_rows": moved, "blocks_freed": drop, "checks": checks}
+    del w
+    return res
+
+
+def cpu_runs(w, runs=3):
+    """The oracle's reference-style torch CPU path over one whole layer of `w` (layer 0), `runs`
+    times from the same inputs: all N action-query folds, one query per fold as the reference
+    (lse_attn.py:63-78), then the keep mask, the compaction plan, the row moves of the layer's
+    K/V planes and the allocator update (paged.py:141-157).  Seconds per run: (folds, evict)."""
+    import torch
+    from oracle import reference as ref
+
+    torch.set_num_threads(os.cpu_count() or 1)
     table = [w.host0[1][0]]
-    out = torch.zeros(ls, w.hkv, w.width)
-    t_fold = 0.0
-    kv_cpu = []
-    for l in range(ls):
-        kv_l = w.kv0[l].cpu()
-        kv_cpu.append(kv_l)
-        q = w.q[l, 0].cpu()            # [N, Hq, D]
-        lse = w.lse[l, 0].cpu()        # [N, Hq]
+    kv_l = w.kv0[0].cpu()
+    q = w.q[0, 0].cpu()            # [N, Hq, D]
+    lse = w.lse[0, 0].cpu()        # [N, Hq]
+    times = []
+    for _ in range(runs):
+        out = torch.zeros(1, w.hkv, w.width)
         ns = torch.zeros(1, dtype=torch.int32)
-        o = out[l:l + 1]
+        model = ref.PagedCacheModel(w.nb, w.bs, w.hkv, w.d, 1)
+        model.kv = kv_l.unsqueeze(0).view(torch.int16).numpy().copy()
+        model.free, model.tables, model.seq_used = list(w.host0[0]), {0: list(table[0])}, {0: w.S}
         t0 = time.perf_counter()
         for n in range(w.N):
-            ref.action_scores_fold(q[n:n + 1], kv_l, table, [w.S], lse[n:n + 1], o, ns)
-        t_fold += time.perf_counter() - t0
-    model = ref.PagedCacheModel(w.nb, w.bs, w.hkv, w.d, ls)
-    model.kv = torch.stack(kv_cpu).view(torch.int16).numpy().copy()
-    model.free, model.tables, model.seq_used = list(w.host0[0]), {0: list(table[0])}, {0: w.S}
-    t1 = time.perf_counter()
-    model.evict(0, out, w.budget, protected=w.args.sinks)
-    t_evict = time.perf_counter() - t1
-    sample = t_fold + t_evict
-    return {"layers": ls, "t_fold_s": t_fold, "t_evict_s": t_evict, "sample_s": sample,
-            "extrapolated_step_s": sample * w.L / ls, "threads": torch.get_num_threads()}
+            ref.action_scores_fold(q[n:n + 1], kv_l, table, [w.S], lse[n:n + 1], out, ns)
+        t1 = time.perf_counter()
+        model.evict(0, out, w.budget, protected=w.args.sinks)
+        t2 = time.perf_counter()
+        times.append((t1 - t0, t2 - t1))
+    return times
+
+
+def cpu_summary(times, nbytes, what, layers=1):
+    """CPU baseline entry from per-run (folds, evict) seconds of one layer: the median run,
+    scaled linearly to `layers` layers when that is more than one (labelled)."""
+    import torch
+    run_s = sorted(f + e for f, e in times)
+    med = statistics.median(run_s)
+    step_s = med * layers
+    sample = (f"{what}: all folds (one action query per reference fold) + keep mask + compaction of one "
+              f"layer, {len(times)} runs, median {med:.2f} s (runs {', '.join(f'{x:.2f}' for x in run_s)} s)")
+    if layers > 1:
+        sample += f"; extrapolated linearly to {layers} layers ({step_s:.0f} s)"
+    info = cpu_info()
+    return {"value": round(nbytes / step_s / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": sample, "runs": len(times), "median_s_per_layer": round(med, 3),
+            "extrapolated": layers > 1, "step_s": round(step_s, 2), **info}
+
+
+def cpu_info():
+    """The host CPU: /proc/cpuinfo's model name and lscpu's full description."""
+    import shutil
+    import subprocess
+    info = {"cpu_model": cpu_model(), "os_cpu_count": os.cpu_count()}
+    if shutil.which("lscpu"):
+        try:
+            out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        except (OSError, subprocess.SubprocessError):
+            out = ""
+        keys = {"Model name": "lscpu_model_name", "BIOS Model name": "lscpu_bios_model_name",
+                "Socket(s)": "lscpu_sockets", "Core(s) per socket": "lscpu_cores_per_socket",
+                "Thread(s) per core": "lscpu_threads_per_core", "CPU(s)": "lscpu_cpus"}
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            if k.strip() in keys:
+                info[keys[k.strip()]] = v.strip()
+    return info
 
 
 def cpu_model():
@@ -965,34 +1325,47 @@ def main(argv=None):
     if not args.no_power:
         log("power and clock while scoring")
         power = power_leg(w)
+    ceiling = None
+    if power:
+        # the step's floor at the clock the scoring call actually runs at (the board's power
+        # limit): scoring at the dense bf16 peak scaled to that clock (or its bytes at 8 TB/s,
+        # whichever is longer), keep mask and compaction at 8 TB/s
+        clk = power["gfx_clock_mhz"]
+        f_score = max(work["flops_score"] / (BF16_PEAK_TFLOPS * 1e12 * clk / 2400.0),
+                      work["bytes_score"] / (HBM_PEAK_GBS * 1e9))
+        floor_us = (f_score + (work["bytes_keep"] + work["bytes_compact"]) / (HBM_PEAK_GBS * 1e9)) * 1e6
+        ceil_gbs = total_bytes / (floor_us * 1e-6) / 1e9
+        ceiling = {"gfx_clock_mhz": clk, "step_floor_us": round(floor_us, 1), "GBps": round(ceil_gbs, 1),
+                   "pct_of_hbm_peak": round(100 * ceil_gbs / HBM_PEAK_GBS, 2),
+                   "value_frac_of_ceiling": round(gbs / ceil_gbs, 4),
+                   "basis": "scoring flops at the dense bf16 peak scaled to the measured GFX clock, keep "
+                            "mask and compaction bytes at 8 TB/s"}
     single = None
-    if not args.no_single_layer and args.layers != 1:
+    cpu = None
+    if args.layers != 1 and not (args.no_single_layer and args.no_cpu):
         log("one-layer workload")
         w1 = Workload(args, 1, dev)
-        c1, mv1, dr1 = check_step(w1)
-        wk1 = w1.algorithmic(mv1, dr1)
-        m1 = measure(w1, args.steps, args.warmup)
-        b1 = wk1["bytes_score"] + wk1["bytes_keep"] + wk1["bytes_compact"]
-        single = {"step_us": round(m1["step_us"], 2), "score_us": round(m1["score_us"], 2),
-                  "evict_us": round(m1["evict_us"], 2),
-                  "score_compact_GBps": round(b1 / (m1["step_us"] * 1e-6) / 1e9, 1),
-                  "pct_of_hbm_peak": round(100 * b1 / (m1["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
-                  "score_TFLOPs": round(wk1["flops_score"] / (m1["score_us"] * 1e-6) / 1e12, 1),
-                  "checks": c1}
+        if not args.no_single_layer:
+            c1, mv1, dr1 = check_step(w1)
+            wk1 = w1.algorithmic(mv1, dr1)
+            m1 = measure(w1, args.steps, args.warmup)
+            b1 = wk1["bytes_score"] + wk1["bytes_keep"] + wk1["bytes_compact"]
+            single = {"step_us": round(m1["step_us"], 2), "score_us": round(m1["score_us"], 2),
+                      "evict_us": round(m1["evict_us"], 2),
+                      "score_compact_GBps": round(b1 / (m1["step_us"] * 1e-6) / 1e9, 1),
+                      "pct_of_hbm_peak": round(100 * b1 / (m1["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
+                      "score_TFLOPs": round(wk1["flops_score"] / (m1["score_us"] * 1e-6) / 1e12, 1),
+                      "checks": c1}
+        if not args.no_cpu:
+            # the one-layer case in full, on this host's cores: the baseline of the one-layer
+            # workload as it is, and of the whole step extrapolated linearly in layers
+            log(f"CPU baseline: the {args.seq}-token layer in full, {args.cpu_runs} runs")
+            times = cpu_runs(w1, args.cpu_runs)
+            what = f"one {args.seq}-token layer with {args.queries} action queries in full"
+            cpu = cpu_summary(times, total_bytes, what, layers=args.layers)
+            if single is not None:
+                single["cpu_baseline"] = cpu_summary(times, b1, what)
         del w1
-
-    cpu = None
-    if not args.no_cpu:
-        log(f"CPU baseline sample ({args.cpu_layers} layers)")
-        c = cpu_baseline(w, args.cpu_layers)
-        cpu = {"value": round(total_bytes / c["extrapolated_step_s"] / 1e9, 4), "unit": "GB/s",
-               "cores": c["threads"], "kind": "port",
-               "sample": (f"{c['layers']} of {args.layers} layers: all {args.queries} one-query folds "
-                          f"(reference torch fold per action token, {c['t_fold_s']:.1f} s) + keep mask + "
-                          f"compaction of those layers ({c['t_evict_s']:.2f} s); extrapolated linearly in "
-                          f"layers to the whole step ({c['extrapolated_step_s']:.0f} s)"),
-               "step_s_extrapolated": round(c["extrapolated_step_s"], 1), "cpu_model": cpu_model(),
-               "os_cpu_count": os.cpu_count()}
 
     log("apply_copies on a plan of the compaction's size")
     copies = time_apply_copies(torch, w, moved, max(args.steps, 5))  # rewrites rows: after every other leg
@@ -1002,6 +1375,18 @@ def main(argv=None):
     if not args.no_table1:
         log("the reference bench's Table-1 cases")
         table1 = run_table1(torch, dev, seed=args.seed)
+    configs = None
+    if not args.no_configs:
+        configs = {}
+        log("config 1: one fp16 layer of 2048 tokens, 64 action queries")
+        configs["cfg1"] = run_cfg1(args, dev, cpu=not args.no_cpu)
+        torch.cuda.empty_cache()
+        log("config 3: 36 layers x 8 ragged sequences, one evict_batch")
+        configs["cfg3"] = run_cfg3(args, dev)
+        torch.cuda.empty_cache()
+        log("config 4: 131072 tokens x 36 layers, clustered keep, compaction")
+        configs["cfg4"] = run_cfg4(args, dev)
+        torch.cuda.empty_cache()
     ora = None
     if args.ora_short > 0 and args.layers == 36:
         log(f"agent loop, first {args.ora_short} rounds")
@@ -1028,13 +1413,15 @@ def main(argv=None):
                       "step_median": round(m["step_us_median"], 2),
                       "step_with_host_launch_exposed": round(m["step_us_sync"], 2)},
         "algorithmic": work,
-        "roofline": {"kernel": "score_mfma_kernel (actkv_action_scores)", "bound": "mfma",
+        "roofline": {"kernel": "score_qreg_kernel (actkv_action_scores)", "bound": "mfma",
                      "achieved": round(score_tflops, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(score_tflops / BF16_PEAK_TFLOPS, 4), "traffic": traffic_bytes,
                      "launch_us": round(k_us, 2),
-                     "hbm_GBps_algorithmic": round(work["bytes_score"] / (k_us * 1e-6) / 1e9, 1)},
+                     "hbm_GBps_algorithmic": round(work["bytes_score"] / (k_us * 1e-6) / 1e9, 1),
+                     "ceiling_at_clock": ceiling},
         "cpu_baseline": cpu,
         "single_layer": single,
+        "configs": configs,
         "apply_copies": copies,
         "extra_mb_per_step": extra_mb,
         "power": power,

@@ -326,7 +326,9 @@ def check_step(w):
     perm = w.step()
     torch.cuda.synchronize()
     scores = w.out[:, 0].cpu()
-    keep_o = ref.keep_mask_from_scores(scores, w.S, w.budget, protected=w.args.sinks)
+    # the oracle's keep mask with the documented tie rule (lower index first), which equals
+    # torch.topk's wherever the k-th and (k+1)-th candidate scores differ
+    keep_o = ref.keep_mask_lowest_index_ties(scores, w.S, w.budget, protected=w.args.sinks)
     kept_o = torch.nonzero(keep_o).flatten()
     ok_mask = bool(torch.equal(torch.sort(perm.cpu()).values, kept_o))
     src, dst, perm_o, drop = ref.plan_compaction(keep_o.numpy(), w.S, w.host0[1][0], w.bs)
@@ -597,7 +599,8 @@ class RaggedWorkload:
 
 def check_ragged(w):
     """One step of the ragged batch against the oracle, request by request in order: keep mask
-    (the oracle's on the GPU's own scores), perm (its compaction plan), the allocator (tables,
+    (the oracle's on the GPU's own scores, equal scores at the boundary taken lower index
+    first), perm (its compaction plan), the allocator (tables,
     the free list's order, lengths: paged.py:135-138 applied sequentially) and the survivors'
     K/V rows of the first and last layer at perm."""
     import torch
@@ -613,7 +616,7 @@ def check_ragged(w):
     moved, drops = [], []
     for i, r in enumerate(w.reqs):
         S = w.S[i]
-        keep_o = ref.keep_mask_from_scores(scores[:, i, :, :S], S, w.budgets[i], protected=w.sinks)
+        keep_o = ref.keep_mask_lowest_index_ties(scores[:, i, :, :S], S, w.budgets[i], protected=w.sinks)
         src, _, perm_o, drop = ref.plan_compaction(keep_o.numpy(), S, tables[r], w.bs)
         moved.append(int(src.size))
         drops.append(int(drop))

@@ -6,8 +6,10 @@ holding a batch of 4 sequences.  Each round appends, per sequence, U[512, 2048] 
 action tokens causally (their lse from the paged attention kernel), updates the LRFU keep
 score (decay 0.5, top-p 0.9; actkv/eviction.py:36-50, :198-224), keeps 4 sinks plus the top
 `budget` tokens by the layer-average keep score with the budget on the 50-round schedule
-4096 -> 16384, and compacts (actkv/paged.py:141-157).  The first 6 rounds of that schedule
-are run: the sequences pass the budget from round 2 on, so blocks are reclaimed.
+4096 -> 16384, and compacts (actkv/paged.py:141-157).  Two stretches of that schedule are
+run: its first 6 rounds (the sequences pass the budget from round 2 on, so blocks are
+reclaimed), and its last 3 (budgets 15882-16384) on sequences pre-filled with 16000 tokens
+each, the length the loop's sequences reach by then.
 
 Checked after every round:
 - scores of layers 0, 17 and 35 against the oracle's N reference folds (rtol 1e-3);
@@ -47,24 +49,36 @@ def _budget(rnd):
     return int(round(B_LO + (B_HI - B_LO) * rnd / (SCHEDULE - 1)))
 
 
-def test_agent_loop_36_layers_batch_4_matches_the_oracle(monkeypatch):
+def _run_rounds(monkeypatch, rounds, prefill=0):
+    """The agent loop over the schedule's `rounds` (indices into the 50-round schedule), each
+    sequence first holding `prefill` tokens of history (appended, never scored)."""
     monkeypatch.setenv("ACTKV_DEBUG", "1")
-    # a request holds at most its last kept count (budget + sinks) plus one round of appends
-    cap = ((_budget(ROUNDS - 1) + SINKS + 2624 + BS - 1) // BS) * BS
+    # a request holds at most its history or its last kept count (budget + sinks), plus one
+    # round of appends
+    cap = ((max(prefill, _budget(rounds[-1]) + SINKS) + 2624 + BS - 1) // BS) * BS
     nb = R * (cap // BS + 2) + 64
-    gcpu = torch.Generator().manual_seed(5)
+    gcpu = torch.Generator().manual_seed(5 + rounds[0])
     cache = PagedKVCache(nb, BS, HKV, D, n_layers=L, dtype=torch.bfloat16, device="cuda")
     cache.free = torch.randperm(nb, generator=gcpu).tolist()
     model = ref.PagedCacheModel(nb, BS, HKV, D, len(HELD))
     model.free = list(cache.free)
-    gdev = torch.Generator(device="cuda").manual_seed(6)
-    rng = np.random.default_rng(7)
+    gdev = torch.Generator(device="cuda").manual_seed(6 + rounds[0])
+    rng = np.random.default_rng(7 + rounds[0])
     reqs = list(range(R))
     lr = PagedLRFU(cache, reqs, cap, LRFUConfig(decay=0.5, top_p=0.9))
     ks_o = torch.zeros(L, R, lr.width)
     held = torch.tensor(HELD, device="cuda")
+    if prefill:
+        k = torch.randn(L, R * prefill, HKV, D, generator=gdev, device="cuda", dtype=torch.bfloat16)
+        v = torch.randn(L, R * prefill, HKV, D, generator=gdev, device="cuda", dtype=torch.bfloat16)
+        cache.append_batch(reqs, k, v, [prefill] * R)
+        kh, vh = _u16(k.index_select(0, held)), _u16(v.index_select(0, held))
+        for j, r in enumerate(reqs):
+            model.append(r, kh[:, j * prefill:(j + 1) * prefill], vh[:, j * prefill:(j + 1) * prefill])
+        del k, v
+        assert cache.tables == model.tables and cache.free == model.free, "prefill allocation"
     reclaimed = 0
-    for rnd in range(ROUNDS):
+    for rnd in rounds:
         budget = _budget(rnd)
         n_act, counts = [], []
         for _ in reqs:
@@ -141,4 +155,15 @@ def test_agent_loop_36_layers_batch_4_matches_the_oracle(monkeypatch):
         print(f"round {rnd}: budget {budget}, {seqs} -> {[cache.seq_used[r] for r in reqs]} tokens, "
               f"{len(cache.free) - free_before} blocks reclaimed", flush=True)
     assert reclaimed > 0, "no round went over its budget"
-    assert all(cache.seq_used[r] <= _budget(ROUNDS - 1) + SINKS for r in reqs)
+    assert all(cache.seq_used[r] <= _budget(rounds[-1]) + SINKS for r in reqs)
+
+
+def test_agent_loop_36_layers_batch_4_matches_the_oracle(monkeypatch):
+    """The schedule's first 6 rounds on empty sequences."""
+    _run_rounds(monkeypatch, list(range(ROUNDS)))
+
+
+def test_agent_loop_late_schedule_matches_the_oracle(monkeypatch):
+    """The schedule's last 3 rounds (budgets 15882, 16133, 16384) on sequences holding 16000
+    tokens of history, as the loop's sequences do by round 47."""
+    _run_rounds(monkeypatch, [SCHEDULE - 3, SCHEDULE - 2, SCHEDULE - 1], prefill=16000)

@@ -667,8 +667,11 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
       acc1 = mfma8(af[1], cur, seed[1]);
       if (k + 1 < NT) read_b(nxt, kb, tile + TG);
       s0 = post(acc0, lim[0], cbase + tile * 32 + lcol);
-      // chain 0 with the VALU work of the previous tile, chain 1 with the
-      // fragment reads of the next tile and the VALU work of chain 0
+      // the first tile's fragment reads all go out before its first MFMA (left
+      // unordered, each was issued and waited for just before its MFMA); chain 0
+      // with the VALU work of the previous tile, chain 1 with the fragment reads
+      // of the next tile and the VALU work of chain 0
+      if (k == 0) __builtin_amdgcn_sched_group_barrier(0x100, KS, 0);   // DS read
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA

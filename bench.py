@@ -82,6 +82,8 @@ def parse(argv=None):
     ap.add_argument("--ora-rounds", type=int, default=50)
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the 2k fp16, 36-layer ragged batch and 131k compaction legs")
+    ap.add_argument("--configs-only", action="store_true",
+                    help="run only those legs (cfg1 without its CPU baseline, cfg3, cfg4); one JSON line")
     ap.add_argument("--ora-short", type=int, default=50,
                     help="rounds of the agent-loop workload reported in the default JSON line (0: none)")
     ap.add_argument("--no-table1", action="store_true", help="skip the reference bench's Table-1 cases")
@@ -1299,6 +1301,14 @@ def main(argv=None):
         return run_attn(args, dev)
     if args.serve:
         return run_serve(args, dev)
+    if args.configs_only:
+        configs = {"cfg1": run_cfg1(args, dev, cpu=False), "cfg3": run_cfg3(args, dev), "cfg4": run_cfg4(args, dev)}
+        line = json.dumps({"configs": configs, **run_info(torch, dev)})
+        print(line)
+        if args.out:
+            with open(args.out, "w") as f:
+                f.write(line + "\n")
+        return 0
 
     log(f"building the {args.layers}-layer workload")
     w = Workload(args, args.layers, dev)

@@ -639,13 +639,25 @@ __global__ void __launch_bounds__(1024) pack_keep_kernel(const uint8_t *keep, in
   const int nw = (padded + 31) >> 5;
   const uint8_t *krow = keep + (int64_t)r * keep_sr;
   uint32_t *brow = bits + (int64_t)r * bits_sr;
+  // a bool byte is 0 or 1: a word of 32 tokens comes from two 16-byte loads when the row is
+  // 16-byte aligned and the word lies wholly below S, bit i = byte i
+  const bool vec = ((uintptr_t)krow & 15) == 0;
+  auto bits4 = [](uint32_t x) {   // 4 bytes of 0/1 -> 4 bits
+    return (x & 1u) | ((x >> 7) & 2u) | ((x >> 14) & 4u) | ((x >> 21) & 8u);
+  };
   uint32_t cnt = 0;
   for (int w = threadIdx.x; w < nw; w += blockDim.x) {
     uint32_t word = 0;
     const int t0 = w * 32;
-    for (int i = 0; i < 32; ++i) {
-      const int t = t0 + i;
-      if (t < S && krow[t]) word |= 1u << i;
+    if (vec && t0 + 32 <= S) {
+      const uint4 lo = *(const uint4 *)(krow + t0), hi = *(const uint4 *)(krow + t0 + 16);
+      word = bits4(lo.x) | (bits4(lo.y) << 4) | (bits4(lo.z) << 8) | (bits4(lo.w) << 12) |
+             (bits4(hi.x) << 16) | (bits4(hi.y) << 20) | (bits4(hi.z) << 24) | (bits4(hi.w) << 28);
+    } else {
+      for (int i = 0; i < 32; ++i) {
+        const int t = t0 + i;
+        if (t < S && krow[t]) word |= 1u << i;
+      }
     }
     brow[w] = word;
     cnt += __popc(word);

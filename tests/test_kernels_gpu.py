@@ -269,6 +269,35 @@ def test_evictions_on_two_side_streams_match_the_oracle():
     _assert_same_state(cache, model)
 
 
+@pytest.mark.parametrize("offset", [0, 1, 16])
+def test_pack_keep_matches_numpy(offset):
+    """actkv_pack_keep (bool mask -> LSB-first bits, zero to whole blocks, kept counts) on rows
+    that are 16-byte aligned (offset 0, 16) or not (offset 1): the vector and byte paths."""
+    from actkv import _hip
+    g = torch.Generator().manual_seed(offset)
+    lens, bs = [70001, 33, 65, 4096], 16
+    R, W = len(lens), 70016 + 48
+    full = torch.rand(R, W + offset, generator=g) < 0.3
+    keep_cpu = full[:, offset:offset + W]
+    keep = full.cuda()[:, offset:offset + W]
+    seq = torch.tensor(lens, dtype=torch.int32, device="cuda")
+    nw = (-(-max(lens) // bs) * bs + 31) // 32
+    bits = torch.full((R, nw), -1, dtype=torch.int32, device="cuda")
+    kept = torch.full((R,), -1, dtype=torch.int32, device="cuda")
+    rc = _hip.lib().actkv_pack_keep(keep.data_ptr(), keep.stride(0), R, seq.data_ptr(), bs, bits.data_ptr(),
+                                    bits.stride(0), kept.data_ptr(), max(lens), _hip.stream(keep.device))
+    assert rc == 0
+    got = bits.cpu().numpy().view(np.uint32)
+    for r, S in enumerate(lens):
+        padded = -(-S // bs) * bs
+        want = np.zeros(padded, dtype=bool)
+        want[:S] = keep_cpu[r, :S].numpy()
+        words = np.packbits(np.pad(want, (0, (-padded) % 32)).reshape(-1, 32)[:, ::-1], axis=1, bitorder="big")
+        want_w = words.view(">u4").reshape(-1).astype(np.uint32)
+        assert np.array_equal(got[r, :want_w.size], want_w), f"row {r}: bits differ"
+        assert int(kept[r]) == int(keep_cpu[r, :S].sum())
+
+
 def test_evict_within_budget_is_a_no_op():
     cache = _filled_cache([20])
     table = list(cache.tables[0])

@@ -639,11 +639,13 @@ __global__ void __launch_bounds__(1024) pack_keep_kernel(const uint8_t *keep, in
   const int nw = (padded + 31) >> 5;
   const uint8_t *krow = keep + (int64_t)r * keep_sr;
   uint32_t *brow = bits + (int64_t)r * bits_sr;
-  // a bool byte is 0 or 1: a word of 32 tokens comes from two 16-byte loads when the row is
-  // 16-byte aligned and the word lies wholly below S, bit i = byte i
+  // a word of 32 tokens comes from two 16-byte loads when the row is 16-byte aligned and the
+  // word lies wholly below S: bit i = (byte i != 0), as in the byte loop
   const bool vec = ((uintptr_t)krow & 15) == 0;
-  auto bits4 = [](uint32_t x) {   // 4 bytes of 0/1 -> 4 bits
-    return (x & 1u) | ((x >> 7) & 2u) | ((x >> 14) & 4u) | ((x >> 21) & 8u);
+  auto bits4 = [](uint32_t x) {   // 4 bytes -> 4 bits, set where the byte is nonzero
+    // (b & 0x7f) + 0x7f carries into bit 7 unless the low 7 bits are zero; | b adds b = 0x80
+    const uint32_t y = (((x & 0x7f7f7f7fu) + 0x7f7f7f7fu) | x) & 0x80808080u;
+    return ((y >> 7) & 1u) | ((y >> 14) & 2u) | ((y >> 21) & 4u) | ((y >> 28) & 8u);
   };
   uint32_t cnt = 0;
   for (int w = threadIdx.x; w < nw; w += blockDim.x) {

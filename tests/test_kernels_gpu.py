@@ -269,16 +269,21 @@ def test_evictions_on_two_side_streams_match_the_oracle():
     _assert_same_state(cache, model)
 
 
-@pytest.mark.parametrize("offset", [0, 1, 16])
-def test_pack_keep_matches_numpy(offset):
-    """actkv_pack_keep (bool mask -> LSB-first bits, zero to whole blocks, kept counts) on rows
-    that are 16-byte aligned (offset 0, 16) or not (offset 1): the vector and byte paths."""
+@pytest.mark.parametrize("offset,any_byte", [(0, False), (1, False), (16, False), (0, True), (1, True)])
+def test_pack_keep_matches_numpy(offset, any_byte):
+    """actkv_pack_keep (keep mask bytes -> LSB-first bits, zero to whole blocks, kept counts) on
+    rows that are 16-byte aligned (offset 0, 16) or not (offset 1): the vector and byte paths.
+    A kept byte is 1, or (any_byte, through the C ABI) any nonzero value 1..255: both paths
+    keep every nonzero byte."""
     from actkv import _hip
-    g = torch.Generator().manual_seed(offset)
+    g = torch.Generator().manual_seed(offset + 100 * any_byte)
     lens, bs = [70001, 33, 65, 4096], 16
     R, W = len(lens), 70016 + 48
     full = torch.rand(R, W + offset, generator=g) < 0.3
-    keep_cpu = full[:, offset:offset + W]
+    if any_byte:
+        full = full.to(torch.uint8) * torch.randint(1, 256, full.shape, generator=g, dtype=torch.uint8)
+        assert (full == 128).any() and (full == 255).any() and (full == 1).any()
+    keep_cpu = full[:, offset:offset + W] != 0
     keep = full.cuda()[:, offset:offset + W]
     seq = torch.tensor(lens, dtype=torch.int32, device="cuda")
     nw = (-(-max(lens) // bs) * bs + 31) // 32

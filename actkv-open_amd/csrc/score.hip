@@ -3,13 +3,14 @@
 // Reference: actkv/kernels/lse_attn.py:85-163.  The reference launches one
 // Triton program per (request, logical block, KV head) and folds ONE action
 // query per launch, so K is re-read from HBM once per action token.  Here one
-// workgroup owns a (layer, request, KV head) pair and a token range, holds the
-// head's whole action-query tile (N queries x G group heads) on chip and reads
-// the range's K rows from HBM exactly once.  Two MFMA kernels: above 384 query
-// rows the tile sits in registers while K chunks are shared through LDS
-// (score_qreg_kernel: fewer LDS reads per MFMA, the matrix cores bound it); up
-// to 384 rows each wave streams its own K slices into registers against the
-// tile in LDS (score_kslice_kernel: more K in flight).  Both compute
+// workgroup owns a (layer, request, KV head) pair -- or, for small tiles, several
+// KV heads of one (layer, request) -- and a token range, holds the whole
+// action-query tile (N queries x G group heads per head) on chip and reads the
+// range's K rows from HBM exactly once.  Two MFMA kernels: above 384 query rows,
+// and up to 128, the tile sits in registers while K chunks are shared through LDS
+// (score_qreg_kernel: fewer LDS reads per MFMA; the matrix cores bound it above
+// 384 rows, HBM up to 128); from 129 to 384 rows each wave streams its own K
+// slices into registers against the tile in LDS (score_kslice_kernel).  Both compute
 //
 //   acc[row, t] = q_row . k_t - lse_row / scale            (bf16/fp16 MFMA, fp32 acc)
 //   p[n, t]     = exp2(scale*log2(e) * max_g acc[(n,g), t]) (max over the GQA group
@@ -32,8 +33,6 @@ namespace actkv {
 // Longest token range of one MFMA workgroup (its block-table slice holds
 // MFMA_MAX_TOKENS / 16 entries, one per thread of the 512).
 constexpr int MFMA_MAX_TOKENS = 8192;
-// Tokens per K chunk of the query-tile kernel (4 tiles of 32).
-constexpr int QREG_CHUNK = 128;
 
 struct ScoreArgs {
   const void *q;
@@ -416,22 +415,25 @@ score_kslice_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
 }
 
 // ------------------------------------------------------------------ MFMA, query tile in registers
-// One workgroup of 8 waves (2 per SIMD) owns a (layer, request, KV head) pair and
-// a token range.  The pair's action-query tile -- rows (query n, group head g),
-// nq*G <= 64*RG of them, head_dim 128, bf16/fp16 -- is split over RG row groups
-// of 64 rows, and the 8 waves over RG row groups x 8/RG token groups: wave
-// (rg, tg) keeps row group rg's two 32-row tiles as MFMA A operands in registers
-// for the whole range, with their accumulator seeds -lse/scale (-inf for padding
-// rows, which then add exp2(-inf) = 0) as the C operand of each chain's first
-// MFMA, and multiplies the 32-token tiles tg, tg + 8/RG, ... of every chunk.
-// RG = 8 for 385..512 rows, 4 up to 256 and 2 up to 128: every wave has rows.
+// One workgroup of 8 waves (2 per SIMD) owns HP KV heads of one (layer, request) and a
+// token range.  Each head's action-query tile -- rows (query n, group head g), nq*G of
+// them, head_dim 128, bf16/fp16 -- is split into row groups of 64 rows; the workgroup
+// holds RG row groups (RG/HP per head) and splits its 8 waves over RG row groups x 8/RG
+// token groups: wave (rg, tg) keeps row group rg's two 32-row tiles as MFMA A operands in
+// registers for the whole range, with their accumulator seeds -lse/scale (-inf for
+// padding rows, which then add exp2(-inf) = 0) as the C operand of each chain's first
+// MFMA, and multiplies the 32-token tiles tg, tg + 8/RG, ... of every chunk of its head.
+// With HP = 1: RG = 8 for 385..512 rows, 4 up to 256 and 2 up to 128.  With HP = 2 or 4
+// (up to 256 or 128 rows) every wave still holds 64 rows and multiplies every tile of
+// a chunk, and each token's K is read as HP heads' contiguous 256-byte pieces.
 //
-// K streams through LDS in chunks of CH tokens, double buffered: the waves load
-// chunk c+1 straight from HBM into LDS (global_load_lds_dwordx4) while they
-// multiply chunk c, and one barrier per chunk hands a chunk over.  A chunk is
-// stored as 1 KiB B fragments, [tile][k step][lane] x 16 bytes, so every
-// fragment read (ds_read_b128) is one contiguous, conflict-free 1 KiB and feeds
-// two MFMAs (one per row tile).
+// K streams through LDS in chunks of CH tokens, NBUF - 1 chunks in flight: the waves
+// load chunk c+NBUF-1 straight from HBM into LDS (global_load_lds_dwordx4) while they
+// multiply chunk c, and one barrier per chunk hands a chunk over.  Two layouts: 1 KiB B
+// fragments, [tile][k step][lane] x 16 bytes (HP = 1 only), so every fragment read
+// (ds_read_b128) is one contiguous 1 KiB; or whole token rows of HP x 256 bytes with
+// each head's 16-byte columns XOR-swizzled by token.  Both are conflict-free, and every
+// fragment read feeds two MFMAs (one per row tile).
 //
 // v_mfma_f32_32x32x16 lane layout: lane L supplies A[L%32][8*(L/32)+j] and
 // B[8*(L/32)+j][L%32] (j < 8) and receives D[8*(r/4) + 4*(L/32) + r%4][L%32] in
@@ -444,41 +446,51 @@ score_kslice_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
 // exp/max/sum of row tile 1 of the previous tile, then the chain of row tile 1
 // beside the exp/max/sum of row tile 0 and the B-fragment reads of the next
 // tile.  Per-token partial sums (one per row group and lane half) go to LDS at
-// the end of the chunk; after the next barrier the first CH threads add them in
-// a fixed order and write the running means.
-template <typename T, typename V8, int G, bool CAUSAL, int RG, int NBUF, bool SWZ>
+// the end of the chunk; after the next barrier the first HP x CH threads add each
+// head's in a fixed order and write the running means.
+template <typename T, typename V8, int G, bool CAUSAL, int RG, int NBUF, bool SWZ, int CH, int HP>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
   constexpr int NW = 8, TG = NW / RG, KS = 8, QG = 4 / G;
   static_assert(RG == 2 || RG == 4 || RG == 8, "row groups");
+  static_assert(HP == 1 || HP == 2 || HP == 4 || HP == 8, "heads per workgroup");
+  static_assert(RG % HP == 0 && (HP == 1 || SWZ), "whole row groups per head; packed heads use rows");
   static_assert(NBUF >= 2 && NBUF <= 4, "K chunk buffers");
-  constexpr int TPC = QREG_CHUNK / 32;  // 32-token tiles per chunk
-  constexpr int CH = QREG_CHUNK;        // tokens per chunk
+  static_assert(CH == 32 || CH == 64 || CH == 128 || CH == 256, "tokens per chunk");
+  constexpr int RGH = RG / HP;          // row groups per head
+  constexpr int TPC = CH / 32;          // 32-token tiles per chunk
   constexpr int NT = TPC / TG;          // tiles per wave per chunk
-  constexpr int LPW = TPC * KS / NW;    // fragment loads per wave per chunk
-  constexpr int NRED = 2 * RG;          // partial sums per token
-  static_assert(KS % LPW == 0, "a wave's loads stay within one tile");
+  static_assert(NT >= 1 && NT * TG == TPC, "token groups");
+  constexpr int HROW = HP * 256;        // bytes of one token's HP head pieces
+  constexpr int CHB = CH * HROW;        // bytes of one chunk
+  constexpr int LPW = CHB / 1024 / NW;  // 1 KiB loads per wave per chunk
+  static_assert(LPW * 1024 * NW == CHB, "whole loads per wave");
+  constexpr int NRED = 2 * RG;          // partial sums per token and head pack
+  constexpr int NOLD = HP * CH / 64;    // 256-byte loads of the old means per chunk
+  static_assert(NOLD * 64 == HP * CH, "whole old-mean loads");
+  static_assert(SWZ || KS % LPW == 0, "a wave's fragment loads stay within one tile");
   // the K buffers are distinct arrays: the compiler then knows that reads of one
   // need not wait for the loads in flight into the others
-  __shared__ __attribute__((aligned(16))) unsigned char kbuf_a[TPC * KS * 1024];
-  __shared__ __attribute__((aligned(16))) unsigned char kbuf_b[TPC * KS * 1024];
-  __shared__ __attribute__((aligned(16))) unsigned char kbuf_c[NBUF >= 3 ? TPC * KS * 1024 : 16];
-  __shared__ __attribute__((aligned(16))) unsigned char kbuf_d[NBUF >= 4 ? TPC * KS * 1024 : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char kbuf_a[CHB];
+  __shared__ __attribute__((aligned(16))) unsigned char kbuf_b[CHB];
+  __shared__ __attribute__((aligned(16))) unsigned char kbuf_c[NBUF >= 3 ? CHB : 16];
+  __shared__ __attribute__((aligned(16))) unsigned char kbuf_d[NBUF >= 4 ? CHB : 16];
   __shared__ float red[2][NRED][CH];
-  __shared__ float oldm[8][CH];   // running means of the chunks in flight, ring of 8 >= NBUF + 1
+  __shared__ float oldm[8][HP * CH];   // running means of the chunks in flight, [head][token]; ring of 8 >= NBUF + 1
   __shared__ int bts[MFMA_MAX_TOKENS / 16];
 
-  // XCD-aware work mapping: all token ranges of one (layer, request, head)
-  // pair land on the same XCD (blockIdx % 8), so its query tile is fetched
-  // from HBM into that XCD's L2 once.
+  // XCD-aware work mapping: all token ranges of one (layer, request, head pack)
+  // land on the same XCD (blockIdx % 8), so its query tiles are fetched from HBM
+  // into that XCD's L2 once.
   const int bid = blockIdx.x;
   const int xcd = bid & 7, jj = bid >> 3;
   const int p = (jj / cpp) * 8 + xcd;
   const int chunk = jj % cpp;
   if (p >= pairs) return;
-  const int h = p % a.Hkv;
-  const int r = (p / a.Hkv) % a.R;
-  const int l = p / (a.Hkv * a.R);
+  const int hpk = a.Hkv / HP;           // head packs per (layer, request)
+  const int h0 = (p % hpk) * HP;
+  const int r = (p / hpk) % a.R;
+  const int l = p / (hpk * a.R);
   const int S = seq_len_of(a, r);
   const int t_begin = chunk * tpw;
   if (t_begin >= S) return;
@@ -493,7 +505,9 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
   const int wave = tid >> 6, lane = tid & 63;
   const int lcol = lane & 31, lh = lane >> 5;
   const int rg = wave % RG, tg = wave / RG;
-  const bool active = rg * 64 < nq * G;  // this wave's rows hold at least one query row
+  const int hi = rg / RGH, rgl = rg % RGH;   // this wave's head in the pack, row group within it
+  const int h = h0 + hi;
+  const bool active = rgl * 64 < nq * G;  // this wave's rows hold at least one query row
 
   // ---- set-up: every load goes out before the first wait
   const int b0 = t_begin >> bs_shift;
@@ -509,7 +523,7 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
     // unconditional loads at clamped rows: no branch serialises them
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt) {
-      const int row = rg * 64 + jt * 32 + lcol;
+      const int row = rgl * 64 + jt * 32 + lcol;
       const int n = row / G, g = row % G;
       const T *qp = qbase + (int64_t)(a.qc0 + min(n, nq - 1)) * a.q_sn + (int64_t)(h * G + g) * a.q_sh + lh * 8;
 #pragma unroll
@@ -521,7 +535,7 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
       for (int i = 0; i < 4; ++i) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int rw = rg * 64 + jt * 32 + 8 * i + 4 * lh + j;
+          const int rw = rgl * 64 + jt * 32 + 8 * i + 4 * lh + j;
           const int nn = rw / G, gg = rw % G;
           const float v = lbase[(int64_t)(a.qc0 + min(nn, nq - 1)) * a.lse_sn + h * G + gg];
           seed[jt][4 * i + j] = nn < nq ? -v * inv_scale : -INFINITY;
@@ -529,7 +543,7 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
         if constexpr (CAUSAL) {
 #pragma unroll
           for (int qg = 0; qg < QG; ++qg) {
-            const int nn = (rg * 64 + jt * 32 + 8 * i + 4 * lh + qg * G) / G;
+            const int nn = (rgl * 64 + jt * 32 + 8 * i + 4 * lh + qg * G) / G;
             const int v = a.kv_len[(int64_t)r * a.N + a.qc0 + min(nn, nq - 1)];
             lim[jt][i][qg] = nn < nq ? v : 0;
           }
@@ -543,20 +557,20 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
   __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();
 
-  const T *krow0 = (const T *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh;
+  const T *krow0 = (const T *)a.kv + (int64_t)l * a.kv_sl;
   const float c2 = a.scale * 1.4426950408889634f;
-  float *obase = a.out + (int64_t)l * a.out_sl + (int64_t)r * a.out_sr + (int64_t)h * a.out_sh;
+  float *obase0 = a.out + (int64_t)l * a.out_sl + (int64_t)r * a.out_sr + (int64_t)h0 * a.out_sh;
   const float fn0 = (float)n0, fden = (float)(n0 + nq);
   const int ld_tile = (wave * LPW) / KS, ld_ks = (wave * LPW) % KS;
 
-  // A chunk in LDS is CH token rows of 256 bytes (the head's 128 elements), each row's
-  // 16-byte columns stored XOR-swizzled: LDS column c of token t holds the row's column
-  // c ^ (t % 16).  This wave's share: tokens [16 wave, 16 wave + 16) of the chunk, as LPW
-  // loads of four whole rows (lane i writes bytes [16i, 16i + 16) of its 1 KiB: row i/16,
-  // LDS column i%16), so every load reads 256 contiguous bytes per row.  A token past
-  // t_end, or in a block the table marks invalid, reads row 0 of block 0 instead; its
-  // score is never written.
-  static_assert(LPW * 4 * NW == CH, "four rows per load");
+  // Swizzled rows: a chunk in LDS is CH token rows of HROW bytes, the 256-byte pieces of
+  // heads h0 .. h0+HP-1 side by side, and each piece's 16-byte columns stored XOR-swizzled:
+  // LDS column c of token t's piece holds that head's column c ^ (t % 16).  The chunk is
+  // CHB / 16 units of 16 bytes; this wave's share is LPW loads of 64 consecutive units
+  // (lane i of load j writes unit 64 (LPW wave + j) + i), so every load reads whole
+  // 256-byte pieces, and with HP > 1 HP x 256 contiguous bytes of each token's row.  A
+  // token past t_end, or in a block the table marks invalid, reads row 0 of block 0
+  // instead; its score is never written.
   auto load_chunk = [&](int cbase, unsigned char *kb) {
     const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_address(&kb[wave * LPW * 1024]));
     if constexpr (!SWZ) {
@@ -567,43 +581,51 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
       const bool ok = t < t_end && phys >= 0;
       phys = ok ? phys : 0;
       const int slot = ok ? (t & (BS - 1)) : 0;
-      const T *kp = krow0 + (int64_t)phys * a.kv_sb + (int64_t)slot * a.kv_ss + lh * 8 + ld_ks * 16;
+      const T *kp = krow0 + (int64_t)h0 * a.kv_sh + (int64_t)phys * a.kv_sb + (int64_t)slot * a.kv_ss + lh * 8 +
+                    ld_ks * 16;
 #pragma unroll
       for (int i = 0; i < LPW; ++i) load_lds16(kp + i * 16, dst + i * 1024);
       return;
     }
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
-      const int tl = wave * 16 + i * 4 + (lane >> 4);   // token of the chunk (tl % 16 = 4i + lane/16)
+      const int u = (wave * LPW + i) * 64 + lane;   // 16-byte unit of the chunk
+      const int tl = u / (HP * 16);                 // token of the chunk
+      const int w = u % (HP * 16);
+      const int hp = w >> 4, col = (w & 15) ^ (tl & 15);
       const int t = cbase + tl;
       const int bi = min((t >> bs_shift) - b0, nbt - 1);
       int phys = bts[bi];
       const bool ok = t < t_end && phys >= 0;
       phys = ok ? phys : 0;
       const int slot = ok ? (t & (BS - 1)) : 0;
-      const int col = (lane & 15) ^ (tl & 15);
-      load_lds16(krow0 + (int64_t)phys * a.kv_sb + (int64_t)slot * a.kv_ss + col * 8, dst + i * 1024);
+      load_lds16(krow0 + (int64_t)phys * a.kv_sb + (int64_t)slot * a.kv_ss + (int64_t)(h0 + hp) * a.kv_sh + col * 8,
+                 dst + i * 1024);
     }
   };
-  // The running means of the CH tokens at cbase -> oldm[slot] (wave 0: two loads into
-  // LDS of 4 bytes per lane, at clamped in-range tokens; those past t_end are not used).
+  // The running means of the HP x CH (head, token) pairs at cbase -> oldm[slot] (wave 0:
+  // NOLD loads into LDS of 4 bytes per lane, at clamped in-range tokens; those past t_end
+  // are not used).
   auto load_old = [&](int cbase, int slot) {
     if (wave == 0) {
       const uint32_t dst = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_address(&oldm[slot][0]));
 #pragma unroll
-      for (int i = 0; i < CH / 64; ++i) load_lds4(obase + min(cbase + i * 64 + lane, t_end - 1), dst + i * 256);
+      for (int i = 0; i < NOLD; ++i) {
+        const int e = i * 64 + lane, eh = e / CH, et = e % CH;
+        load_lds4(obase0 + (int64_t)eh * a.out_sh + min(cbase + et, t_end - 1), dst + i * 256);
+      }
     }
   };
-  // B operand of k step ks: lane (lcol, lh) takes token lcol's column 2 ks + lh, at LDS
-  // column (2 ks + lh) ^ (lcol % 16) of its row; any 16 consecutive lanes read 16
+  // B operand of k step ks: lane (lcol, lh) takes token lcol's column 2 ks + lh of head hi,
+  // at LDS column (2 ks + lh) ^ (lcol % 16) of its piece; any 16 consecutive lanes read 16
   // distinct columns (no bank conflict)
   int roff[KS];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) roff[ks] = lcol * 256 + (((2 * ks + lh) ^ (lcol & 15)) << 4);
+  for (int ks = 0; ks < KS; ++ks) roff[ks] = lcol * HROW + hi * 256 + (((2 * ks + lh) ^ (lcol & 15)) << 4);
   auto read_b = [&](V8 (&b8)[KS], const unsigned char *kb, int tile) {
     if constexpr (SWZ) {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) b8[ks] = *(const V8 *)(&kb[tile * 32 * 256 + roff[ks]]);
+      for (int ks = 0; ks < KS; ++ks) b8[ks] = *(const V8 *)(&kb[tile * 32 * HROW + roff[ks]]);
     } else {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) b8[ks] = *(const V8 *)(&kb[((tile * KS + ks) * 64 + lane) * 16]);
@@ -690,14 +712,17 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
 #pragma unroll
     for (int k = 0; k < NT; ++k) red[buf][2 * rg + lh][(tg + k * TG) * 32 + lcol] = part[k];
   };
+  // thread (head eh, token et) of the first HP x CH adds that head's 2 RGH partial sums of
+  // the token in a fixed order
   auto reduce_chunk = [&](int cbase, int buf, int slot) {
-    if (tid < CH) {
-      const int t = cbase + tid;
+    if (tid < HP * CH) {
+      const int eh = tid / CH, et = tid % CH;
+      const int t = cbase + et;
       if (t < t_end && bts[(t >> bs_shift) - b0] >= 0) {
         float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < NRED; ++i) s += red[buf][i][tid];
-        obase[t] = (oldm[slot][tid] * fn0 + s) / fden;
+        for (int i = 0; i < 2 * RGH; ++i) s += red[buf][2 * RGH * eh + i][et];
+        obase0[(int64_t)eh * a.out_sh + t] = (oldm[slot][tid] * fn0 + s) / fden;
       }
     }
   };
@@ -706,10 +731,10 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
   // and issues the loads of chunk c + NBUF - 1 (K into the buffer chunk c - 1 used, the
   // old means into ring slot (c + NBUF - 1) % 8, which no chunk still to be reduced
   // holds).  After the set-up every vector memory operation of the loop is a load into
-  // LDS or a store: a wave issues LPW K loads per chunk, and wave 0 two more for the old
-  // means, after them.  So at most (NBUF - 2) * LPW of a wave's operations issued after
-  // chunk c's loads are outstanding when chunk c's are: vmcnt((NBUF - 2) * LPW) means
-  // chunk c's share of this wave is in LDS.
+  // LDS or a store: a wave issues LPW K loads per chunk, and wave 0 NOLD more for the old
+  // means, after them.  Loads complete in issue order, so while any of chunk c's loads is
+  // outstanding so are the (NBUF - 2) * LPW K loads of later chunks issued after it:
+  // vmcnt((NBUF - 2) * LPW) means chunk c's share of this wave is in LDS.
   const int nch = (t_end - t_begin + CH - 1) / CH;
   constexpr int VMW = (NBUF - 2) * LPW;
   auto step = [&](int c, const unsigned char *kcur, unsigned char *knext) {
@@ -792,12 +817,10 @@ static int kslice_tokens_per_wg(int pairs, int span, int nw) {
 // Token range per workgroup of the query-tile kernel: a whole number of chunks.  One
 // workgroup fills a CU, so the launch runs in rounds of CU-count workgroups, and
 // each workgroup pays a set-up (block-table slice, query tile, first chunk) of
-// about SETUP chunks before its pipeline runs.  The range minimises
-// rounds x (SETUP + chunks per workgroup): one layer of one request spreads over
+// about `setup` chunks before its pipeline runs.  The range minimises
+// rounds x (setup + chunks per workgroup): one layer of one request spreads over
 // every CU, 36 layers run 9 full rounds of 4096 tokens.
-static int qreg_tokens_per_wg(int pairs, int span) {
-  constexpr double SETUP = 1.5;  // measured: ~5 us against ~3.7 us per 512-row chunk
-  constexpr int chunk = QREG_CHUNK;
+static int qreg_tokens_per_wg(int pairs, int span, int chunk, double setup) {
   const int64_t cus = device_cus();
   const int span_chunks = (span + chunk - 1) / chunk;
   const int max_chunks = std::min(span_chunks, MFMA_MAX_TOKENS / chunk);
@@ -805,7 +828,7 @@ static int qreg_tokens_per_wg(int pairs, int span) {
   double best_cost = 0.0;
   for (int k = 1; k <= max_chunks; ++k) {
     const int64_t items = (int64_t)pairs * ((span_chunks + k - 1) / k);
-    const double cost = (double)((items + cus - 1) / cus) * (SETUP + k);
+    const double cost = (double)((items + cus - 1) / cus) * (setup + k);
     if (k == 1 || cost < best_cost) { best_cost = cost; best = k; }
   }
   return best * chunk;
@@ -838,29 +861,41 @@ static int launch_mfma(const ScoreArgs &a0, int bs_shift, hipStream_t st) {
     a.qcn = std::min(q_per_launch, a0.N - qc0);
     const int rows = a.qcn * G;
     // measured on 36 layers x 4 x 8k (causal) and 36 x 32k: the query-register kernel
-    // is faster up to 128 rows (whole-row loads: 4.4-4.7 TB/s of K against 3.5-4.4) and
-    // above 384 (the matrix cores bound it); the K-slice kernel from 129 to 384 rows
+    // is faster up to 128 rows (several heads per workgroup: 4.6-4.9 TB/s of K against
+    // 3.5-4.4) and above 384 (the matrix cores bound it); the K-slice kernel from 129 to
+    // 384 rows (with 2 heads per workgroup, 4 row groups each, or 1 head and 4 row
+    // groups, the query-register kernel took 4-10% longer there)
     const bool qreg = choice == MFMA_QREG || (choice == MFMA_AUTO && (rows <= 128 || rows > 384));
     if (qreg) {
-      // query tile in registers, K shared through LDS; RG row groups of 64 rows
-      const int tpw = qreg_tokens_per_wg(pairs, span);
-      const int cpp = (span + tpw - 1) / tpw;
-      const int grid = ((pairs + 7) / 8) * 8 * cpp;
-#define ACTKV_QREG(RGV, NB, SW)                                                                    \
+      // query tile in registers, K shared through LDS; RG row groups of 64 rows over HPV
+      // heads per workgroup, chunks of CHV tokens, the first one's set-up costing about
+      // SETUP chunks
+#define ACTKV_QREG(RGV, NB, SW, CHV, SETUP, HPV)                                                   \
   do {                                                                                             \
+    const int packs = a0.L * a0.R * (a0.Hkv / HPV);                                                \
+    const int tpw = qreg_tokens_per_wg(packs, span, CHV, SETUP);                                   \
+    const int cpp = (span + tpw - 1) / tpw;                                                        \
+    const int grid = ((packs + 7) / 8) * 8 * cpp;                                                  \
     if (causal)                                                                                    \
-      hipLaunchKernelGGL((score_qreg_kernel<T, V8, G, true, RGV, NB, SW>), dim3(grid), dim3(512), 0, \
-                         st, a, tpw, cpp, pairs, bs_shift);                                        \
+      hipLaunchKernelGGL((score_qreg_kernel<T, V8, G, true, RGV, NB, SW, CHV, HPV>), dim3(grid),   \
+                         dim3(512), 0, st, a, tpw, cpp, packs, bs_shift);                          \
     else                                                                                           \
-      hipLaunchKernelGGL((score_qreg_kernel<T, V8, G, false, RGV, NB, SW>), dim3(grid), dim3(512),  \
-                         0, st, a, tpw, cpp, pairs, bs_shift);                                     \
+      hipLaunchKernelGGL((score_qreg_kernel<T, V8, G, false, RGV, NB, SW, CHV, HPV>), dim3(grid),  \
+                         dim3(512), 0, st, a, tpw, cpp, packs, bs_shift);                          \
   } while (0)
-      // up to 256 rows the call streams K at the HBM rate: whole-row loads into swizzled
-      // rows and three chunks in flight; above, the matrix cores bound it: fragment
-      // layout (fewer address instructions) and two chunks in flight
-      if (rows <= 128) ACTKV_QREG(2, 3, true);
-      else if (rows <= 256) ACTKV_QREG(4, 3, true);
-      else ACTKV_QREG(8, 2, false);
+      // Up to 128 rows the call streams K at the HBM rate.  Several KV heads of the same
+      // tokens then share a workgroup (8 up to 64 rows, 4 up to 128): every wave keeps 64
+      // rows, and each token's K arrives as 4 or 8 contiguous 256-byte pieces (whole 2 KiB
+      // rows with 8 heads of 128).  Measured on 36 layers x 4 x 8k, causal: 16 queries 491
+      // against 532 us with one head per workgroup, 32 queries 530 against 580.  Above 384
+      // rows the matrix cores bound it: fragment layout (fewer address instructions) and
+      // two chunks in flight.  Set-up measured at ~5 us against ~3.7 us per 512-row chunk
+      // of 128 tokens.
+      if (rows <= 64 && a0.Hkv % 8 == 0) ACTKV_QREG(8, 2, true, 32, 8.0, 8);
+      else if (rows <= 128 && a0.Hkv % 4 == 0) ACTKV_QREG(8, 2, true, 64, 4.0, 4);
+      else if (rows <= 128) ACTKV_QREG(2, 3, true, 128, 1.5, 1);
+      else if (rows <= 256) ACTKV_QREG(4, 3, true, 128, 1.5, 1);
+      else ACTKV_QREG(8, 2, false, 128, 1.5, 1);
 #undef ACTKV_QREG
     } else {
       // 12 waves stream their own K slices against the tile in LDS, which keeps

@@ -420,6 +420,62 @@ def test_action_scores_leave_tokens_of_out_of_pool_blocks_untouched(dtype, hq, h
         torch.testing.assert_close(got[r][:, keep], out_o[r][:, keep], rtol=rtol, atol=1e-6)
 
 
+@pytest.mark.parametrize("hq,hkv,n_q,half", [
+    (32, 8, 16, 0),      # 64 rows: 8 KV heads per workgroup
+    (32, 8, 32, 1),      # 128 rows: 4 KV heads per workgroup
+    (8, 8, 9, 1),        # group 1, 9 rows: 8 heads per workgroup
+    (16, 4, 30, 0),      # group 4 over 4 KV heads, 120 rows: 4 heads per workgroup
+])
+def test_action_scores_heads_per_workgroup_with_strided_heads(hq, hkv, n_q, half):
+    """Small query tiles score several KV heads of the same tokens in one workgroup, reading
+    each token's heads side by side.  K here is a view with a head stride of 2 x head_dim
+    (every other 128-element piece of a wider row, starting at piece `half`), so the heads
+    are not contiguous; with ragged query counts, causal limits and two out-of-pool table
+    entries, against the oracle's folds."""
+    d, bs, lens = 128, 16, [700, 333, 1400]
+    R = len(lens)
+    g = torch.Generator().manual_seed(40 + n_q)
+    nb = sum(-(-s // bs) for s in lens) + 5
+    wide = torch.randn(2, nb, bs, hkv, 2 * d, generator=g).to(torch.bfloat16)
+    kv = wide.cuda()[..., half * d:(half + 1) * d]
+    assert kv.stride(-2) == 2 * d and not kv.is_contiguous()
+    perm = torch.randperm(nb, generator=g).tolist()
+    tables, pos = [], 0
+    for s in lens:
+        nblk = -(-s // bs)
+        tables.append(perm[pos:pos + nblk])
+        pos += nblk
+    mb = max(len(t) for t in tables)
+    bt = torch.zeros(R, mb, dtype=torch.int32)
+    for r, t in enumerate(tables):
+        bt[r, :len(t)] = torch.tensor(t, dtype=torch.int32)
+    kv0 = wide[..., half * d:(half + 1) * d].contiguous()
+    q = torch.randn(R, n_q, hq, d, generator=g).to(torch.bfloat16)
+    lse = torch.stack([ref.decode_lse(q[:, n], kv0, tables, lens) for n in range(n_q)], 1)
+    n_valid = torch.tensor([n_q, max(1, n_q // 3), n_q - 1], dtype=torch.int32)
+    kv_len = torch.stack([torch.randint(1, s + 1, (n_q,), generator=g) for s in lens]).to(torch.int32)
+    width = mb * bs
+    out0 = torch.rand(R, hkv, width, generator=g)
+    n0 = torch.tensor([3, 0, 1], dtype=torch.int32)
+    bad = bt.clone()
+    bad[0, 5] = -1                      # tokens 80..95 of request 0
+    bad[2, 40] = nb + 3                 # tokens 640..655 of request 2
+    out_k, n_k = out0.cuda(), n0.cuda()
+    action_scores(q.cuda(), kv, bad.cuda(), torch.tensor(lens, dtype=torch.int32, device="cuda"), lse.cuda(),
+                  out_k, n_k, n_valid=n_valid.cuda(), kv_len=kv_len.cuda())
+    out_o, n_o = out0.clone(), n0.clone()
+    ref.action_scores_nfold(q, kv0, tables, lens, lse, out_o, n_o, n_valid=n_valid, kv_len=kv_len)
+    got = out_k.cpu()
+    untouched = torch.zeros(R, width, dtype=torch.bool)
+    untouched[0, 80:96] = True
+    untouched[2, 640:656] = True
+    for r in range(R):
+        assert torch.equal(got[r][:, untouched[r]], out0[r][:, untouched[r]]), f"request {r}: out-of-pool columns"
+        keep = ~untouched[r]
+        torch.testing.assert_close(got[r][:, keep], out_o[r][:, keep], rtol=1e-3, atol=1e-6)
+    assert torch.equal(n_k.cpu(), n_o)
+
+
 def test_action_scores_every_layer_in_one_launch():
     """kv [L, 2, ...] with q [L, R, N, Hq, D]: each layer scored against its own K (extension)."""
     lens = [300, 77]

@@ -772,8 +772,9 @@ def run_cfg1(args, dev, cpu=True):
     return res
 
 
-def run_cfg3(args, dev, steps=5):
-    """36 layers x 8 ragged sequences scored and evicted in one cal_attn + one evict_batch."""
+def run_cfg3(args, dev, steps=5, cpu=False):
+    """36 layers x 8 ragged sequences scored and evicted in one cal_attn + one evict_batch.
+    cpu: also time the CPU baseline on one layer of one request, extrapolated (labelled)."""
     w = RaggedWorkload(args, dev)
     checks, moved, drops = check_ragged(w)
     work = w.algorithmic(moved, drops)
@@ -796,12 +797,15 @@ def run_cfg3(args, dev, steps=5):
                      > work["bytes_score"] / (HBM_PEAK_GBS * 1e9) else "hbm"),
            "floor_us": round(floor, 1), "frac_of_floor": round(floor / m["step_us"], 4),
            "moved_rows": sum(moved), "blocks_freed": sum(drops), "checks": checks}
+    if cpu:
+        res["cpu_baseline"] = cpu_ragged(w, nbytes)
     del w
     return res
 
 
-def run_cfg4(args, dev, steps=5):
-    """131072 tokens x 36 layers, clustered keep runs, compaction only."""
+def run_cfg4(args, dev, steps=5, cpu=False):
+    """131072 tokens x 36 layers, clustered keep runs, compaction only.  cpu: also time the
+    CPU baseline on one layer's planes, extrapolated to every layer (labelled)."""
     w = ClusteredWorkload(args, dev)
     checks, moved, drop = check_clustered(w)
     work = w.algorithmic(moved, drop)
@@ -816,6 +820,8 @@ def run_cfg4(args, dev, steps=5):
            "pct_of_hbm_peak": round(100 * work["bytes_compact"] / (m["step_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 2),
            "bound": "hbm", "floor_us": round(floor, 1), "frac_of_floor": round(floor / m["step_us"], 4),
            "moved_rows": moved, "blocks_freed": drop, "checks": checks}
+    if cpu:
+        res["cpu_baseline"] = cpu_clustered(w, work["bytes_compact"])
     del w
     return res
 
@@ -848,6 +854,89 @@ def cpu_runs(w, runs=3):
         t2 = time.perf_counter()
         times.append((t1 - t0, t2 - t1))
     return times
+
+
+def cpu_ragged(w, nbytes, runs=3):
+    """CPU baseline of the ragged batch: the oracle's reference-style path on one layer of the
+    request with the least scoring work -- its N action-query folds one query at a time
+    (lse_attn.py:63-78), then its evict on that layer (keep mask, plan, row moves, allocator;
+    paged.py:141-157) -- `runs` times, median.  The whole step is extrapolated linearly: the
+    folds by sum_r N_r S_r over this request's N S, the evict by sum_r S_r over its S, each
+    times L layers (a full run would take tens of minutes)."""
+    import torch
+    from oracle import reference as ref
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    s = min(w.reqs, key=lambda r: w.S[r] * w.Nq[r])
+    S, N = w.S[s], w.Nq[s]
+    table = [w.host0[1][s]]
+    kv_l = w.kv0[0].cpu()
+    q = w.q[0, s, :N].cpu()
+    lse = w.lse[0, s, :N].cpu()
+    folds, evicts = [], []
+    for _ in range(runs):
+        out = torch.zeros(1, w.hkv, w.width)
+        ns = torch.zeros(1, dtype=torch.int32)
+        model = ref.PagedCacheModel(w.nb, w.bs, w.hkv, w.d, 1)
+        model.kv = kv_l.unsqueeze(0).view(torch.int16).numpy().copy()
+        model.free, model.tables, model.seq_used = list(w.host0[0]), {0: list(table[0])}, {0: S}
+        t0 = time.perf_counter()
+        for n in range(N):
+            ref.action_scores_fold(q[n:n + 1], kv_l, table, [S], lse[n:n + 1], out, ns)
+        t1 = time.perf_counter()
+        model.evict(0, out, w.budgets[s], protected=w.sinks)
+        t2 = time.perf_counter()
+        folds.append(t1 - t0)
+        evicts.append(t2 - t1)
+        del model
+    f_med, e_med = statistics.median(folds), statistics.median(evicts)
+    f_scale = sum(n * t for n, t in zip(w.Nq, w.S)) / (N * S) * w.L
+    e_scale = sum(w.S) / S * w.L
+    step_s = f_med * f_scale + e_med * e_scale
+    sample = (f"one layer of request {s} ({S} tokens, {N} action queries): all folds (one action query per "
+              f"reference fold) + evict of that layer, {runs} runs, median folds {f_med:.2f} s (runs "
+              f"{', '.join(f'{x:.2f}' for x in folds)} s), evict {e_med:.3f} s; extrapolated linearly to the whole "
+              f"step: folds x {f_scale:.1f} (sum of N_r S_r over this request's, times {w.L} layers), evict x "
+              f"{e_scale:.1f} (sum of S_r over this request's, times {w.L} layers) = {step_s:.0f} s")
+    return {"value": round(nbytes / step_s / 1e9, 5), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": sample, "runs": runs, "extrapolated": True, "step_s": round(step_s, 1),
+            **cpu_info()}
+
+
+def cpu_clustered(w, nbytes, runs=3):
+    """CPU baseline of the 131k compaction: the oracle's reference-style compact (plan_compaction,
+    apply_copies on the layer's K and V planes, allocator; paged.py:125-139) on one layer,
+    `runs` times, median; the plan is per sequence, so the step is extrapolated as the plan's
+    time plus the moves' time times L layers (labelled)."""
+    import torch
+    from oracle import reference as ref
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    kv_l = w.kv0[0].cpu()
+    keep = w.keep_host.numpy()
+    table = list(w.host0[1][0])
+    plans, compacts = [], []
+    for _ in range(runs):
+        model = ref.PagedCacheModel(w.nb, w.bs, w.hkv, w.d, 1)
+        model.kv = kv_l.unsqueeze(0).view(torch.int16).numpy().copy()
+        model.free, model.tables, model.seq_used = list(w.host0[0]), {0: list(table)}, {0: w.S}
+        t0 = time.perf_counter()
+        ref.plan_compaction(keep, w.S, table, w.bs)
+        t1 = time.perf_counter()
+        model.compact(0, keep)
+        t2 = time.perf_counter()
+        plans.append(t1 - t0)
+        compacts.append(t2 - t1)
+        del model
+    p_med, c_med = statistics.median(plans), statistics.median(compacts)
+    moves = max(c_med - p_med, 0.0)
+    step_s = p_med + moves * w.L
+    sample = (f"compact of one layer ({w.S} tokens, K and V planes), {runs} runs, median {c_med:.2f} s (runs "
+              f"{', '.join(f'{x:.2f}' for x in compacts)} s), of which the plan {p_med:.2f} s; extrapolated "
+              f"linearly: plan + moves x {w.L} layers = {step_s:.1f} s")
+    return {"value": round(nbytes / step_s / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": sample, "runs": runs, "extrapolated": True, "step_s": round(step_s, 2),
+            **cpu_info()}
 
 
 def cpu_summary(times, nbytes, what, layers=1):
@@ -1395,10 +1484,10 @@ def main(argv=None):
         configs["cfg1"] = run_cfg1(args, dev, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
         log("config 3: 36 layers x 8 ragged sequences, one evict_batch")
-        configs["cfg3"] = run_cfg3(args, dev)
+        configs["cfg3"] = run_cfg3(args, dev, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
         log("config 4: 131072 tokens x 36 layers, clustered keep, compaction")
-        configs["cfg4"] = run_cfg4(args, dev)
+        configs["cfg4"] = run_cfg4(args, dev, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
     ora = None
     if args.ora_short > 0 and args.layers == 36:

@@ -25,8 +25,10 @@ step), checks of the step's results and, under `configs`, the other workloads of
   cfg1 : one fp16 layer of 2048 tokens, 64 action queries, keep 25% + 4 sinks (with its CPU
          baseline in full)
   cfg3 : 36 layers x 8 ragged sequences of 8k-64k tokens, 64-256 action queries, keep 5-30%
-         + 4 sinks, one shared shuffled pool; one cal_attn + one evict_batch
-  cfg4 : 131072 tokens x 36 layers, keep mask of clustered runs, compaction only
+         + 4 sinks, one shared shuffled pool; one cal_attn + one evict_batch (CPU baseline:
+         one layer of one request, extrapolated and labelled so)
+  cfg4 : 131072 tokens x 36 layers, keep mask of clustered runs, compaction only (CPU
+         baseline: one layer's planes, extrapolated and labelled so)
 each with its step time, algorithmic bytes and flops, GB/s, its floor and checks against the
 oracle.  The agent loop (`ora`) runs all 50 rounds of its schedule.
 """

@@ -278,10 +278,20 @@ __global__ void __launch_bounds__(LT) lrfu_update_kernel(LrfuArgs a) {
       const uint32_t ties = cnt[b3];
       uint32_t need = ties;
       {
-        u64 run = above3;
-        for (uint32_t j = 1; j <= ties; ++j) {
-          run += qstar;
-          if (fixed_to_f32(run, qinv) >= thr) { need = j; break; }
+        // the running sum with j ties is above3 + j * qstar exactly (integers, and the ties'
+        // sum is part of the total, so no overflow), and its float32 rounding never
+        // decreases with j: a binary search finds the first j that reaches thr in about
+        // log2(ties) steps, where adding one tie at a time took up to S steps when many
+        // scores are equal
+        auto reached = [&](uint32_t j) { return fixed_to_f32(above3 + (u64)j * qstar, qinv) >= thr; };
+        if (ties > 0 && reached(ties)) {
+          uint32_t lo = 1, hi = ties;   // reached(hi) holds
+          while (lo < hi) {
+            const uint32_t mid = lo + (hi - lo) / 2;
+            if (reached(mid)) hi = mid;
+            else lo = mid + 1;
+          }
+          need = lo;
         }
       }
       // ordered scan for the index just past the need-th tie: round j covers tokens

@@ -151,8 +151,9 @@ int actkv_keep_mask(const void *scores, int scores_dtype, int64_t s_sl, int64_t 
  * process ends.  Calls whose actkv_workspace_size(ACTKV_WS_KEEP_MASK, R, max_seq) exceeds
  * it return ACTKV_ERR_WORKSPACE and launch nothing.  The array's address is looked up on
  * the current device at its first call there, so `stream` must belong to the current
- * device.  Every call on a GPU shares that GPU's array (each clears what it accumulates
- * into): calls that may overlap on one GPU race and must be ordered on one stream.
+ * device.  Every call on a GPU shares that GPU's array (each call writes every part it
+ * reads first, so a call never sees the last one's contents): calls that may overlap on one
+ * GPU race and must be ordered on one stream.
  */
 #define ACTKV_KEEP_MASK_SCRATCH_BYTES ((size_t)8 << 20)
 int actkv_keep_mask_noalloc(const void *scores, int scores_dtype, int64_t s_sl, int64_t s_sr,
@@ -163,10 +164,11 @@ int actkv_keep_mask_noalloc(const void *scores, int scores_dtype, int64_t s_sl, 
                             int block_size, int max_seq, void *stream);
 
 /*
- * actkv_pack_keep -- bool keep mask [R, >=S] -> packed bits (LSB-first),
- * zero beyond seq_used[r] up to a whole number of blocks, plus the popcount
- * of each request's mask in kept_out[r] (optional).  Support for
- * actkv_compact when the caller holds a bool mask (actkv/paged.py:125-132).
+ * actkv_pack_keep -- keep mask bytes [R, >=S] (a nonzero byte is a kept token, as a
+ * bool mask's 1) -> packed bits (LSB-first), zero beyond seq_used[r] up to a whole
+ * number of blocks, plus the popcount of each request's mask in kept_out[r]
+ * (optional).  Support for actkv_compact when the caller holds a bool mask
+ * (actkv/paged.py:125-132).
  */
 int actkv_pack_keep(const uint8_t *keep, int64_t keep_sr, int R, const int32_t *seq_used,
                     int block_size, uint32_t *keep_bits, int64_t bits_sr,

@@ -476,6 +476,46 @@ def test_action_scores_heads_per_workgroup_with_strided_heads(hq, hkv, n_q, half
     assert torch.equal(n_k.cpu(), n_o)
 
 
+@pytest.mark.parametrize("hq,hkv,n_q,dtype", [
+    (32, 8, 16, torch.bfloat16),    # 64 rows: 8 KV heads per workgroup
+    (32, 8, 32, torch.float16),     # 128 rows: 4 KV heads per workgroup
+    (6, 3, 40, torch.bfloat16),     # 80 rows over 3 KV heads: one head, 2 row groups
+    (32, 8, 60, torch.bfloat16),    # 240 rows: K-slice kernel
+    (32, 8, 100, torch.bfloat16),   # 400 rows: query tile in registers, 8 row groups
+])
+def test_action_scores_ragged_lengths_in_a_padded_table(hq, hkv, n_q, dtype):
+    """Requests of very different lengths in a block table padded well past the longest: the
+    launch is sized for the table, so most of a short request's token ranges are empty and
+    each pair takes its ranges in rotated order.  Every token below seq_used is scored as the
+    oracle scores it; every column past it (whose padded entries name a valid block) is left
+    as it was."""
+    lens = [2900, 45, 1333, 700]
+    bs, d = 16, 128
+    cache = _filled_cache(lens, bs=bs, hkv=hkv, d=d, dtype=dtype, seed=31)
+    reqs = list(range(len(lens)))
+    bt0, seq = cache.block_table(reqs), cache.seq_tensor(reqs)
+    pad = 150
+    bt = torch.zeros(len(reqs), bt0.shape[1] + pad, dtype=torch.int32, device="cuda")
+    bt[:, :bt0.shape[1]] = bt0
+    width = bt.shape[1] * bs
+    g = torch.Generator().manual_seed(32)
+    q = torch.randn(len(reqs), n_q, hq, d, generator=g).to(dtype)
+    kv0 = cache.kv[0].cpu()
+    tables = [cache.tables[r] for r in reqs]
+    lse = torch.stack([ref.decode_lse(q[:, n], kv0, tables, lens) for n in range(n_q)], 1)
+    out0 = torch.rand(len(reqs), hkv, width, generator=g)
+    n0 = torch.tensor([0, 2, 5, 1], dtype=torch.int32)
+    out_k, n_k = out0.cuda(), n0.cuda()
+    action_scores(q.cuda(), cache.kv[0], bt, seq, lse.cuda(), out_k, n_k)
+    out_o, n_o = out0.clone(), n0.clone()
+    ref.action_scores_nfold(q, kv0, tables, lens, lse, out_o, n_o)
+    got = out_k.cpu()
+    for r, s in enumerate(lens):
+        torch.testing.assert_close(got[r][:, :s], out_o[r][:, :s], rtol=1e-3, atol=1e-6)
+        assert torch.equal(got[r][:, s:], out0[r][:, s:])
+    assert torch.equal(n_k.cpu(), n_o)
+
+
 def test_action_scores_every_layer_in_one_launch():
     """kv [L, 2, ...] with q [L, R, N, Hq, D]: each layer scored against its own K (extension)."""
     lens = [300, 77]

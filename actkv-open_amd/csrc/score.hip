@@ -487,10 +487,10 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
   // the XCD, which spreads the empty and partial ones over the dispatch positions.
   // In plain order range c always sits at position c mod 4 of the XCD's sequence,
   // and with 8 ranges per pair the positions holding ranges 0 and 4 then carry
-  // most of the work (config 3's lengths: 9.29 ms plain, 8.65 ms rotated; uniform
-  // lengths in a table padded to 8 ranges: 10.9 ms plain, 9.0 ms rotated).  One
-  // request keeps the plain order (36 x 32768 tokens: 1.044 ms plain, 1.061 ms
-  // rotated).
+  // most of the work (36 layers x 8 requests of 13103-58038 tokens: 9.29 ms plain,
+  // 8.65 ms rotated; uniform lengths in a table padded to 8 ranges: 10.9 ms plain,
+  // 9.0 ms rotated).  One request keeps the plain order (36 x 32768 tokens:
+  // 1.044 ms plain, 1.061 ms rotated).
   const int bid = blockIdx.x;
   const int xcd = bid & 7, jj = bid >> 3;
   const int p = (jj / cpp) * 8 + xcd;

@@ -769,7 +769,7 @@ def run_cfg1(args, dev, cpu=True):
            "bound": "hbm", "floor_us": round(floor, 2), "frac_of_floor": round(floor / m["step_us"], 4),
            "checks": checks}
     if cpu:
-        res["cpu_baseline"] = cpu_summary(cpu_runs(w, 3), nbytes, "the whole case (config 1)")
+        res["cpu_baseline"] = cpu_summary(cpu_runs(w, 3), nbytes, "the whole case (one fp16 layer, 2048 tokens, 64 action queries)")
     del w
     return res
 
@@ -1482,13 +1482,13 @@ def main(argv=None):
     configs = None
     if not args.no_configs:
         configs = {}
-        log("config 1: one fp16 layer of 2048 tokens, 64 action queries")
+        log("leg cfg1: one fp16 layer of 2048 tokens, 64 action queries")
         configs["cfg1"] = run_cfg1(args, dev, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
-        log("config 3: 36 layers x 8 ragged sequences, one evict_batch")
+        log("leg cfg3: 36 layers x 8 ragged sequences, one evict_batch")
         configs["cfg3"] = run_cfg3(args, dev, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
-        log("config 4: 131072 tokens x 36 layers, clustered keep, compaction")
+        log("leg cfg4: 131072 tokens x 36 layers, clustered keep, compaction")
         configs["cfg4"] = run_cfg4(args, dev, cpu=not args.no_cpu)
         torch.cuda.empty_cache()
     ora = None

@@ -516,6 +516,45 @@ def test_action_scores_ragged_lengths_in_a_padded_table(hq, hkv, n_q, dtype):
     assert torch.equal(n_k.cpu(), n_o)
 
 
+@pytest.mark.parametrize("dtype,hq,hkv,n_q,causal,partial", [
+    (torch.bfloat16, 64, 8, 5, False, False),    # 40 rows: 2 row groups
+    (torch.bfloat16, 64, 8, 24, True, True),     # 192 rows: 4 row groups, causal, partial counts
+    (torch.float16, 16, 2, 64, False, True),     # 512 rows: 8 row groups, fragment layout
+    (torch.bfloat16, 64, 8, 64, True, False),    # 512 rows, causal
+    (torch.bfloat16, 16, 2, 100, True, True),    # 800 rows: two launches (64 + 36 queries)
+    (torch.float16, 64, 8, 16, True, False),     # 128 rows, causal
+])
+def test_action_scores_groups_of_eight_heads(dtype, hq, hkv, n_q, causal, partial):
+    """G = 8 (64 query heads over 8 KV heads, as Qwen3-32B): a query's eight heads span both
+    halves of a wave, and the max over them is taken across the halves before the exp."""
+    lens = [700, 90, 1500]
+    d, bs = 128, 16
+    cache = _filled_cache(lens, bs=bs, hkv=hkv, d=d, dtype=dtype, seed=41)
+    reqs = list(range(len(lens)))
+    bt, seq = cache.block_table(reqs), cache.seq_tensor(reqs)
+    width = bt.shape[1] * bs
+    g = torch.Generator().manual_seed(42)
+    q = torch.randn(len(reqs), n_q, hq, d, generator=g).to(dtype)
+    kv0 = cache.kv[0].cpu()
+    tables = [cache.tables[r] for r in reqs]
+    lse = torch.stack([ref.decode_lse(q[:, n], kv0, tables, lens) for n in range(n_q)], 1)
+    n_valid = torch.tensor([n_q, min(3, n_q), max(n_q - 7, 0)], dtype=torch.int32) if partial else None
+    kv_len = None
+    if causal:
+        kv_len = torch.stack([torch.randint(1, s + 1, (n_q,), generator=g) for s in lens]).to(torch.int32)
+        kv_len[0, 0] = lens[0]
+    out0 = torch.rand(len(reqs), hkv, width, generator=g)
+    n0 = torch.tensor([1, 0, 4], dtype=torch.int32)
+    out_k, n_k = out0.cuda(), n0.cuda()
+    action_scores(q.cuda(), cache.kv[0], bt, seq, lse.cuda(), out_k, n_k,
+                  n_valid=None if n_valid is None else n_valid.cuda(),
+                  kv_len=None if kv_len is None else kv_len.cuda())
+    out_o, n_o = out0.clone(), n0.clone()
+    ref.action_scores_nfold(q, kv0, tables, lens, lse, out_o, n_o, n_valid=n_valid, kv_len=kv_len)
+    torch.testing.assert_close(out_k.cpu(), out_o, rtol=1e-3, atol=1e-6)
+    assert torch.equal(n_k.cpu(), n_o)
+
+
 def test_action_scores_every_layer_in_one_launch():
     """kv [L, 2, ...] with q [L, R, N, Hq, D]: each layer scored against its own K (extension)."""
     lens = [300, 77]

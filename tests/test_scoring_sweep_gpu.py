@@ -64,3 +64,49 @@ def test_random_shapes_match_the_oracle(seed):
     ref.action_scores_nfold(q, kv0, tables, lens, lse, out_o, n_o, n_valid=n_valid, kv_len=kv_len)
     torch.testing.assert_close(out_k.cpu(), out_o, rtol=1e-3, atol=1e-6)
     assert torch.equal(n_k.cpu(), n_o)
+
+
+def _case8(seed):
+    rnd = random.Random(5000 + seed)
+    n_req = rnd.randint(1, 4)
+    return dict(lens=[rnd.choice([rnd.randint(1, 300), rnd.randint(300, 4000)]) for _ in range(n_req)],
+                gqa=rnd.choice([(64, 8), (16, 2), (8, 1)]), n_q=rnd.choice([1, rnd.randint(2, 16), rnd.randint(17, 90)]),
+                dtype=rnd.choice([torch.bfloat16, torch.float16]), bs=rnd.choice([16, 32, 64]),
+                causal=rnd.random() < 0.5, partial=rnd.random() < 0.3)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_shapes_with_groups_of_eight_match_the_oracle(seed):
+    """The same sweep for G = 8 (64/8, 16/2, 8/1 query/KV heads): more than 64 queries run as
+    several launches."""
+    c = _case8(seed)
+    lens, (hq, hkv), n_q, dtype, bs = c["lens"], c["gqa"], c["n_q"], c["dtype"], c["bs"]
+    print(f"case {seed}: {c}", flush=True)
+    g = torch.Generator().manual_seed(100 + seed)
+    nb = sum(math.ceil(n / bs) for n in lens) + 3
+    cache = PagedKVCache(nb, bs, hkv, 128, n_layers=1, dtype=dtype, device="cuda")
+    cache.free = torch.randperm(nb, generator=g).tolist()
+    for r, n in enumerate(lens):
+        cache.append(r, torch.randn(1, n, hkv, 128, generator=g).to(dtype).cuda(),
+                     torch.randn(1, n, hkv, 128, generator=g).to(dtype).cuda())
+    reqs = list(range(len(lens)))
+    bt, seq = cache.block_table(reqs), cache.seq_tensor(reqs)
+    width = bt.shape[1] * bs
+    q = torch.randn(len(reqs), n_q, hq, 128, generator=g).to(dtype)
+    kv0 = cache.kv[0].cpu()
+    tables = [cache.tables[r] for r in reqs]
+    lse = torch.stack([ref.decode_lse(q[:, n], kv0, tables, lens) for n in range(n_q)], 1)
+    kv_len = (torch.stack([torch.randint(1, s + 1, (n_q,), generator=g) for s in lens]).to(torch.int32)
+              if c["causal"] else None)
+    n_valid = (torch.tensor([random.Random(seed + r).randint(0, n_q) for r in reqs], dtype=torch.int32)
+               if c["partial"] else None)
+    out0 = torch.rand(len(reqs), hkv, width, generator=g)
+    n0 = torch.randint(0, 9, (len(reqs),), generator=g).to(torch.int32)
+    out_k, n_k = out0.cuda(), n0.cuda()
+    action_scores(q.cuda(), cache.kv[0], bt, seq, lse.cuda(), out_k, n_k,
+                  n_valid=None if n_valid is None else n_valid.cuda(),
+                  kv_len=None if kv_len is None else kv_len.cuda())
+    out_o, n_o = out0.clone(), n0.clone()
+    ref.action_scores_nfold(q, kv0, tables, lens, lse, out_o, n_o, n_valid=n_valid, kv_len=kv_len)
+    torch.testing.assert_close(out_k.cpu(), out_o, rtol=1e-3, atol=1e-6)
+    assert torch.equal(n_k.cpu(), n_o)

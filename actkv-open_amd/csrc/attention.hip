@@ -10,7 +10,7 @@
 // out and lse are float32.  A row that sees no token gets lse = -inf, out = 0
 // (torch's logsumexp and softmax-einsum over an empty set).
 //
-// MFMA path (bf16/fp16, head_dim 128, GQA group 1/2/4, more than one 32-row tile of
+// MFMA path (bf16/fp16, head_dim 128, GQA group 1/2/4/8, more than one 32-row tile of
 // query rows per pair): FlashAttention-style,
 // one workgroup per (layer, request, KV head, group of NW row tiles), NW waves,
 // each owning one 32-row tile of the pair's query rows (n, g) and streaming all
@@ -1084,15 +1084,17 @@ extern "C" int actkv_paged_attention(
                       kv_sl % 8 == 0 && kv_sv % 8 == 0 && kv_sb % 8 == 0 && kv_ss % 8 == 0 &&
                       kv_sh % 8 == 0 && o_sl % 4 == 0 && o_sr % 4 == 0 && o_sn % 4 == 0 && o_sh % 4 == 0;
   const bool mfma_ok = q_dtype == kv_dtype && (kv_dtype == ACTKV_BF16 || kv_dtype == ACTKV_F16) &&
-                       D == 128 && (G == 1 || G == 2 || G == 4) && vec_ok && bs_shift >= 0;
+                       D == 128 && (G == 1 || G == 2 || G == 4 || G == 8) && vec_ok && bs_shift >= 0;
   if (mfma_ok) {
     void *ws = workspace;
     const size_t wb = workspace_bytes;
     if (kv_dtype == ACTKV_BF16)
-      return G == 4 ? launch_attn_mfma<__bf16, bf16x8, 4>(a, bs_shift, ws, wb, st)
+      return G == 8 ? launch_attn_mfma<__bf16, bf16x8, 8>(a, bs_shift, ws, wb, st)
+           : G == 4 ? launch_attn_mfma<__bf16, bf16x8, 4>(a, bs_shift, ws, wb, st)
            : G == 2 ? launch_attn_mfma<__bf16, bf16x8, 2>(a, bs_shift, ws, wb, st)
                     : launch_attn_mfma<__bf16, bf16x8, 1>(a, bs_shift, ws, wb, st);
-    return G == 4 ? launch_attn_mfma<_Float16, f16x8, 4>(a, bs_shift, ws, wb, st)
+    return G == 8 ? launch_attn_mfma<_Float16, f16x8, 8>(a, bs_shift, ws, wb, st)
+         : G == 4 ? launch_attn_mfma<_Float16, f16x8, 4>(a, bs_shift, ws, wb, st)
          : G == 2 ? launch_attn_mfma<_Float16, f16x8, 2>(a, bs_shift, ws, wb, st)
                   : launch_attn_mfma<_Float16, f16x8, 1>(a, bs_shift, ws, wb, st);
   }
@@ -1107,7 +1109,7 @@ extern "C" size_t actkv_paged_attention_workspace_size(int L, int R, int N, int 
                                                        int max_blocks, int block_size) {
   if (L < 1 || R < 1 || N < 1 || Hkv < 1 || Hq % Hkv != 0 || max_blocks < 1 || block_size < 1) return 0;
   const int G = Hq / Hkv;
-  if (D != 128 || !(G == 1 || G == 2 || G == 4)) return 0;  // the float32 path does not split
+  if (D != 128 || !(G == 1 || G == 2 || G == 4 || G == 8)) return 0;  // the float32 path does not split
   if ((int64_t)max_blocks * block_size > 0x7fffffffLL) return 0;
   const int pairs = L * R * Hkv;
   return attn_ws_bytes(pairs, attn_split(pairs, N, G, max_blocks * block_size, device_cus()));

@@ -57,6 +57,10 @@ def _atol(dtype):
     ([3000, 47], 32, 8, 8, torch.bfloat16, True),        # 32 rows: the one-tile decode kernel, causal
     ([2100], 16, 8, 5, torch.float16, True),             # GQA 2, 10 rows, fp16, causal
     ([5000, 1], 8, 8, 3, torch.bfloat16, False),         # GQA 1, 3 rows, a one-token request
+    ([1800, 333], 64, 8, 48, torch.bfloat16, True),      # GQA 8, 384 rows, causal
+    ([2500], 16, 2, 100, torch.float16, False),          # GQA 8, 800 rows: four groups of 8 tiles
+    ([700, 4100], 64, 8, 1, torch.bfloat16, False),      # GQA 8 decode: one tile, 8 real rows
+    ([3000, 47], 64, 8, 4, torch.bfloat16, True),        # GQA 8, 32 rows: the one-tile decode kernel
 ])
 def test_matrix_core_path_matches_the_oracle(lens, hq, hkv, n_q, dtype, causal):
     cache = _cache(lens, hkv=hkv, dtype=dtype, seed=len(lens) * 100 + n_q)

@@ -64,3 +64,42 @@ def test_random_shapes_match_the_oracle(seed):
         kv_len=None if kv_len is None else kv_len.tolist(), n_valid=None if n_valid is None else n_valid.tolist())
     torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
     torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=2e-4)   # P as hi + lo terms
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_shapes_with_groups_of_eight_match_the_oracle(seed):
+    """The same sweep for G = 8 (Hq/Hkv 64/8, 16/2, 8/1): decode tiles of up to 4 queries and
+    multi-tile row groups."""
+    rnd = random.Random(9000 + seed)
+    n_req = rnd.randint(1, 4)
+    lens = [rnd.choice([0, rnd.randint(1, 200), rnd.randint(200, 5000)]) for _ in range(n_req)]
+    if max(lens) == 0:
+        lens[0] = rnd.randint(1, 3000)
+    hq, hkv = rnd.choice([(64, 8), (16, 2), (8, 1)])
+    n_q = rnd.choice([1, rnd.randint(2, 4), rnd.randint(5, 60)])
+    dtype, bs = rnd.choice([torch.bfloat16, torch.float16]), rnd.choice([16, 32, 64])
+    causal, partial = rnd.random() < 0.5, rnd.random() < 0.3
+    print(f"case {seed}: lens {lens} hq {hq} hkv {hkv} n_q {n_q} {dtype} bs {bs} causal {causal} "
+          f"partial {partial}", flush=True)
+    g = torch.Generator().manual_seed(7000 + seed)
+    nb = sum(math.ceil(n / bs) for n in lens) + 3
+    cache = PagedKVCache(nb, bs, hkv, 128, n_layers=1, dtype=dtype, device="cuda")
+    cache.free = torch.randperm(nb, generator=g).tolist()
+    for r, n in enumerate(lens):
+        cache.append(r, torch.randn(1, n, hkv, 128, generator=g).to(dtype).cuda(),
+                     torch.randn(1, n, hkv, 128, generator=g).to(dtype).cuda())
+    reqs = list(range(len(lens)))
+    seq, bt = cache._device_tables(reqs)
+    q = torch.randn(len(lens), n_q, hq, 128, generator=g).to(dtype)
+    kv_len = (torch.stack([torch.randint(0, S + 4, (n_q,), generator=g) for S in lens]).to(torch.int32)
+              if causal else None)
+    n_valid = (torch.tensor([random.Random(seed + r).randint(0, n_q) for r in reqs], dtype=torch.int32)
+               if partial else None)
+    out, lse = paged_decode_attention(q.cuda(), cache.kv[0], bt, seq,
+                                      kv_len=None if kv_len is None else kv_len.cuda(),
+                                      n_valid=None if n_valid is None else n_valid.cuda())
+    want_out, want_lse = ref.paged_attention(
+        q.float(), cache.kv[0].cpu().float(), [cache.tables[r] for r in reqs], [cache.seq_used[r] for r in reqs],
+        kv_len=None if kv_len is None else kv_len.tolist(), n_valid=None if n_valid is None else n_valid.tolist())
+    torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
+    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=2e-4)

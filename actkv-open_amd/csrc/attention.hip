@@ -10,7 +10,7 @@
 // out and lse are float32.  A row that sees no token gets lse = -inf, out = 0
 // (torch's logsumexp and softmax-einsum over an empty set).
 //
-// MFMA path (bf16/fp16, head_dim 128, GQA group 1/2/4/8, more than one 32-row tile of
+// MFMA path (bf16/fp16, head_dim 128, any GQA group, more than one 32-row tile of
 // query rows per pair): FlashAttention-style,
 // one workgroup per (layer, request, KV head, group of NW row tiles), NW waves,
 // each owning one 32-row tile of the pair's query rows (n, g) and streaming all
@@ -180,9 +180,10 @@ __device__ __forceinline__ int dswz(int t) { return 4 * (t & 3) + ((t >> 2) & 3)
 
 typedef short dv4s __attribute__((ext_vector_type(4)));
 
-template <typename T, typename V8, int G, bool CAUSAL>
+template <typename T, typename V8, bool CAUSAL>
 __global__ void __launch_bounds__(DW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
+  const int G = a.G;   // query heads per KV head: rows (n, g) of a tile are independent
   __shared__ __attribute__((aligned(16))) unsigned char reg_lds[DW][DREG];
   __shared__ float mrg_ml[DW][32][2];
   __shared__ int wg_lim;
@@ -496,10 +497,11 @@ __device__ __forceinline__ void buf_lds16(ri32x4 rsrc, unsigned voff, unsigned l
                : "memory");
 }
 
-template <typename T, typename V8, int G, int NW, int RT, bool CAUSAL>
+template <typename T, typename V8, int NW, int RT, bool CAUSAL>
 __global__ void __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(RT >= 2 ? 1 : (NW >= 4 ? 2 : 1), RT >= 2 ? 1 : 2)))
 attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
+  const int G = a.G;   // query heads per KV head: rows (n, g) of a tile are independent
   using SH = RingShape<NW * RT>;
   constexpr int ST = SH::ST, NSTG = SH::NSTG, TBLW = SH::TBLW;
   constexpr int PER = 2 * SH::IPP / NW;  // load instructions per wave per stage
@@ -976,7 +978,7 @@ static size_t attn_ws_bytes(int pairs, const AttnSplit &sp) {
   return (size_t)pairs * sp.rows_pad * sp.nchunk * (128 + 2) * sizeof(float);
 }
 
-template <typename T, typename V8, int G>
+template <typename T, typename V8>
 static int launch_attn_mfma(AttnArgs a, int bs_shift, void *ws, size_t ws_bytes, hipStream_t st) {
   const int pairs = a.L * a.R * a.Hkv;
   const int rtiles = (a.N * a.G + 31) / 32;
@@ -994,18 +996,18 @@ static int launch_attn_mfma(AttnArgs a, int bs_shift, void *ws, size_t ws_bytes,
   if (rtiles == 1) {
     const int grid = pairs * sp.nchunk;
     if (causal)
-      hipLaunchKernelGGL((attn_decode_kernel<T, V8, G, true>), dim3(grid), dim3(DW * 64), 0, st, a, pairs, bs_shift);
+      hipLaunchKernelGGL((attn_decode_kernel<T, V8, true>), dim3(grid), dim3(DW * 64), 0, st, a, pairs, bs_shift);
     else
-      hipLaunchKernelGGL((attn_decode_kernel<T, V8, G, false>), dim3(grid), dim3(DW * 64), 0, st, a, pairs, bs_shift);
+      hipLaunchKernelGGL((attn_decode_kernel<T, V8, false>), dim3(grid), dim3(DW * 64), 0, st, a, pairs, bs_shift);
   } else {
 #define ACTKV_ATTN(NWV, RTV)                                                                       \
   do {                                                                                             \
     const int grid = ((pairs + 7) / 8) * 8 * sp.ngroups * sp.nchunk;                               \
     if (causal)                                                                                    \
-      hipLaunchKernelGGL((attn_ring_kernel<T, V8, G, NWV, RTV, true>), dim3(grid), dim3(NWV * 64), \
+      hipLaunchKernelGGL((attn_ring_kernel<T, V8, NWV, RTV, true>), dim3(grid), dim3(NWV * 64), \
                          0, st, a, pairs, sp.ngroups, bs_shift);                                   \
     else                                                                                           \
-      hipLaunchKernelGGL((attn_ring_kernel<T, V8, G, NWV, RTV, false>), dim3(grid), dim3(NWV * 64),\
+      hipLaunchKernelGGL((attn_ring_kernel<T, V8, NWV, RTV, false>), dim3(grid), dim3(NWV * 64),\
                          0, st, a, pairs, sp.ngroups, bs_shift);                                   \
   } while (0)
   const RingCfg cfg = ring_cfg(rtiles);
@@ -1084,19 +1086,13 @@ extern "C" int actkv_paged_attention(
                       kv_sl % 8 == 0 && kv_sv % 8 == 0 && kv_sb % 8 == 0 && kv_ss % 8 == 0 &&
                       kv_sh % 8 == 0 && o_sl % 4 == 0 && o_sr % 4 == 0 && o_sn % 4 == 0 && o_sh % 4 == 0;
   const bool mfma_ok = q_dtype == kv_dtype && (kv_dtype == ACTKV_BF16 || kv_dtype == ACTKV_F16) &&
-                       D == 128 && (G == 1 || G == 2 || G == 4 || G == 8) && vec_ok && bs_shift >= 0;
+                       D == 128 && G >= 1 && vec_ok && bs_shift >= 0;
   if (mfma_ok) {
     void *ws = workspace;
     const size_t wb = workspace_bytes;
     if (kv_dtype == ACTKV_BF16)
-      return G == 8 ? launch_attn_mfma<__bf16, bf16x8, 8>(a, bs_shift, ws, wb, st)
-           : G == 4 ? launch_attn_mfma<__bf16, bf16x8, 4>(a, bs_shift, ws, wb, st)
-           : G == 2 ? launch_attn_mfma<__bf16, bf16x8, 2>(a, bs_shift, ws, wb, st)
-                    : launch_attn_mfma<__bf16, bf16x8, 1>(a, bs_shift, ws, wb, st);
-    return G == 8 ? launch_attn_mfma<_Float16, f16x8, 8>(a, bs_shift, ws, wb, st)
-         : G == 4 ? launch_attn_mfma<_Float16, f16x8, 4>(a, bs_shift, ws, wb, st)
-         : G == 2 ? launch_attn_mfma<_Float16, f16x8, 2>(a, bs_shift, ws, wb, st)
-                  : launch_attn_mfma<_Float16, f16x8, 1>(a, bs_shift, ws, wb, st);
+      return launch_attn_mfma<__bf16, bf16x8>(a, bs_shift, ws, wb, st);
+    return launch_attn_mfma<_Float16, f16x8>(a, bs_shift, ws, wb, st);
   }
   switch (q_dtype) {
     case ACTKV_F32: return dispatch_attn_generic<float>(a, kv_dtype, st);
@@ -1109,7 +1105,7 @@ extern "C" size_t actkv_paged_attention_workspace_size(int L, int R, int N, int 
                                                        int max_blocks, int block_size) {
   if (L < 1 || R < 1 || N < 1 || Hkv < 1 || Hq % Hkv != 0 || max_blocks < 1 || block_size < 1) return 0;
   const int G = Hq / Hkv;
-  if (D != 128 || !(G == 1 || G == 2 || G == 4 || G == 8)) return 0;  // the float32 path does not split
+  if (D != 128 || G < 1) return 0;  // the float32 path does not split
   if ((int64_t)max_blocks * block_size > 0x7fffffffLL) return 0;
   const int pairs = L * R * Hkv;
   return attn_ws_bytes(pairs, attn_split(pairs, N, G, max_blocks * block_size, device_cus()));

@@ -61,6 +61,11 @@ def _atol(dtype):
     ([2500], 16, 2, 100, torch.float16, False),          # GQA 8, 800 rows: four groups of 8 tiles
     ([700, 4100], 64, 8, 1, torch.bfloat16, False),      # GQA 8 decode: one tile, 8 real rows
     ([3000, 47], 64, 8, 4, torch.bfloat16, True),        # GQA 8, 32 rows: the one-tile decode kernel
+    ([1800, 333], 24, 8, 30, torch.bfloat16, True),      # GQA 3, 90 rows
+    ([2500], 40, 8, 20, torch.float16, False),           # GQA 5, 100 rows
+    ([700], 48, 8, 60, torch.bfloat16, True),            # GQA 6, 360 rows
+    ([1200, 900], 28, 4, 5, torch.bfloat16, True),       # GQA 7, 35 rows (two tiles)
+    ([3000, 47], 28, 4, 4, torch.float16, True),         # GQA 7, 28 rows: the decode kernel
 ])
 def test_matrix_core_path_matches_the_oracle(lens, hq, hkv, n_q, dtype, causal):
     cache = _cache(lens, hkv=hkv, dtype=dtype, seed=len(lens) * 100 + n_q)

@@ -66,16 +66,16 @@ def test_random_shapes_match_the_oracle(seed):
     torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=2e-4)   # P as hi + lo terms
 
 
-@pytest.mark.parametrize("seed", range(16))
-def test_random_shapes_with_groups_of_eight_match_the_oracle(seed):
-    """The same sweep for G = 8 (Hq/Hkv 64/8, 16/2, 8/1): decode tiles of up to 4 queries and
-    multi-tile row groups."""
+@pytest.mark.parametrize("seed", range(24))
+def test_random_shapes_with_other_groups_match_the_oracle(seed):
+    """The same sweep for groups of 3 and 5 to 8 query heads per KV head (Hq/Hkv 64/8, 16/2,
+    8/1, 24/8, 40/8, 48/8, 28/4): decode tiles and multi-tile row groups."""
     rnd = random.Random(9000 + seed)
     n_req = rnd.randint(1, 4)
     lens = [rnd.choice([0, rnd.randint(1, 200), rnd.randint(200, 5000)]) for _ in range(n_req)]
     if max(lens) == 0:
         lens[0] = rnd.randint(1, 3000)
-    hq, hkv = rnd.choice([(64, 8), (16, 2), (8, 1)])
+    hq, hkv = rnd.choice([(64, 8), (16, 2), (8, 1), (24, 8), (40, 8), (48, 8), (28, 4)])
     n_q = rnd.choice([1, rnd.randint(2, 4), rnd.randint(5, 60)])
     dtype, bs = rnd.choice([torch.bfloat16, torch.float16]), rnd.choice([16, 32, 64])
     causal, partial = rnd.random() < 0.5, rnd.random() < 0.3

@@ -19,9 +19,10 @@
 //   out[t]      = (out[t] * n_seen + sum[t]) / (n_seen + nq) (== nq reference folds)
 //
 // Groups of 8 heads run on the query-register kernel only: a query's eight rows
-// span both halves of a wave, and their max is taken across the halves.
-// The generic kernel covers every other shape/dtype (fp32 caches, head_dim not
-// 128, group sizes other than 1/2/4/8) and follows the reference fold order
+// span both halves of a wave, and their max is taken across the halves.  Groups of
+// 3 and 5-7 take that kernel too, laid out as 4 and 8 rows per query (padding rows
+// load no query and start at -inf).  The generic kernel covers every other
+// shape/dtype (fp32 caches, head_dim not 128, groups above 8) and follows the reference fold order
 // exactly: for each query in turn, out += (p - out) / (n_seen + n + 1).
 #include "common.h"
 
@@ -534,16 +535,21 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
     const T *qbase = (const T *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr;
     const float *lbase = a.lse + (int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr;
     const float inv_scale = 1.0f / a.scale;
+    // rows are laid out by G, the group size padded to 1, 2, 4 or 8; a.G <= G is the
+    // model's own (query head h * a.G + g): rows with g >= a.G are padding, a zero query
+    // with seed -inf, so they never win the max over the group
+    const int GR = a.G;
     // unconditional loads at clamped rows: no branch serialises them
 #pragma unroll
     for (int jt = 0; jt < 2; ++jt) {
       const int row = rgl * 64 + jt * 32 + lcol;
       const int n = row / G, g = row % G;
-      const T *qp = qbase + (int64_t)(a.qc0 + min(n, nq - 1)) * a.q_sn + (int64_t)(h * G + g) * a.q_sh + lh * 8;
+      const T *qp = qbase + (int64_t)(a.qc0 + min(n, nq - 1)) * a.q_sn + (int64_t)(h * GR + min(g, GR - 1)) * a.q_sh +
+                    lh * 8;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const V8 v = *(const V8 *)(qp + ks * 16);
-        af[jt][ks] = n < nq ? v : (V8)(T)0;
+        af[jt][ks] = n < nq && g < GR ? v : (V8)(T)0;
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -551,8 +557,8 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
         for (int j = 0; j < 4; ++j) {
           const int rw = rgl * 64 + jt * 32 + 8 * i + 4 * lh + j;
           const int nn = rw / G, gg = rw % G;
-          const float v = lbase[(int64_t)(a.qc0 + min(nn, nq - 1)) * a.lse_sn + h * G + gg];
-          seed[jt][4 * i + j] = nn < nq ? -v * inv_scale : -INFINITY;
+          const float v = lbase[(int64_t)(a.qc0 + min(nn, nq - 1)) * a.lse_sn + h * GR + min(gg, GR - 1)];
+          seed[jt][4 * i + j] = nn < nq && gg < GR ? -v * inv_scale : -INFINITY;
         }
         if constexpr (CAUSAL && G == 8) {
           // rows 8 i' .. 8 i' + 7 of the tile are one query (heads 0-3 in lanes 0-31,
@@ -908,8 +914,10 @@ static int launch_mfma(const ScoreArgs &a0, int bs_shift, hipStream_t st) {
     // 3.5-4.4) and above 384 (the matrix cores bound it); the K-slice kernel from 129 to
     // 384 rows (with 2 heads per workgroup, 4 row groups each, or 1 head and 4 row
     // groups, the query-register kernel took 4-10% longer there)
-    // groups of 8 heads run on the query-register kernel alone (one head per workgroup)
-    const bool qreg = G == 8 || choice == MFMA_QREG || (choice == MFMA_AUTO && (rows <= 128 || rows > 384));
+    // groups of 8 heads, and groups padded to 4 or 8 (3, 5, 6, 7), run on the query-register
+    // kernel alone
+    const bool qreg = G == 8 || a0.G != G || choice == MFMA_QREG ||
+                      (choice == MFMA_AUTO && (rows <= 128 || rows > 384));
     if (qreg) {
       // query tile in registers, K shared through LDS; RG row groups of 64 rows over HPV
       // heads per workgroup, chunks of CHV tokens, the first one's set-up costing about
@@ -1039,18 +1047,18 @@ extern "C" int actkv_action_scores(
   for (int sh = 4; sh < 31; ++sh)
     if (block_size == (1 << sh)) bs_shift = sh;
   const bool mfma_ok = q_dtype == kv_dtype && (kv_dtype == ACTKV_BF16 || kv_dtype == ACTKV_F16) &&
-                       D == 128 && (G == 1 || G == 2 || G == 4 || G == 8) && scale > 0.f && vec_ok &&
+                       D == 128 && G >= 1 && G <= 8 && scale > 0.f && vec_ok &&
                        bs_shift >= 0;
   int rc;
   if (mfma_ok) {
     if (kv_dtype == ACTKV_BF16) {
-      rc = G == 8 ? launch_mfma<__bf16, bf16x8, 8>(a, bs_shift, st)
-         : G == 4 ? launch_mfma<__bf16, bf16x8, 4>(a, bs_shift, st)
+      rc = G > 4 ? launch_mfma<__bf16, bf16x8, 8>(a, bs_shift, st)
+         : G > 2 ? launch_mfma<__bf16, bf16x8, 4>(a, bs_shift, st)
          : G == 2 ? launch_mfma<__bf16, bf16x8, 2>(a, bs_shift, st)
                   : launch_mfma<__bf16, bf16x8, 1>(a, bs_shift, st);
     } else {
-      rc = G == 8 ? launch_mfma<_Float16, f16x8, 8>(a, bs_shift, st)
-         : G == 4 ? launch_mfma<_Float16, f16x8, 4>(a, bs_shift, st)
+      rc = G > 4 ? launch_mfma<_Float16, f16x8, 8>(a, bs_shift, st)
+         : G > 2 ? launch_mfma<_Float16, f16x8, 4>(a, bs_shift, st)
          : G == 2 ? launch_mfma<_Float16, f16x8, 2>(a, bs_shift, st)
                   : launch_mfma<_Float16, f16x8, 1>(a, bs_shift, st);
     }

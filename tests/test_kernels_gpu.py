@@ -523,10 +523,17 @@ def test_action_scores_ragged_lengths_in_a_padded_table(hq, hkv, n_q, dtype):
     (torch.bfloat16, 64, 8, 64, True, False),    # 512 rows, causal
     (torch.bfloat16, 16, 2, 100, True, True),    # 800 rows: two launches (64 + 36 queries)
     (torch.float16, 64, 8, 16, True, False),     # 128 rows, causal
+    (torch.bfloat16, 24, 8, 12, True, False),    # G = 3 padded to 4: 48 rows, 8 heads per workgroup
+    (torch.bfloat16, 24, 8, 90, False, True),    # G = 3: 360 rows
+    (torch.float16, 40, 8, 30, True, True),      # G = 5 padded to 8: 240 rows
+    (torch.bfloat16, 48, 8, 70, True, False),    # G = 6: two launches (64 + 6 queries)
+    (torch.bfloat16, 28, 4, 9, False, False),    # G = 7: 72 rows
 ])
 def test_action_scores_groups_of_eight_heads(dtype, hq, hkv, n_q, causal, partial):
     """G = 8 (64 query heads over 8 KV heads, as Qwen3-32B): a query's eight heads span both
-    halves of a wave, and the max over them is taken across the halves before the exp."""
+    halves of a wave, and the max over them is taken across the halves before the exp.  Groups
+    of 3, 5, 6 and 7 are laid out as 4 or 8 rows per query with padding rows that never win
+    the max."""
     lens = [700, 90, 1500]
     d, bs = 128, 16
     cache = _filled_cache(lens, bs=bs, hkv=hkv, d=d, dtype=dtype, seed=41)

@@ -70,15 +70,17 @@ def _case8(seed):
     rnd = random.Random(5000 + seed)
     n_req = rnd.randint(1, 4)
     return dict(lens=[rnd.choice([rnd.randint(1, 300), rnd.randint(300, 4000)]) for _ in range(n_req)],
-                gqa=rnd.choice([(64, 8), (16, 2), (8, 1)]), n_q=rnd.choice([1, rnd.randint(2, 16), rnd.randint(17, 90)]),
+                gqa=rnd.choice([(64, 8), (16, 2), (8, 1), (24, 8), (40, 8), (48, 8), (28, 4)]),
+                n_q=rnd.choice([1, rnd.randint(2, 16), rnd.randint(17, 90)]),
                 dtype=rnd.choice([torch.bfloat16, torch.float16]), bs=rnd.choice([16, 32, 64]),
                 causal=rnd.random() < 0.5, partial=rnd.random() < 0.3)
 
 
-@pytest.mark.parametrize("seed", range(16))
-def test_random_shapes_with_groups_of_eight_match_the_oracle(seed):
-    """The same sweep for G = 8 (64/8, 16/2, 8/1 query/KV heads): more than 64 queries run as
-    several launches."""
+@pytest.mark.parametrize("seed", range(24))
+def test_random_shapes_with_other_groups_match_the_oracle(seed):
+    """The same sweep for groups of 3 and 5 to 8 query heads per KV head (64/8, 16/2, 8/1, 24/8,
+    40/8, 48/8, 28/4): more than 512/G' queries (G' the group padded to 4 or 8) run as several
+    launches."""
     c = _case8(seed)
     lens, (hq, hkv), n_q, dtype, bs = c["lens"], c["gqa"], c["n_q"], c["dtype"], c["bs"]
     print(f"case {seed}: {c}", flush=True)

@@ -22,8 +22,9 @@
 // span both halves of a wave, and their max is taken across the halves.  Groups of
 // 3 and 5-7 take that kernel too, laid out as 4 and 8 rows per query (padding rows
 // load no query and start at -inf).  The generic kernel covers every other
-// shape/dtype (fp32 caches, head_dim not 128, groups above 8) and follows the reference fold order
-// exactly: for each query in turn, out += (p - out) / (n_seen + n + 1).
+// shape/dtype (fp32 caches, head_dim not 128, groups above 8) and follows the
+// reference fold order exactly: for each query in turn,
+// out += (p - out) / (n_seen + n + 1).
 #include "common.h"
 
 #include <algorithm>

@@ -18,11 +18,11 @@
 //   sum[t]      = sum_n p[n, t]                              (per-wave sums + LDS)
 //   out[t]      = (out[t] * n_seen + sum[t]) / (n_seen + nq) (== nq reference folds)
 //
-// Groups of 8 heads run on the query-register kernel only: a query's eight rows
+// Groups of 8 and 16 heads run on the query-register kernel only: a query's rows
 // span both halves of a wave, and their max is taken across the halves.  Groups of
-// 3 and 5-7 take that kernel too, laid out as 4 and 8 rows per query (padding rows
-// load no query and start at -inf).  The generic kernel covers every other
-// shape/dtype (fp32 caches, head_dim not 128, groups above 8) and follows the
+// 3, 5-7 and 9-15 take that kernel too, laid out as 4, 8 and 16 rows per query
+// (padding rows load no query and start at -inf).  The generic kernel covers every
+// other shape/dtype (fp32 caches, head_dim not 128, groups above 16) and follows the
 // reference fold order exactly: for each query in turn,
 // out += (p - out) / (n_seen + n + 1).
 #include "common.h"
@@ -456,9 +456,10 @@ template <typename T, typename V8, int G, bool CAUSAL, int RG, int NBUF, bool SW
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
   // QG: queries in an aligned group of four output rows (G <= 4); with G = 8 a query's
-  // heads span two such groups, one in each half of the wave
+  // heads span two such groups, one in each half of the wave, with G = 16 four (two in
+  // each half)
   constexpr int NW = 8, TG = NW / RG, KS = 8, QG = G >= 4 ? 1 : 4 / G;
-  static_assert(G == 1 || G == 2 || G == 4 || G == 8, "group sizes");
+  static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16, "group sizes");
   static_assert(RG == 2 || RG == 4 || RG == 8, "row groups");
   static_assert(HP == 1 || HP == 2 || HP == 4 || HP == 8, "heads per workgroup");
   static_assert(RG % HP == 0 && (HP == 1 || SWZ), "whole row groups per head; packed heads use rows");
@@ -561,7 +562,17 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
           const float v = lbase[(int64_t)(a.qc0 + min(nn, nq - 1)) * a.lse_sn + h * GR + min(gg, GR - 1)];
           seed[jt][4 * i + j] = nn < nq && gg < GR ? -v * inv_scale : -INFINITY;
         }
-        if constexpr (CAUSAL && G == 8) {
+        if constexpr (CAUSAL && G == 16) {
+          // rows 16 q' .. 16 q' + 15 of the tile are one query (groups 2 q' and 2 q' + 1 of
+          // both halves); this lane finishes query q' = lh
+          if (i == 0) {
+            const int nn = (rgl * 64 + jt * 32 + 16 * lh) / G;
+            const int v = a.kv_len[(int64_t)r * a.N + a.qc0 + min(nn, nq - 1)];
+            lim[jt][0][0] = nn < nq ? v : 0;
+          } else {
+            lim[jt][i][0] = 0;
+          }
+        } else if constexpr (CAUSAL && G == 8) {
           // rows 8 i' .. 8 i' + 7 of the tile are one query (heads 0-3 in lanes 0-31,
           // 4-7 in lanes 32-63); this lane finishes queries i' = 2 lh and 2 lh + 1
           if (i < 2) {
@@ -676,6 +687,24 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
   // exp/max/sum of one row tile at token t: sum over this lane's 16 rows
   auto post = [&](const f32x16 &acc, const int (&lm)[4][QG], int t) {
     float sum = 0.f;
+    if constexpr (G == 16) {
+      // query q' of the tile: groups 2 q' and 2 q' + 1 of this lane (8 heads) and of
+      // lane +- 32 (the other 8); the swap gives both halves the max of all sixteen, and
+      // half lh finishes query lh
+      float m[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        float h8 = acc[8 * k];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) h8 = vmax(h8, acc[8 * k + e]);
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(h8), __float_as_uint(h8), false, false);
+        m[k] = vmax(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      }
+      const float e = __builtin_amdgcn_exp2f((lh ? m[1] : m[0]) * c2);
+      if constexpr (CAUSAL) sum += t < lm[0][0] ? e : 0.f;
+      else sum += e;
+      return sum;
+    }
     if constexpr (G == 8) {
       // query i' of the tile: heads 0-3 in this lane's group i' (lanes 0-31), heads 4-7
       // in the same group of lane + 32; the symmetric swap gives both halves the max of
@@ -915,9 +944,9 @@ static int launch_mfma(const ScoreArgs &a0, int bs_shift, hipStream_t st) {
     // 3.5-4.4) and above 384 (the matrix cores bound it); the K-slice kernel from 129 to
     // 384 rows (with 2 heads per workgroup, 4 row groups each, or 1 head and 4 row
     // groups, the query-register kernel took 4-10% longer there)
-    // groups of 8 heads, and groups padded to 4 or 8 (3, 5, 6, 7), run on the query-register
-    // kernel alone
-    const bool qreg = G == 8 || a0.G != G || choice == MFMA_QREG ||
+    // groups of 8 and 16 heads, and groups padded to 4, 8 or 16 (3, 5-7, 9-15), run on the
+    // query-register kernel alone (one head per workgroup)
+    const bool qreg = G >= 8 || a0.G != G || choice == MFMA_QREG ||
                       (choice == MFMA_AUTO && (rows <= 128 || rows > 384));
     if (qreg) {
       // query tile in registers, K shared through LDS; RG row groups of 64 rows over HPV
@@ -944,7 +973,7 @@ static int launch_mfma(const ScoreArgs &a0, int bs_shift, hipStream_t st) {
       // rows the matrix cores bound it: fragment layout (fewer address instructions) and
       // two chunks in flight.  Set-up measured at ~5 us against ~3.7 us per 512-row chunk
       // of 128 tokens.
-      if constexpr (G == 8) {
+      if constexpr (G >= 8) {
         if (rows <= 128) ACTKV_QREG(2, 3, true, 128, 1.5, 1);
         else if (rows <= 256) ACTKV_QREG(4, 3, true, 128, 1.5, 1);
         else ACTKV_QREG(8, 2, false, 128, 1.5, 1);
@@ -970,7 +999,7 @@ static int launch_mfma(const ScoreArgs &a0, int bs_shift, hipStream_t st) {
       hipLaunchKernelGGL((score_kslice_kernel<T, V8, G, ROWSV, false, NW, TT>), dim3(grid),        \
                          dim3(NW * 64), 0, st, a, tpw, cpp, pairs, bs_shift);                      \
   } while (0)
-      if constexpr (G != 8) {   // never reached with G = 8 (above)
+      if constexpr (G < 8) {    // never reached with G >= 8 (above)
         if (rows <= 128) ACTKV_LAUNCH(128);
         else if (rows <= 256) ACTKV_LAUNCH(256);
         else ACTKV_LAUNCH(512);
@@ -1048,17 +1077,19 @@ extern "C" int actkv_action_scores(
   for (int sh = 4; sh < 31; ++sh)
     if (block_size == (1 << sh)) bs_shift = sh;
   const bool mfma_ok = q_dtype == kv_dtype && (kv_dtype == ACTKV_BF16 || kv_dtype == ACTKV_F16) &&
-                       D == 128 && G >= 1 && G <= 8 && scale > 0.f && vec_ok &&
+                       D == 128 && G >= 1 && G <= 16 && scale > 0.f && vec_ok &&
                        bs_shift >= 0;
   int rc;
   if (mfma_ok) {
     if (kv_dtype == ACTKV_BF16) {
-      rc = G > 4 ? launch_mfma<__bf16, bf16x8, 8>(a, bs_shift, st)
+      rc = G > 8 ? launch_mfma<__bf16, bf16x8, 16>(a, bs_shift, st)
+         : G > 4 ? launch_mfma<__bf16, bf16x8, 8>(a, bs_shift, st)
          : G > 2 ? launch_mfma<__bf16, bf16x8, 4>(a, bs_shift, st)
          : G == 2 ? launch_mfma<__bf16, bf16x8, 2>(a, bs_shift, st)
                   : launch_mfma<__bf16, bf16x8, 1>(a, bs_shift, st);
     } else {
-      rc = G > 4 ? launch_mfma<_Float16, f16x8, 8>(a, bs_shift, st)
+      rc = G > 8 ? launch_mfma<_Float16, f16x8, 16>(a, bs_shift, st)
+         : G > 4 ? launch_mfma<_Float16, f16x8, 8>(a, bs_shift, st)
          : G > 2 ? launch_mfma<_Float16, f16x8, 4>(a, bs_shift, st)
          : G == 2 ? launch_mfma<_Float16, f16x8, 2>(a, bs_shift, st)
                   : launch_mfma<_Float16, f16x8, 1>(a, bs_shift, st);

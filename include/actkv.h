@@ -75,10 +75,10 @@ const char *actkv_version(void);
  * out   : float32 [L, R, Hkv, W], strides out_sl out_sr out_sh, unit last,
  *         W >= max_blocks*block_size (checked)
  * scale : softmax scale (the reference default is head_dim^-0.5, lse_attn.py:148)
- * bf16/fp16 q and K of one dtype with D = 128 and Hq/Hkv from 1 to 8 run on the matrix
- * cores (groups of 3 and 5-7 laid out as 4 and 8 rows per query, the extra rows padding;
- * 512/G' queries per launch for the laid-out group G', more as several launches); every
- * other case uses float32 dot products.
+ * bf16/fp16 q and K of one dtype with D = 128 and Hq/Hkv from 1 to 16 run on the matrix
+ * cores (groups of 3, 5-7 and 9-15 laid out as 4, 8 and 16 rows per query, the extra rows
+ * padding; 512/G' queries per launch for the laid-out group G', more as several
+ * launches); every other case uses float32 dot products.
  */
 int actkv_action_scores(
     const void *q, int q_dtype, int64_t q_sl, int64_t q_sr, int64_t q_sn, int64_t q_sh,

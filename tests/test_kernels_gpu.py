@@ -528,6 +528,11 @@ def test_action_scores_ragged_lengths_in_a_padded_table(hq, hkv, n_q, dtype):
     (torch.float16, 40, 8, 30, True, True),      # G = 5 padded to 8: 240 rows
     (torch.bfloat16, 48, 8, 70, True, False),    # G = 6: two launches (64 + 6 queries)
     (torch.bfloat16, 28, 4, 9, False, False),    # G = 7: 72 rows
+    (torch.bfloat16, 128, 8, 10, True, True),    # G = 16 (Llama-3.1-405B): 160 rows
+    (torch.float16, 128, 8, 32, False, False),   # G = 16: 512 rows
+    (torch.bfloat16, 32, 2, 70, True, False),    # G = 16: three launches (32 + 32 + 6 queries)
+    (torch.bfloat16, 96, 8, 40, True, True),     # G = 12 padded to 16: two launches
+    (torch.float16, 72, 8, 7, False, False),     # G = 9 padded to 16: 112 rows
 ])
 def test_action_scores_groups_of_eight_heads(dtype, hq, hkv, n_q, causal, partial):
     """G = 8 (64 query heads over 8 KV heads, as Qwen3-32B): a query's eight heads span both

@@ -112,3 +112,46 @@ def test_random_shapes_with_other_groups_match_the_oracle(seed):
     ref.action_scores_nfold(q, kv0, tables, lens, lse, out_o, n_o, n_valid=n_valid, kv_len=kv_len)
     torch.testing.assert_close(out_k.cpu(), out_o, rtol=1e-3, atol=1e-6)
     assert torch.equal(n_k.cpu(), n_o)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_shapes_with_groups_above_eight_match_the_oracle(seed):
+    """Groups of 9 to 16 query heads per KV head (laid out as 16 rows per query): 128/8, 96/8,
+    72/8, 32/2; more than 32 queries run as several launches."""
+    rnd = random.Random(8000 + seed)
+    n_req = rnd.randint(1, 3)
+    lens = [rnd.choice([rnd.randint(1, 300), rnd.randint(300, 3000)]) for _ in range(n_req)]
+    hq, hkv = rnd.choice([(128, 8), (96, 8), (72, 8), (32, 2)])
+    n_q = rnd.choice([1, rnd.randint(2, 16), rnd.randint(17, 70)])
+    dtype, bs = rnd.choice([torch.bfloat16, torch.float16]), rnd.choice([16, 32])
+    causal, partial = rnd.random() < 0.5, rnd.random() < 0.3
+    print(f"case {seed}: lens {lens} hq {hq} hkv {hkv} n_q {n_q} {dtype} bs {bs} causal {causal} "
+          f"partial {partial}", flush=True)
+    g = torch.Generator().manual_seed(300 + seed)
+    nb = sum(math.ceil(n / bs) for n in lens) + 3
+    cache = PagedKVCache(nb, bs, hkv, 128, n_layers=1, dtype=dtype, device="cuda")
+    cache.free = torch.randperm(nb, generator=g).tolist()
+    for r, n in enumerate(lens):
+        cache.append(r, torch.randn(1, n, hkv, 128, generator=g).to(dtype).cuda(),
+                     torch.randn(1, n, hkv, 128, generator=g).to(dtype).cuda())
+    reqs = list(range(len(lens)))
+    bt, seq = cache.block_table(reqs), cache.seq_tensor(reqs)
+    width = bt.shape[1] * bs
+    q = torch.randn(len(reqs), n_q, hq, 128, generator=g).to(dtype)
+    kv0 = cache.kv[0].cpu()
+    tables = [cache.tables[r] for r in reqs]
+    lse = torch.stack([ref.decode_lse(q[:, n], kv0, tables, lens) for n in range(n_q)], 1)
+    kv_len = (torch.stack([torch.randint(1, s + 1, (n_q,), generator=g) for s in lens]).to(torch.int32)
+              if causal else None)
+    n_valid = (torch.tensor([random.Random(seed + r).randint(0, n_q) for r in reqs], dtype=torch.int32)
+               if partial else None)
+    out0 = torch.rand(len(reqs), hkv, width, generator=g)
+    n0 = torch.randint(0, 9, (len(reqs),), generator=g).to(torch.int32)
+    out_k, n_k = out0.cuda(), n0.cuda()
+    action_scores(q.cuda(), cache.kv[0], bt, seq, lse.cuda(), out_k, n_k,
+                  n_valid=None if n_valid is None else n_valid.cuda(),
+                  kv_len=None if kv_len is None else kv_len.cuda())
+    out_o, n_o = out0.clone(), n0.clone()
+    ref.action_scores_nfold(q, kv0, tables, lens, lse, out_o, n_o, n_valid=n_valid, kv_len=kv_len)
+    torch.testing.assert_close(out_k.cpu(), out_o, rtol=1e-3, atol=1e-6)
+    assert torch.equal(n_k.cpu(), n_o)

@@ -452,13 +452,17 @@ score_kslice_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
 // tile.  Per-token partial sums (one per row group and lane half) go to LDS at
 // the end of the chunk; after the next barrier the first HP x CH threads add each
 // head's in a fixed order and write the running means.
-template <typename T, typename V8, int G, bool CAUSAL, int RG, int NBUF, bool SWZ, int CH, int HP>
+template <typename T, typename V8, int G, bool CAUSAL, int RG, int NBUF, bool SWZ, int CH, int HP, int DH = 128>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
   // QG: queries in an aligned group of four output rows (G <= 4); with G = 8 a query's
   // heads span two such groups, one in each half of the wave, with G = 16 four (two in
   // each half)
-  constexpr int NW = 8, TG = NW / RG, KS = 8, QG = G >= 4 ? 1 : 4 / G;
+  constexpr int NW = 8, TG = NW / RG, KS = DH / 16, QG = G >= 4 ? 1 : 4 / G;
+  static_assert(DH == 64 || DH == 128, "head dims");
+  constexpr int PB = DH * 2;            // bytes of one head's piece of a token row
+  constexpr int NC = PB / 16;           // its 16-byte columns
+  constexpr int NCS = NC == 16 ? 4 : 3;  // log2(NC)
   static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16, "group sizes");
   static_assert(RG == 2 || RG == 4 || RG == 8, "row groups");
   static_assert(HP == 1 || HP == 2 || HP == 4 || HP == 8, "heads per workgroup");
@@ -469,7 +473,7 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
   constexpr int TPC = CH / 32;          // 32-token tiles per chunk
   constexpr int NT = TPC / TG;          // tiles per wave per chunk
   static_assert(NT >= 1 && NT * TG == TPC, "token groups");
-  constexpr int HROW = HP * 256;        // bytes of one token's HP head pieces
+  constexpr int HROW = HP * PB;         // bytes of one token's HP head pieces
   constexpr int CHB = CH * HROW;        // bytes of one chunk
   constexpr int LPW = CHB / 1024 / NW;  // 1 KiB loads per wave per chunk
   static_assert(LPW * 1024 * NW == CHB, "whole loads per wave");
@@ -605,12 +609,13 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
   const float fn0 = (float)n0, fden = (float)(n0 + nq);
   const int ld_tile = (wave * LPW) / KS, ld_ks = (wave * LPW) % KS;
 
-  // Swizzled rows: a chunk in LDS is CH token rows of HROW bytes, the 256-byte pieces of
+  // Swizzled rows: a chunk in LDS is CH token rows of HROW bytes, the PB-byte pieces (256 at
+  // head dim 128) of
   // heads h0 .. h0+HP-1 side by side, and each piece's 16-byte columns stored XOR-swizzled:
-  // LDS column c of token t's piece holds that head's column c ^ (t % 16).  The chunk is
+  // LDS column c of token t's piece holds that head's column c ^ (t % NC).  The chunk is
   // CHB / 16 units of 16 bytes; this wave's share is LPW loads of 64 consecutive units
   // (lane i of load j writes unit 64 (LPW wave + j) + i), so every load reads whole
-  // 256-byte pieces, and with HP > 1 HP x 256 contiguous bytes of each token's row.  A
+  // PB-byte pieces, and with HP > 1 HP x PB contiguous bytes of each token's row.  A
   // token past t_end, or in a block the table marks invalid, reads row 0 of block 0
   // instead; its score is never written.
   auto load_chunk = [&](int cbase, unsigned char *kb) {
@@ -632,9 +637,9 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {
       const int u = (wave * LPW + i) * 64 + lane;   // 16-byte unit of the chunk
-      const int tl = u / (HP * 16);                 // token of the chunk
-      const int w = u % (HP * 16);
-      const int hp = w >> 4, col = (w & 15) ^ (tl & 15);
+      const int tl = u / (HP * NC);                 // token of the chunk
+      const int w = u % (HP * NC);
+      const int hp = w >> NCS, col = (w & (NC - 1)) ^ (tl & (NC - 1));
       const int t = cbase + tl;
       const int bi = min((t >> bs_shift) - b0, nbt - 1);
       int phys = bts[bi];
@@ -663,7 +668,7 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
   // distinct columns (no bank conflict)
   int roff[KS];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) roff[ks] = lcol * HROW + hi * 256 + (((2 * ks + lh) ^ (lcol & 15)) << 4);
+  for (int ks = 0; ks < KS; ++ks) roff[ks] = lcol * HROW + hi * PB + (((2 * ks + lh) ^ (lcol & (NC - 1))) << 4);
   auto read_b = [&](V8 (&b8)[KS], const unsigned char *kb, int tile) {
     if constexpr (SWZ) {
 #pragma unroll
@@ -774,12 +779,12 @@ score_qreg_kernel(ScoreArgs a, int tpw, int cpp, int pairs, int bs_shift) {
       // of the next tile and the VALU work of chain 0
       if (k == 0) __builtin_amdgcn_sched_group_barrier(0x100, KS, 0);   // DS read
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < KS; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
         if (k > 0) __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < KS; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         if (k + 1 < NT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
         __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
@@ -927,7 +932,7 @@ static int mfma_choice() {
   return c;
 }
 
-template <typename T, typename V8, int G>
+template <typename T, typename V8, int G, int DH = 128>
 static int launch_mfma(const ScoreArgs &a0, int bs_shift, hipStream_t st) {
   const int pairs = a0.L * a0.R * a0.Hkv;
   const int span = a0.max_blocks * a0.BS;
@@ -946,7 +951,7 @@ static int launch_mfma(const ScoreArgs &a0, int bs_shift, hipStream_t st) {
     // groups, the query-register kernel took 4-10% longer there)
     // groups of 8 and 16 heads, and groups padded to 4, 8 or 16 (3, 5-7, 9-15), run on the
     // query-register kernel alone (one head per workgroup)
-    const bool qreg = G >= 8 || a0.G != G || choice == MFMA_QREG ||
+    const bool qreg = DH != 128 || G >= 8 || a0.G != G || choice == MFMA_QREG ||
                       (choice == MFMA_AUTO && (rows <= 128 || rows > 384));
     if (qreg) {
       // query tile in registers, K shared through LDS; RG row groups of 64 rows over HPV
@@ -959,10 +964,10 @@ static int launch_mfma(const ScoreArgs &a0, int bs_shift, hipStream_t st) {
     const int cpp = (span + tpw - 1) / tpw;                                                        \
     const int grid = ((packs + 7) / 8) * 8 * cpp;                                                  \
     if (causal)                                                                                    \
-      hipLaunchKernelGGL((score_qreg_kernel<T, V8, G, true, RGV, NB, SW, CHV, HPV>), dim3(grid),   \
+      hipLaunchKernelGGL((score_qreg_kernel<T, V8, G, true, RGV, NB, SW, CHV, HPV, DH>), dim3(grid), \
                          dim3(512), 0, st, a, tpw, cpp, packs, bs_shift);                          \
     else                                                                                           \
-      hipLaunchKernelGGL((score_qreg_kernel<T, V8, G, false, RGV, NB, SW, CHV, HPV>), dim3(grid),  \
+      hipLaunchKernelGGL((score_qreg_kernel<T, V8, G, false, RGV, NB, SW, CHV, HPV, DH>), dim3(grid),\
                          dim3(512), 0, st, a, tpw, cpp, packs, bs_shift);                          \
   } while (0)
       // Up to 128 rows the call streams K at the HBM rate.  Several KV heads of the same
@@ -999,7 +1004,7 @@ static int launch_mfma(const ScoreArgs &a0, int bs_shift, hipStream_t st) {
       hipLaunchKernelGGL((score_kslice_kernel<T, V8, G, ROWSV, false, NW, TT>), dim3(grid),        \
                          dim3(NW * 64), 0, st, a, tpw, cpp, pairs, bs_shift);                      \
   } while (0)
-      if constexpr (G < 8) {    // never reached with G >= 8 (above)
+      if constexpr (G < 8 && DH == 128) {   // never reached otherwise (above)
         if (rows <= 128) ACTKV_LAUNCH(128);
         else if (rows <= 256) ACTKV_LAUNCH(256);
         else ACTKV_LAUNCH(512);
@@ -1010,6 +1015,16 @@ static int launch_mfma(const ScoreArgs &a0, int bs_shift, hipStream_t st) {
     if (rc) return rc;
   }
   return ACTKV_OK;
+}
+
+// The group size laid out in rows (1, 2, 4, 8 or 16; groups in between are padded).
+template <typename T, typename V8, int DH>
+static int launch_mfma_groups(const ScoreArgs &a, int G, int bs_shift, hipStream_t st) {
+  return G > 8 ? launch_mfma<T, V8, 16, DH>(a, bs_shift, st)
+       : G > 4 ? launch_mfma<T, V8, 8, DH>(a, bs_shift, st)
+       : G > 2 ? launch_mfma<T, V8, 4, DH>(a, bs_shift, st)
+       : G == 2 ? launch_mfma<T, V8, 2, DH>(a, bs_shift, st)
+                : launch_mfma<T, V8, 1, DH>(a, bs_shift, st);
 }
 
 template <typename QT, typename KT>
@@ -1077,23 +1092,16 @@ extern "C" int actkv_action_scores(
   for (int sh = 4; sh < 31; ++sh)
     if (block_size == (1 << sh)) bs_shift = sh;
   const bool mfma_ok = q_dtype == kv_dtype && (kv_dtype == ACTKV_BF16 || kv_dtype == ACTKV_F16) &&
-                       D == 128 && G >= 1 && G <= 16 && scale > 0.f && vec_ok &&
+                       (D == 128 || D == 64) && G >= 1 && G <= 16 && scale > 0.f && vec_ok &&
                        bs_shift >= 0;
   int rc;
   if (mfma_ok) {
-    if (kv_dtype == ACTKV_BF16) {
-      rc = G > 8 ? launch_mfma<__bf16, bf16x8, 16>(a, bs_shift, st)
-         : G > 4 ? launch_mfma<__bf16, bf16x8, 8>(a, bs_shift, st)
-         : G > 2 ? launch_mfma<__bf16, bf16x8, 4>(a, bs_shift, st)
-         : G == 2 ? launch_mfma<__bf16, bf16x8, 2>(a, bs_shift, st)
-                  : launch_mfma<__bf16, bf16x8, 1>(a, bs_shift, st);
-    } else {
-      rc = G > 8 ? launch_mfma<_Float16, f16x8, 16>(a, bs_shift, st)
-         : G > 4 ? launch_mfma<_Float16, f16x8, 8>(a, bs_shift, st)
-         : G > 2 ? launch_mfma<_Float16, f16x8, 4>(a, bs_shift, st)
-         : G == 2 ? launch_mfma<_Float16, f16x8, 2>(a, bs_shift, st)
-                  : launch_mfma<_Float16, f16x8, 1>(a, bs_shift, st);
-    }
+    if (kv_dtype == ACTKV_BF16)
+      rc = D == 64 ? launch_mfma_groups<__bf16, bf16x8, 64>(a, G, bs_shift, st)
+                   : launch_mfma_groups<__bf16, bf16x8, 128>(a, G, bs_shift, st);
+    else
+      rc = D == 64 ? launch_mfma_groups<_Float16, f16x8, 64>(a, G, bs_shift, st)
+                   : launch_mfma_groups<_Float16, f16x8, 128>(a, G, bs_shift, st);
   } else {
     switch (q_dtype) {
       case ACTKV_F32: rc = dispatch_generic_kv<float>(a, kv_dtype, st); break;

@@ -75,8 +75,8 @@ const char *actkv_version(void);
  * out   : float32 [L, R, Hkv, W], strides out_sl out_sr out_sh, unit last,
  *         W >= max_blocks*block_size (checked)
  * scale : softmax scale (the reference default is head_dim^-0.5, lse_attn.py:148)
- * bf16/fp16 q and K of one dtype with D = 128 and Hq/Hkv from 1 to 16 run on the matrix
- * cores (groups of 3, 5-7 and 9-15 laid out as 4, 8 and 16 rows per query, the extra rows
+ * bf16/fp16 q and K of one dtype with D = 128 or 64 and Hq/Hkv from 1 to 16 run on the
+ * matrix cores (groups of 3, 5-7 and 9-15 laid out as 4, 8 and 16 rows per query, the extra rows
  * padding; 512/G' queries per launch for the laid-out group G', more as several
  * launches); every other case uses float32 dot products.
  */

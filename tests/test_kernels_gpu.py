@@ -567,6 +567,47 @@ def test_action_scores_groups_of_eight_heads(dtype, hq, hkv, n_q, causal, partia
     assert torch.equal(n_k.cpu(), n_o)
 
 
+@pytest.mark.parametrize("dtype,hq,hkv,n_q,causal,partial", [
+    (torch.bfloat16, 64, 8, 10, True, True),     # GPT-OSS shape (G = 8): 80 rows
+    (torch.bfloat16, 64, 8, 64, False, False),   # G = 8: 512 rows
+    (torch.float16, 32, 8, 100, True, False),    # G = 4: 400 rows, fragment layout
+    (torch.bfloat16, 32, 8, 12, False, True),    # G = 4: 48 rows, 8 heads per workgroup
+    (torch.bfloat16, 32, 8, 30, True, False),    # G = 4: 120 rows, 4 heads per workgroup
+    (torch.float16, 16, 8, 70, False, False),    # G = 2: 140 rows
+    (torch.bfloat16, 8, 8, 300, True, True),     # G = 1: 300 rows
+    (torch.bfloat16, 128, 8, 40, True, False),   # G = 16: two launches
+])
+def test_action_scores_head_dim_64(dtype, hq, hkv, n_q, causal, partial):
+    """head_dim 64 (GPT-OSS, Llama-3.2-1B): the query-register kernel with 128-byte head pieces
+    (4 k steps, 8 swizzled 16-byte columns)."""
+    lens = [700, 90, 1500]
+    d, bs = 64, 16
+    cache = _filled_cache(lens, bs=bs, hkv=hkv, d=d, dtype=dtype, seed=51)
+    reqs = list(range(len(lens)))
+    bt, seq = cache.block_table(reqs), cache.seq_tensor(reqs)
+    width = bt.shape[1] * bs
+    g = torch.Generator().manual_seed(52)
+    q = torch.randn(len(reqs), n_q, hq, d, generator=g).to(dtype)
+    kv0 = cache.kv[0].cpu()
+    tables = [cache.tables[r] for r in reqs]
+    lse = torch.stack([ref.decode_lse(q[:, n], kv0, tables, lens) for n in range(n_q)], 1)
+    n_valid = torch.tensor([n_q, min(3, n_q), max(n_q - 7, 0)], dtype=torch.int32) if partial else None
+    kv_len = None
+    if causal:
+        kv_len = torch.stack([torch.randint(1, s + 1, (n_q,), generator=g) for s in lens]).to(torch.int32)
+        kv_len[0, 0] = lens[0]
+    out0 = torch.rand(len(reqs), hkv, width, generator=g)
+    n0 = torch.tensor([1, 0, 4], dtype=torch.int32)
+    out_k, n_k = out0.cuda(), n0.cuda()
+    action_scores(q.cuda(), cache.kv[0], bt, seq, lse.cuda(), out_k, n_k,
+                  n_valid=None if n_valid is None else n_valid.cuda(),
+                  kv_len=None if kv_len is None else kv_len.cuda())
+    out_o, n_o = out0.clone(), n0.clone()
+    ref.action_scores_nfold(q, kv0, tables, lens, lse, out_o, n_o, n_valid=n_valid, kv_len=kv_len)
+    torch.testing.assert_close(out_k.cpu(), out_o, rtol=1e-3, atol=1e-6)
+    assert torch.equal(n_k.cpu(), n_o)
+
+
 def test_action_scores_every_layer_in_one_launch():
     """kv [L, 2, ...] with q [L, R, N, Hq, D]: each layer scored against its own K (extension)."""
     lens = [300, 77]

@@ -2,8 +2,8 @@
 
 Drop-in for the reference module actkv/kernels/lse_attn.py: same names, arguments, in-place
 semantics and errors.  `action_scores` runs the HIP kernels of libactkv_hip.so (bf16/fp16
-MFMA tile kernel for head_dim 128 and GQA groups of 1, 2 or 4; a VALU kernel for every other
-shape and for float32 caches).  It has no CPU path: CPU tensors raise.
+MFMA kernels for head_dim 128 or 64 and 1 to 16 query heads per KV head; a VALU kernel for
+every other shape and for float32 caches).  It has no CPU path: CPU tensors raise.
 
 Layout (vLLM-style), one layer:
     kv          [2, num_blocks, block_size, n_kv_heads, head_dim]

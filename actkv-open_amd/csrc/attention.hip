@@ -10,8 +10,8 @@
 // out and lse are float32.  A row that sees no token gets lse = -inf, out = 0
 // (torch's logsumexp and softmax-einsum over an empty set).
 //
-// MFMA path (bf16/fp16, head_dim 128, any GQA group, more than one 32-row tile of
-// query rows per pair): FlashAttention-style,
+// MFMA path (bf16/fp16, head_dim 128 or 64, any GQA group, more than one 32-row tile
+// of query rows per pair): FlashAttention-style,
 // one workgroup per (layer, request, KV head, group of NW row tiles), NW waves,
 // each owning one 32-row tile of the pair's query rows (n, g) and streaming all
 // of the request's tokens.  The transposed products keep every per-query
@@ -34,7 +34,11 @@
 // slices through a private LDS region without workgroup barriers; V comes back
 // transposed from LDS (ds_read_b64_tr_b16).  Described at attn_decode_kernel.
 //
-// Generic path (any other dtype / head_dim / group): one workgroup per query row,
+// Head dim 64 runs the same kernels with half-length token rows: a 16-byte load
+// instruction then moves eight rows instead of four, the rows' eight 16-byte chunks are
+// swizzled with their own pattern (dswz), and two 32-dim output tiles replace four.
+//
+// Generic path (any other dtype / head_dim): one workgroup per query row,
 // float32 dot products, an online max/sum pass for lse and a second pass that
 // accumulates out through LDS-staged probabilities.
 #include "common.h"
@@ -63,7 +67,7 @@ struct AttnArgs {
   // the partial results of each chunk (row-major [pair][row][chunk])
   // dyn: the decode kernel's interleaved split (attn_dec_chunks); tpc is then unused
   int nchunk, tpc, rows_pad, dyn;
-  float *ws_o;   // [pairs][rows_pad][nchunk][128]: unnormalised sum p v
+  float *ws_o;   // [pairs][rows_pad][nchunk][D]: unnormalised sum p v
   float *ws_ml;  // [pairs][rows_pad][nchunk][2]: running max (log2 units), sum p
 };
 
@@ -92,23 +96,25 @@ __device__ __forceinline__ int attn_phys(const AttnArgs &a, int r, int b) {
 
 // ------------------------------------------------------------------ chunk merge
 // One wave merges the nc token chunks of query row `id` (pair * rows_pad + row) and writes
-// out and lse, two dims per lane:
+// out and lse, DH / 64 dims per lane:
 //   M = max_c m_c, w_c = 2^(m_c - M), out = sum_c w_c O_c / sum_c w_c l_c,
 //   lse = ln 2 * (M + log2 sum_c w_c l_c)
 // Lane c reads chunk c's (max, sum) for up to 64 chunks at a time (a butterfly max and sum);
 // the O rows of the first 16 chunks are loaded in the same round trip (rows past nc are
 // never written: their terms are selected away, not multiplied by zero), later ones after.
+template <int DH>
 __device__ __forceinline__ void attn_merge_row(const AttnArgs &a, int64_t id, int nc, int64_t o_off,
                                                int64_t lse_off, int lane) {
+  static_assert(DH == 64 || DH == 128, "head dims");
   constexpr int PRE = 16;
   const float *ml = a.ws_ml + id * a.nchunk * 2;
-  const float *wo = a.ws_o + id * a.nchunk * 128;
+  const float *wo = a.ws_o + id * a.nchunk * DH;
   float pre0[PRE], pre1[PRE];
 #pragma unroll
   for (int j = 0; j < PRE; ++j) {
     const int jc = max(0, min(j, nc - 1));  // an in-bounds row: the workspace holds nchunk >= max(nc, 1)
-    pre0[j] = wo[(int64_t)jc * 128 + lane];
-    pre1[j] = wo[(int64_t)jc * 128 + 64 + lane];
+    pre0[j] = wo[(int64_t)jc * DH + lane];
+    if constexpr (DH == 128) pre1[j] = wo[(int64_t)jc * DH + 64 + lane];
   }
   float M = -INFINITY;
   for (int c = lane; c < nc; c += 64) M = fmaxf(M, ml[2 * c]);
@@ -128,20 +134,20 @@ __device__ __forceinline__ void attn_merge_row(const AttnArgs &a, int64_t id, in
       for (int j = 0; j < PRE; ++j) {
         const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
         o0 += j < nc ? wj * pre0[j] : 0.f;
-        o1 += j < nc ? wj * pre1[j] : 0.f;
+        if constexpr (DH == 128) o1 += j < nc ? wj * pre1[j] : 0.f;
       }
     }
-    const float *wc = wo + (int64_t)c0 * 128;
+    const float *wc = wo + (int64_t)c0 * DH;
     for (int j = c0 == 0 ? PRE : 0; j < min(64, nc - c0); ++j) {
       const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
-      o0 += wj * wc[j * 128 + lane];
-      o1 += wj * wc[j * 128 + 64 + lane];
+      o0 += wj * wc[j * DH + lane];
+      if constexpr (DH == 128) o1 += wj * wc[j * DH + 64 + lane];
     }
   }
   const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
   float *op = a.out + o_off;
   op[lane] = o0 * inv;
-  op[64 + lane] = o1 * inv;
+  if constexpr (DH == 128) op[64 + lane] = o1 * inv;
   if (lane == 0) a.lse[lse_off] = Lsum > 0.f ? (M + __log2f(Lsum)) * 0.6931471805599453f : -INFINITY;
 }
 
@@ -160,7 +166,17 @@ __device__ __forceinline__ void attn_merge_row(const AttnArgs &a, int64_t id, in
 // (max(8, 1.5 * CUs / pairs), slices interleaved over their waves: attn_split), merged by the
 // combine launch; a sequence whose slices fit one chunk is written here directly.
 constexpr int DW = 4;                         // waves per decode workgroup
-constexpr int DREG = 2 * 32 * 256;            // LDS bytes per wave: K rows, then V rows
+
+// Token-row geometry at head dim DH (2-byte elements): one KV head's row of a token is PB
+// bytes, NC 16-byte chunks (NC = 2^NCS); a 64-lane 16-byte load moves RPI = 2^RPS rows;
+// the S^T product takes KS 16-dim steps and O^T has DT 32-dim tiles.
+template <int DH> struct RowShape {
+  static_assert(DH == 64 || DH == 128, "head dims");
+  static constexpr int PB = 2 * DH, NC = PB / 16, NCS = NC == 16 ? 4 : 3;
+  static constexpr int RPI = 64 / NC, RPS = 6 - NCS;
+  static constexpr int KS = DH / 16, DT = DH / 32;
+  static constexpr int DREG = 2 * 32 * PB;    // decode LDS bytes per wave: K rows, then V rows
+};
 
 // The decode split (a.dyn): slice s of a pair (tokens 32s .. 32s + 31) goes to wave
 // s mod (nchunk * DW), that is wave s mod DW of chunk (s / DW) mod nchunk.  A wave's slices
@@ -171,20 +187,31 @@ __device__ __forceinline__ int attn_dec_chunks(const AttnArgs &a, int S) {
   return min(a.nchunk, (((S + 31) >> 5) + DW - 1) / DW);
 }
 
-// 16-byte chunk slot of chunk c of token t is c ^ dswz(t).  Distinct slots, so no LDS bank
-// conflicts, for: 16 consecutive tokens at one chunk (K A-operand reads); four consecutive
-// tokens at four consecutive chunks (a 32-lane transposed V read: 16 slots); 16 chunks of
-// one token (row writes).  2 (t mod 8) + (t / 8 mod 2) left the transposed V reads
-// 2-way conflicted.
-__device__ __forceinline__ int dswz(int t) { return 4 * (t & 3) + ((t >> 2) & 3); }
+// 16-byte chunk slot of chunk c of token t is c ^ dswz(t).  Distinct bank groups (the
+// address's 16-byte unit mod 16), so no LDS bank conflicts, for: 16 consecutive tokens at
+// one chunk (K A-operand reads); four consecutive tokens at four consecutive chunks (a
+// 32-lane transposed V read: 16 slots); the chunks of one row (row writes).
+//   Head dim 128 (16 chunks, a row is 16 units): 4 (t mod 4) + (t / 4 mod 4).  2 (t mod 8)
+//   + (t / 8 mod 2) left the transposed V reads 2-way conflicted.
+//   Head dim 64 (8 chunks, a row is 8 units, so rows of odd t use units 8-15): 4 (t / 2 mod 2)
+//   + (t / 4 mod 4).  Among 16 tokens each parity takes all 8 values; tokens 4m and 4m + 2
+//   (and 4m + 1, 4m + 3) differ in bit 2, so four consecutive chunks of them fall in
+//   disjoint halves.
+template <int DH>
+__device__ __forceinline__ int dswz(int t) {
+  if constexpr (DH == 128) return 4 * (t & 3) + ((t >> 2) & 3);
+  else return 4 * ((t >> 1) & 1) + ((t >> 2) & 3);
+}
 
 typedef short dv4s __attribute__((ext_vector_type(4)));
 
-template <typename T, typename V8, bool CAUSAL>
+template <typename T, typename V8, int DH, bool CAUSAL>
 __global__ void __launch_bounds__(DW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
+  using RS = RowShape<DH>;
+  constexpr int PB = RS::PB, NC = RS::NC, NCS = RS::NCS, RPI = RS::RPI, KS = RS::KS, DT = RS::DT;
   const int G = a.G;   // query heads per KV head: rows (n, g) of a tile are independent
-  __shared__ __attribute__((aligned(16))) unsigned char reg_lds[DW][DREG];
+  __shared__ __attribute__((aligned(16))) unsigned char reg_lds[DW][RS::DREG];
   __shared__ float mrg_ml[DW][32][2];
   __shared__ int wg_lim;
   const int p = blockIdx.x / a.nchunk, chunk = blockIdx.x % a.nchunk;
@@ -220,34 +247,37 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
   }
   const int nsl = (s_end + 31) / 32;  // slices of the pair anyone needs
 
-  V8 qf[8];
+  V8 qf[KS];
   {
     const T *qp = (const T *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr +
                   (int64_t)(valid ? n : 0) * a.q_sn + (int64_t)(h * G + g) * a.q_sh + lh * 8;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qf[ks] = *(const V8 *)(qp + ks * 16);
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = *(const V8 *)(qp + ks * 16);
     if (!valid) {
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) qf[ks] = V8{};
+      for (int ks = 0; ks < KS; ++ks) qf[ks] = V8{};
     }
   }
   const T *kplane = (const T *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh;
   const T *vplane = kplane + a.kv_sv;
   unsigned char *kl = reg_lds[wave];
-  unsigned char *vl = kl + 32 * 256;
+  unsigned char *vl = kl + 32 * PB;
 
   // block-table entry of token group i (tokens 4i..4i+3) of slice s: lane i < 8 holds it.
   // Entries past the sequence are read too (bounds-checked by attn_phys): load_slice skips
   // their tokens.
   auto slice_phys = [&](int s) { return attn_phys(a, r, (s * 32 + 4 * (lane & 7)) >> bs_shift); };
-  // lane: token rows 4i + lane/16 (i = 0..7), 16-byte chunk lane%16, of K and V
-  uint4 kr[8], vr[8];
+  // lane: token rows RPI i + lane/NC (i < 32/RPI), 16-byte chunk lane%NC, of K and V.  The
+  // RPI (4 or 8) rows of one load lie in one block (blocks hold at least 16 tokens), the
+  // block of token group RPI i / 4.
+  constexpr int NI = 32 / RPI;
+  uint4 kr[NI], vr[NI];
   auto load_slice = [&](int s, int ph) {
-    const int c = lane & 15;
+    const int c = lane & (NC - 1);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int pb = __builtin_amdgcn_readlane(ph, i);
-      const int t = s * 32 + 4 * i + (lane >> 4);
+    for (int i = 0; i < NI; ++i) {
+      const int pb = __builtin_amdgcn_readlane(ph, i * RPI / 4);
+      const int t = s * 32 + RPI * i + (lane >> NCS);
       const bool ok = pb >= 0 && t < S;
       const int64_t off = ok ? (int64_t)pb * a.kv_sb + (int64_t)(t & (BS - 1)) * a.kv_ss + c * 8 : 0;
       kr[i] = *(const uint4 *)(kplane + off);
@@ -256,11 +286,11 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
     }
   };
   auto store_slice = [&]() {
-    const int c = lane & 15;
+    const int c = lane & (NC - 1);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int t = 4 * i + (lane >> 4);
-      const int o = t * 256 + ((c ^ dswz(t)) << 4);
+    for (int i = 0; i < NI; ++i) {
+      const int t = RPI * i + (lane >> NCS);
+      const int o = t * PB + ((c ^ dswz<DH>(t)) << 4);
       *(uint4 *)(kl + o) = kr[i];
       *(uint4 *)(vl + o) = vr[i];
     }
@@ -268,9 +298,9 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
 
   const float c2 = a.scale * 1.4426950408889634f;
   float m2 = -INFINITY, lsum = 0.f;
-  f32x16 oacc[4];
+  f32x16 oacc[DT];
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+  for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
     for (int e = 0; e < 16; ++e) oacc[dt][e] = 0.f;
 
@@ -278,9 +308,9 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
     // S^T = K . Q^T for the slice's 32 tokens (A: token lcol, dims 16ks + 8lh .. +7)
     f32x16 st = {};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
+    for (int ks = 0; ks < KS; ++ks) {
       const int c = 2 * ks + lh;
-      const V8 kf = *(const V8 *)(kl + lcol * 256 + ((c ^ dswz(lcol)) << 4));
+      const V8 kf = *(const V8 *)(kl + lcol * PB + ((c ^ dswz<DH>(lcol)) << 4));
       if constexpr (__is_same(T, __bf16))
         st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[ks], st, 0, 0, 0);
       else
@@ -322,7 +352,7 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
     m2 = m_new;
     if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0ull) {
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int e = 0; e < 16; ++e) oacc[dt][e] *= alpha;
     }
@@ -334,14 +364,14 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
+      for (int dt = 0; dt < DT; ++dt) {
         const int d = 32 * dt + dgrp;
         const int cc = d >> 3, half = (d >> 2) & 1;
         const int t_lo = 16 * kb + 4 * lh + jj, t_hi = t_lo + 8;
         const dv4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (dv4s __attribute__((address_space(3))) *)(vl + t_lo * 256 + ((cc ^ dswz(t_lo)) << 4) + half * 8));
+            (dv4s __attribute__((address_space(3))) *)(vl + t_lo * PB + ((cc ^ dswz<DH>(t_lo)) << 4) + half * 8));
         const dv4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (dv4s __attribute__((address_space(3))) *)(vl + t_hi * 256 + ((cc ^ dswz(t_hi)) << 4) + half * 8));
+            (dv4s __attribute__((address_space(3))) *)(vl + t_hi * PB + ((cc ^ dswz<DH>(t_hi)) << 4) + half * 8));
         // whole-register casts: the 64-bit results become the operand's two halves
         // (inserting the 16-bit elements one by one compiled to a wrong operand)
         const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
@@ -372,9 +402,9 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
   // ---- merge the waves' (max, sum, O) through LDS
   __syncthreads();
   {
-    float *om = (float *)reg_lds[wave];
+    float *om = (float *)reg_lds[wave];   // DT x 4 KiB: the wave's DREG bytes
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int e = 0; e < 16; ++e) om[(dt * 16 + e) * 64 + lane] = oacc[dt][e];
     if (lh == 0) { mrg_ml[wave][lcol][0] = m2; mrg_ml[wave][lcol][1] = lsum; }
@@ -392,7 +422,7 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
       Lsum += wgt[w] * mrg_ml[w][lcol][1];
     }
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         float o = 0.f;
@@ -402,9 +432,9 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
       }
     if (valid && nact > 1) {  // this chunk's partial result
       const int64_t pr = ((int64_t)p * a.rows_pad + row) * a.nchunk + chunk;
-      float *wo = a.ws_o + pr * 128;
+      float *wo = a.ws_o + pr * DH;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           f32x4 v;
@@ -416,7 +446,7 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
       const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
       float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * G + g) * a.o_sh;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int d0 = 32 * dt + 8 * i + 4 * lh;
@@ -437,8 +467,8 @@ attn_decode_kernel(AttnArgs a, int pairs, int bs_shift) {
 // shares ST-token stages of K and V held in an NSTG-deep LDS ring.  The stages are
 // loaded straight into LDS with buffer_load_dwordx4 ... lds, NSTG - 1 stages ahead of
 // the one being multiplied: no register staging, one LDS barrier per stage, and the
-// wait for a stage is counted by hand (wait_stages).  Each load
-// instruction moves four token rows (1 KB) of one block, so the buffer resource is that
+// wait for a stage is counted by hand (wait_stages).  Each load instruction moves
+// four token rows (eight at head dim 64; 1 KB) of one block, so the buffer resource is that
 // block (wave-uniform); its lanes pick the global 16-byte chunk that lands in their LDS
 // slot, which lays rows out with the decode path's XOR swizzle, and tokens past the
 // chunk (or in blocks the table marks invalid) are out of the resource's range, so the
@@ -465,12 +495,12 @@ __device__ __forceinline__ void lds_barrier() {
 // little (3 or 4 stages of 64 tokens and 2 of 128 are within 8%) and fewer, larger stages
 // (fewer barriers) win; 4- and 2-wave workgroups keep 64-token stages so that two fit
 // per CU.
-template <int TILES> struct RingShape {                      // TILES: row tiles per workgroup
+template <int TILES, int DH> struct RingShape {             // TILES: row tiles per workgroup
   static constexpr int ST = TILES >= 8 ? 128 : 64;            // tokens per stage
   static constexpr int NSTG = 2;                              // ring depth
   static constexpr int TBLW = TILES >= 8 ? 4096 : 2048;       // block-table window (entries)
-  static constexpr int SBYTES = 2 * ST * 256;                 // K then V rows of a stage
-  static constexpr int IPP = ST / 4;                          // load instructions per plane
+  static constexpr int SBYTES = 2 * ST * RowShape<DH>::PB;    // K then V rows of a stage
+  static constexpr int IPP = ST / RowShape<DH>::RPI;          // load instructions per plane
   static_assert(ST % 32 == 0, "whole slices per stage");
 };
 
@@ -497,12 +527,14 @@ __device__ __forceinline__ void buf_lds16(ri32x4 rsrc, unsigned voff, unsigned l
                : "memory");
 }
 
-template <typename T, typename V8, int NW, int RT, bool CAUSAL>
+template <typename T, typename V8, int DH, int NW, int RT, bool CAUSAL>
 __global__ void __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(RT >= 2 ? 1 : (NW >= 4 ? 2 : 1), RT >= 2 ? 1 : 2)))
 attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
   const int G = a.G;   // query heads per KV head: rows (n, g) of a tile are independent
-  using SH = RingShape<NW * RT>;
+  using SH = RingShape<NW * RT, DH>;
+  using RS = RowShape<DH>;
+  constexpr int PB = RS::PB, NC = RS::NC, NCS = RS::NCS, RPI = RS::RPI, KS = RS::KS, DT = RS::DT;
   constexpr int ST = SH::ST, NSTG = SH::NSTG, TBLW = SH::TBLW;
   constexpr int PER = 2 * SH::IPP / NW;  // load instructions per wave per stage
   static_assert((2 * SH::IPP) % NW == 0, "whole load instructions per wave");
@@ -556,16 +588,16 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
   }
   const int nst = (s_end + ST - 1) / ST;
 
-  V8 qf[RT][8];
+  V8 qf[RT][KS];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const T *qp = (const T *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr +
                   (int64_t)(valid[rt] ? n[rt] : 0) * a.q_sn + (int64_t)(h * G + g[rt]) * a.q_sh + lh * 8;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qf[rt][ks] = *(const V8 *)(qp + ks * 16);
+    for (int ks = 0; ks < KS; ++ks) qf[rt][ks] = *(const V8 *)(qp + ks * 16);
     if (!valid[rt]) {
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) qf[rt][ks] = V8{};
+      for (int ks = 0; ks < KS; ++ks) qf[rt][ks] = V8{};
     }
   }
   // the query loads complete here, before the first ring load: otherwise the compiler's
@@ -574,7 +606,7 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) asm volatile("" ::"v"(qf[rt][ks]));
+    for (int ks = 0; ks < KS; ++ks) asm volatile("" ::"v"(qf[rt][ks]));
 
   // ---- block table window: logical blocks [blk0 + wbase, blk0 + wbase + TBLW)
   const int blk0 = c_begin >> bs_shift;
@@ -596,17 +628,17 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
     }
   };
 
-  // ---- stage loads: instruction k of a stage: plane k / IPP, tokens 4(k % IPP) .. +3
+  // ---- stage loads: instruction k of a stage: plane k / IPP, tokens RPI(k % IPP) .. +RPI-1
   const uint64_t kbase = (uint64_t)(uintptr_t)((const T *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh);
   const uint64_t vbase = kbase + (uint64_t)a.kv_sv * sizeof(T);
-  const unsigned blk_bytes = (unsigned)(((int64_t)(BS - 1) * a.kv_ss + 128) * sizeof(T));
+  const unsigned blk_bytes = (unsigned)(((int64_t)(BS - 1) * a.kv_ss + DH) * sizeof(T));
   const unsigned ring_base = (unsigned)(uintptr_t)&ring[0][0];
   auto issue = [&](int gi) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
       const int k = wave * PER + i;
       const int plane = k / SH::IPP, tg = k % SH::IPP;
-      const int t0 = gi * ST + 4 * tg;                       // chunk-relative first token
+      const int t0 = gi * ST + RPI * tg;                     // chunk-relative first token
       const int bi = ((c_begin + t0) >> bs_shift) - blk0 - wbase;
       const int ph = __builtin_amdgcn_readfirstlane(tbl[bi]);
       const uint64_t bb = (plane ? vbase : kbase) + (uint64_t)(ph < 0 ? 0 : ph) * (uint64_t)a.kv_sb * sizeof(T);
@@ -615,24 +647,24 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
       rs[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(bb >> 32) & 0xffffu));
       rs[2] = __builtin_amdgcn_readfirstlane(ph < 0 ? 0 : (int)blk_bytes);
       rs[3] = 0x00020000;
-      const int tl = 4 * tg + (lane >> 4);                   // token within the stage
+      const int tl = RPI * tg + (lane >> NCS);               // token within the stage
       const int t = gi * ST + tl;
-      const int c = (lane & 15) ^ dswz(tl);                   // global chunk landing in slot lane%16
+      const int c = (lane & (NC - 1)) ^ dswz<DH>(tl);         // global chunk landing in slot lane%NC
       const unsigned voff = t < S ? (unsigned)((((c_begin + t) & (BS - 1)) * a.kv_ss + c * 8) * sizeof(T)) : 0xfffffff0u;
-      const unsigned dst = ring_base + (unsigned)((gi % NSTG) * SH::SBYTES + plane * ST * 256 + tg * 1024);
+      const unsigned dst = ring_base + (unsigned)((gi % NSTG) * SH::SBYTES + plane * ST * PB + tg * 1024);
       buf_lds16(rs, voff, __builtin_amdgcn_readfirstlane(dst));
     }
   };
 
   const float c2 = a.scale * 1.4426950408889634f;
   float m2[RT], lsum[RT];
-  f32x16 oacc[RT][4];
+  f32x16 oacc[RT][DT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     m2[rt] = -INFINITY;
     lsum[rt] = 0.f;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int e = 0; e < 16; ++e) oacc[rt][dt][e] = 0.f;
   }
@@ -646,9 +678,9 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) st.s[rt] = f32x16{};
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
+    for (int ks = 0; ks < KS; ++ks) {
       const int c = 2 * ks + lh;
-      const V8 kf = *(const V8 *)(kl + lcol * 256 + ((c ^ dswz(lcol)) << 4));
+      const V8 kf = *(const V8 *)(kl + lcol * PB + ((c ^ dswz<DH>(lcol)) << 4));
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
         if constexpr (__is_same(T, __bf16))
@@ -701,7 +733,7 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
       // O is rescaled only when some row of the tile raised its max
       if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0ull) {
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
           for (int e = 0; e < 16; ++e) oacc[rt][dt][e] *= alpha;
       }
@@ -709,14 +741,14 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
+      for (int dt = 0; dt < DT; ++dt) {
         const int d = 32 * dt + dgrp;
         const int cc = d >> 3, half = (d >> 2) & 1;
         const int t_lo = 16 * kb + 4 * lh + jq, t_hi = t_lo + 8;
         const dv4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (dv4s __attribute__((address_space(3))) *)(vl + t_lo * 256 + ((cc ^ dswz(t_lo)) << 4) + half * 8));
+            (dv4s __attribute__((address_space(3))) *)(vl + t_lo * PB + ((cc ^ dswz<DH>(t_lo)) << 4) + half * 8));
         const dv4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (dv4s __attribute__((address_space(3))) *)(vl + t_hi * 256 + ((cc ^ dswz(t_hi)) << 4) + half * 8));
+            (dv4s __attribute__((address_space(3))) *)(vl + t_hi * PB + ((cc ^ dswz<DH>(t_hi)) << 4) + half * 8));
         const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
         const V8 va = __builtin_bit_cast(V8, make_uint4(l2.x, l2.y, h2.x, h2.y));
 #pragma unroll
@@ -750,15 +782,15 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
       issue(gi);
     }
     const unsigned char *kl = ring[gs % NSTG];
-    const unsigned char *vl = kl + ST * 256;
+    const unsigned char *vl = kl + ST * PB;
     // the next slice's S^T chain is issued before this slice's softmax, so the matrix
     // core works while the VALU does the exp/max/sum
     Tiles st_cur = qk(kl);
 #pragma unroll
     for (int b = 0; b < ST / 32; ++b) {
       Tiles st_next;
-      if (b + 1 < ST / 32) st_next = qk(kl + (b + 1) * 32 * 256);
-      softmax_pv(st_cur, vl + b * 32 * 256, gs * ST + 32 * b);
+      if (b + 1 < ST / 32) st_next = qk(kl + (b + 1) * 32 * PB);
+      softmax_pv(st_cur, vl + b * 32 * PB, gs * ST + 32 * b);
       st_cur = st_next;
     }
   }
@@ -769,9 +801,9 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
     // ---- split: the chunk's partial (unnormalised O, max, sum) for the combine kernel
     if (a.nchunk > 1) {
       const int64_t pr = ((int64_t)p * a.rows_pad + row[rt]) * a.nchunk + chunk;
-      float *wo = a.ws_o + pr * 128;
+      float *wo = a.ws_o + pr * DH;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           f32x4 v;
@@ -786,7 +818,7 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
     float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n[rt] * a.o_sn +
                 (int64_t)(h * G + g[rt]) * a.o_sh;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int d0 = 32 * dt + 8 * i + 4 * lh;
@@ -805,6 +837,7 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
 // grid ceil(pairs*rows_pad/4), 256 threads: one wave per (pair, row) merging with
 // attn_merge_row.  The decode kernel (a.dyn) wrote a sequence of at most one chunk's tokens
 // itself: those rows are skipped.
+template <int DH>
 __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int pairs) {
   const int64_t id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (id >= (int64_t)pairs * a.rows_pad) return;
@@ -819,7 +852,7 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int pairs
   const int S_all = attn_seq_len(a, r);
   const int nc = a.dyn ? attn_dec_chunks(a, S_all) : min(a.nchunk, (S_all + a.tpc - 1) / a.tpc);
   if (a.dyn && nc <= 1) return;
-  attn_merge_row(a, id, nc,
+  attn_merge_row<DH>(a, id, nc,
                  (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * a.G + g) * a.o_sh,
                  (int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * a.G + g, lane);
 }
@@ -973,18 +1006,18 @@ static AttnSplit attn_split(int pairs, int N, int G, int span, int cus) {
   return sp;
 }
 
-static size_t attn_ws_bytes(int pairs, const AttnSplit &sp) {
+static size_t attn_ws_bytes(int pairs, const AttnSplit &sp, int D) {
   if (sp.nchunk <= 1) return 0;
-  return (size_t)pairs * sp.rows_pad * sp.nchunk * (128 + 2) * sizeof(float);
+  return (size_t)pairs * sp.rows_pad * sp.nchunk * (D + 2) * sizeof(float);
 }
 
-template <typename T, typename V8>
+template <typename T, typename V8, int DH>
 static int launch_attn_mfma(AttnArgs a, int bs_shift, void *ws, size_t ws_bytes, hipStream_t st) {
   const int pairs = a.L * a.R * a.Hkv;
   const int rtiles = (a.N * a.G + 31) / 32;
   const bool causal = a.kv_len != nullptr;
   AttnSplit sp = attn_split(pairs, a.N, a.G, a.max_blocks * a.BS, device_cus());
-  const size_t need = attn_ws_bytes(pairs, sp);
+  const size_t need = attn_ws_bytes(pairs, sp, DH);
   if (sp.nchunk > 1 && (!ws || ws_bytes < need)) {  // no (large enough) workspace: no split
     sp.nchunk = 1;
     sp.tpc = std::max(a.max_blocks * a.BS, 1);
@@ -992,22 +1025,22 @@ static int launch_attn_mfma(AttnArgs a, int bs_shift, void *ws, size_t ws_bytes,
   a.nchunk = sp.nchunk; a.tpc = sp.tpc; a.rows_pad = sp.rows_pad;
   a.dyn = rtiles == 1 && sp.nchunk > 1;
   a.ws_o = sp.nchunk > 1 ? (float *)ws : nullptr;
-  a.ws_ml = sp.nchunk > 1 ? (float *)((char *)ws + (size_t)pairs * sp.rows_pad * sp.nchunk * 128 * sizeof(float)) : nullptr;
+  a.ws_ml = sp.nchunk > 1 ? (float *)((char *)ws + (size_t)pairs * sp.rows_pad * sp.nchunk * DH * sizeof(float)) : nullptr;
   if (rtiles == 1) {
     const int grid = pairs * sp.nchunk;
     if (causal)
-      hipLaunchKernelGGL((attn_decode_kernel<T, V8, true>), dim3(grid), dim3(DW * 64), 0, st, a, pairs, bs_shift);
+      hipLaunchKernelGGL((attn_decode_kernel<T, V8, DH, true>), dim3(grid), dim3(DW * 64), 0, st, a, pairs, bs_shift);
     else
-      hipLaunchKernelGGL((attn_decode_kernel<T, V8, false>), dim3(grid), dim3(DW * 64), 0, st, a, pairs, bs_shift);
+      hipLaunchKernelGGL((attn_decode_kernel<T, V8, DH, false>), dim3(grid), dim3(DW * 64), 0, st, a, pairs, bs_shift);
   } else {
 #define ACTKV_ATTN(NWV, RTV)                                                                       \
   do {                                                                                             \
     const int grid = ((pairs + 7) / 8) * 8 * sp.ngroups * sp.nchunk;                               \
     if (causal)                                                                                    \
-      hipLaunchKernelGGL((attn_ring_kernel<T, V8, NWV, RTV, true>), dim3(grid), dim3(NWV * 64), \
+      hipLaunchKernelGGL((attn_ring_kernel<T, V8, DH, NWV, RTV, true>), dim3(grid), dim3(NWV * 64), \
                          0, st, a, pairs, sp.ngroups, bs_shift);                                   \
     else                                                                                           \
-      hipLaunchKernelGGL((attn_ring_kernel<T, V8, NWV, RTV, false>), dim3(grid), dim3(NWV * 64),\
+      hipLaunchKernelGGL((attn_ring_kernel<T, V8, DH, NWV, RTV, false>), dim3(grid), dim3(NWV * 64),\
                          0, st, a, pairs, sp.ngroups, bs_shift);                                   \
   } while (0)
   const RingCfg cfg = ring_cfg(rtiles);
@@ -1019,7 +1052,7 @@ static int launch_attn_mfma(AttnArgs a, int bs_shift, void *ws, size_t ws_bytes,
   int rc = actkv_check_launch();
   if (rc || sp.nchunk <= 1) return rc;
   const int64_t waves = (int64_t)pairs * sp.rows_pad;
-  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a, pairs);
+  hipLaunchKernelGGL(attn_combine_kernel<DH>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a, pairs);
   return actkv_check_launch();
 }
 
@@ -1086,13 +1119,15 @@ extern "C" int actkv_paged_attention(
                       kv_sl % 8 == 0 && kv_sv % 8 == 0 && kv_sb % 8 == 0 && kv_ss % 8 == 0 &&
                       kv_sh % 8 == 0 && o_sl % 4 == 0 && o_sr % 4 == 0 && o_sn % 4 == 0 && o_sh % 4 == 0;
   const bool mfma_ok = q_dtype == kv_dtype && (kv_dtype == ACTKV_BF16 || kv_dtype == ACTKV_F16) &&
-                       D == 128 && G >= 1 && vec_ok && bs_shift >= 0;
+                       (D == 128 || D == 64) && G >= 1 && vec_ok && bs_shift >= 0;
   if (mfma_ok) {
     void *ws = workspace;
     const size_t wb = workspace_bytes;
     if (kv_dtype == ACTKV_BF16)
-      return launch_attn_mfma<__bf16, bf16x8>(a, bs_shift, ws, wb, st);
-    return launch_attn_mfma<_Float16, f16x8>(a, bs_shift, ws, wb, st);
+      return D == 64 ? launch_attn_mfma<__bf16, bf16x8, 64>(a, bs_shift, ws, wb, st)
+                     : launch_attn_mfma<__bf16, bf16x8, 128>(a, bs_shift, ws, wb, st);
+    return D == 64 ? launch_attn_mfma<_Float16, f16x8, 64>(a, bs_shift, ws, wb, st)
+                   : launch_attn_mfma<_Float16, f16x8, 128>(a, bs_shift, ws, wb, st);
   }
   switch (q_dtype) {
     case ACTKV_F32: return dispatch_attn_generic<float>(a, kv_dtype, st);
@@ -1105,8 +1140,8 @@ extern "C" size_t actkv_paged_attention_workspace_size(int L, int R, int N, int 
                                                        int max_blocks, int block_size) {
   if (L < 1 || R < 1 || N < 1 || Hkv < 1 || Hq % Hkv != 0 || max_blocks < 1 || block_size < 1) return 0;
   const int G = Hq / Hkv;
-  if (D != 128 || G < 1) return 0;  // the float32 path does not split
+  if ((D != 128 && D != 64) || G < 1) return 0;  // the float32 path does not split
   if ((int64_t)max_blocks * block_size > 0x7fffffffLL) return 0;
   const int pairs = L * R * Hkv;
-  return attn_ws_bytes(pairs, attn_split(pairs, N, G, max_blocks * block_size, device_cus()));
+  return attn_ws_bytes(pairs, attn_split(pairs, N, G, max_blocks * block_size, device_cus()), D);
 }

@@ -299,7 +299,7 @@ size_t actkv_lrfu_workspace_size(int L, int R, int max_seq);
  *       block_table (ids outside the pool are skipped).
  * out : float32 [L, R, N, Hq, D], strides o_sl o_sr o_sn o_sh, unit last
  * lse : float32 [L, R, N, Hq], strides lse_sl lse_sr lse_sn, unit last
- * bf16/fp16 with D = 128 (any Hq/Hkv) run on the matrix cores
+ * bf16/fp16 with D = 128 or 64 (any Hq/Hkv) run on the matrix cores
  * (each probability enters the P.V product as a hi and a lo term in the cache
  * dtype, P = hi + lo to about 2^-16 relative, float32 accumulation); every other
  * case uses float32 dot products.  D <= 512.

@@ -84,6 +84,46 @@ def test_matrix_core_path_matches_the_oracle(lens, hq, hkv, n_q, dtype, causal):
         assert float(lse[0, 0, 0]) == -math.inf and torch.equal(out[0, 0].cpu(), torch.zeros(hq, 128))
 
 
+@pytest.mark.parametrize("lens,hq,hkv,n_q,dtype,causal,bs,split", [
+    ([700, 1500], 32, 8, 1, torch.bfloat16, False, 16, True),    # decode: 4 real rows
+    ([3000, 47], 64, 8, 4, torch.bfloat16, True, 16, True),      # GQA 8 decode tile, causal
+    ([3000, 47], 64, 8, 4, torch.float16, True, 16, False),      # the same in one pass, fp16
+    ([900], 16, 8, 20, torch.float16, False, 16, True),          # GQA 2, 40 rows: 2-wave ring
+    ([2000, 1337], 32, 8, 30, torch.bfloat16, True, 16, True),   # 120 rows: 4-wave ring
+    ([640], 32, 8, 200, torch.bfloat16, True, 16, True),         # 800 rows: 8-wave ring groups
+    ([640, 2200], 32, 8, 200, torch.bfloat16, True, 16, False),  # the same in one pass
+    ([2500], 64, 8, 50, torch.float16, False, 32, True),         # GQA 8, 400 rows, block 32
+    ([5000, 700], 8, 2, 48, torch.bfloat16, True, 256, True),    # chunk starts inside blocks
+    ([4400, 1], 56, 8, 1, torch.bfloat16, False, 64, True),      # GQA 7 decode, a one-token request
+    ([1800, 333], 24, 8, 30, torch.bfloat16, True, 16, True),    # GQA 3, 90 rows
+])
+def test_matrix_core_path_head_dim_64(monkeypatch, lens, hq, hkv, n_q, dtype, causal, bs, split):
+    """Head dim 64 on the matrix-core kernels (128-byte token rows: eight rows per 16-byte
+    load instruction, their own LDS swizzle, two 32-dim output tiles), every kernel form,
+    with and without the token split, against the oracle at the same tolerances."""
+    from actkv import _hip
+    cache = _cache(lens, hkv=hkv, d=64, bs=bs, dtype=dtype, seed=len(lens) * 100 + n_q + bs)
+    reqs = list(range(len(lens)))
+    g = torch.Generator().manual_seed(n_q + 64)
+    q = torch.randn(len(lens), n_q, hq, 64, generator=g).to(dtype)
+    kv_len = None
+    if causal:
+        kv_len = torch.stack([torch.randint(0, S + 8, (n_q,), generator=g) for S in lens]).to(torch.int32)
+        kv_len[0, 0] = 0                                           # a query that sees nothing
+    lib = _hip.lib()
+    mb = max(len(t) for t in cache.tables.values())
+    if split:
+        assert lib.actkv_paged_attention_workspace_size(1, len(lens), n_q, hq, hkv, 64, mb, bs) > 0
+    else:
+        monkeypatch.setattr(lib, "actkv_paged_attention_workspace_size", lambda *a: 0)
+    out, lse = cache.decode_attention(reqs, q.cuda(), kv_len=None if kv_len is None else kv_len.cuda())
+    want_out, want_lse = _oracle(cache, reqs, q, 0, kv_len=None if kv_len is None else kv_len.tolist())
+    torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
+    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=_atol(dtype))
+    if causal:
+        assert float(lse[0, 0, 0]) == -math.inf and torch.equal(out[0, 0].cpu(), torch.zeros(hq, 64))
+
+
 def test_reference_signature_one_query_per_request():
     """q [R, Hq, D] -> out [R, Hq, D], lse [R, Hq], as paged_decode_attention_ref."""
     cache = _cache([333, 1024, 17], seed=5)
@@ -127,7 +167,7 @@ def test_empty_sequence_gives_minus_inf_and_zero(n0, n_q):
 
 
 @pytest.mark.parametrize("d,hq,hkv,bs,dtype", [
-    (64, 8, 2, 16, torch.bfloat16),      # head_dim 64
+    (96, 8, 2, 16, torch.bfloat16),      # head_dim 96
     (32, 4, 2, 16, torch.float32),       # float32 cache
     (128, 12, 4, 12, torch.float16),     # GQA 3, block size 12
 ])

@@ -103,3 +103,44 @@ def test_random_shapes_with_other_groups_match_the_oracle(seed):
         kv_len=None if kv_len is None else kv_len.tolist(), n_valid=None if n_valid is None else n_valid.tolist())
     torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
     torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=2e-4)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_shapes_at_head_dim_64_match_the_oracle(seed):
+    """The same sweep at head dim 64 (Hq/Hkv 32/8, 64/8, 16/2, 8/8, 56/8): decode tiles and
+    multi-tile row groups, blocks 16-64, a table up to twice as wide as the longest request."""
+    rnd = random.Random(11000 + seed)
+    n_req = rnd.randint(1, 4)
+    lens = [rnd.choice([0, rnd.randint(1, 200), rnd.randint(200, 5000)]) for _ in range(n_req)]
+    if max(lens) == 0:
+        lens[0] = rnd.randint(1, 3000)
+    hq, hkv = rnd.choice([(32, 8), (64, 8), (16, 2), (8, 8), (56, 8)])
+    n_q = rnd.choice([1, rnd.randint(2, 4), rnd.randint(5, 60)])
+    dtype, bs = rnd.choice([torch.bfloat16, torch.float16]), rnd.choice([16, 32, 64])
+    causal, partial, widen = rnd.random() < 0.5, rnd.random() < 0.3, rnd.choice([1, 2])
+    print(f"case {seed}: lens {lens} hq {hq} hkv {hkv} n_q {n_q} {dtype} bs {bs} causal {causal} "
+          f"partial {partial} widen {widen}", flush=True)
+    g = torch.Generator().manual_seed(13000 + seed)
+    nb = sum(math.ceil(n / bs) for n in lens) + 3
+    cache = PagedKVCache(nb, bs, hkv, 64, n_layers=1, dtype=dtype, device="cuda")
+    cache.free = torch.randperm(nb, generator=g).tolist()
+    for r, n in enumerate(lens):
+        cache.append(r, torch.randn(1, n, hkv, 64, generator=g).to(dtype).cuda(),
+                     torch.randn(1, n, hkv, 64, generator=g).to(dtype).cuda())
+    reqs = list(range(len(lens)))
+    seq, bt = cache._device_tables(reqs)
+    table = torch.zeros(len(lens), bt.shape[1] * widen, dtype=torch.int32, device="cuda")
+    table[:, : bt.shape[1]] = bt
+    q = torch.randn(len(lens), n_q, hq, 64, generator=g).to(dtype)
+    kv_len = (torch.stack([torch.randint(0, S + 4, (n_q,), generator=g) for S in lens]).to(torch.int32)
+              if causal else None)
+    n_valid = (torch.tensor([random.Random(seed + r).randint(0, n_q) for r in reqs], dtype=torch.int32)
+               if partial else None)
+    out, lse = paged_decode_attention(q.cuda(), cache.kv[0], table, seq,
+                                      kv_len=None if kv_len is None else kv_len.cuda(),
+                                      n_valid=None if n_valid is None else n_valid.cuda())
+    want_out, want_lse = ref.paged_attention(
+        q.float(), cache.kv[0].cpu().float(), [cache.tables[r] for r in reqs], [cache.seq_used[r] for r in reqs],
+        kv_len=None if kv_len is None else kv_len.tolist(), n_valid=None if n_valid is None else n_valid.tolist())
+    torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
+    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=2e-4)   # P as hi + lo terms

@@ -420,19 +420,21 @@ def test_action_scores_leave_tokens_of_out_of_pool_blocks_untouched(dtype, hq, h
         torch.testing.assert_close(got[r][:, keep], out_o[r][:, keep], rtol=rtol, atol=1e-6)
 
 
-@pytest.mark.parametrize("hq,hkv,n_q,half", [
-    (32, 8, 16, 0),      # 64 rows: 8 KV heads per workgroup
-    (32, 8, 32, 1),      # 128 rows: 4 KV heads per workgroup
-    (8, 8, 9, 1),        # group 1, 9 rows: 8 heads per workgroup
-    (16, 4, 30, 0),      # group 4 over 4 KV heads, 120 rows: 4 heads per workgroup
+@pytest.mark.parametrize("hq,hkv,n_q,half,d", [
+    (32, 8, 16, 0, 128),      # 64 rows: 8 KV heads per workgroup
+    (32, 8, 32, 1, 128),      # 128 rows: 4 KV heads per workgroup
+    (8, 8, 9, 1, 128),        # group 1, 9 rows: 8 heads per workgroup
+    (16, 4, 30, 0, 128),      # group 4 over 4 KV heads, 120 rows: 4 heads per workgroup
+    (32, 8, 16, 1, 64),       # head dim 64, 64 rows: 8 KV heads per workgroup
+    (8, 8, 9, 0, 64),         # head dim 64, group 1, 9 rows
 ])
-def test_action_scores_heads_per_workgroup_with_strided_heads(hq, hkv, n_q, half):
+def test_action_scores_heads_per_workgroup_with_strided_heads(hq, hkv, n_q, half, d):
     """Small query tiles score several KV heads of the same tokens in one workgroup, reading
     each token's heads side by side.  K here is a view with a head stride of 2 x head_dim
-    (every other 128-element piece of a wider row, starting at piece `half`), so the heads
-    are not contiguous; with ragged query counts, causal limits and two out-of-pool table
-    entries, against the oracle's folds."""
-    d, bs, lens = 128, 16, [700, 333, 1400]
+    (every other head_dim-element piece of a wider row, starting at piece `half`), so the
+    heads are not contiguous; with ragged query counts, causal limits and two out-of-pool
+    table entries, against the oracle's folds."""
+    bs, lens = 16, [700, 333, 1400]
     R = len(lens)
     g = torch.Generator().manual_seed(40 + n_q)
     nb = sum(-(-s // bs) for s in lens) + 5

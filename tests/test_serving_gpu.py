@@ -98,8 +98,9 @@ def test_fp32_logits_equal_eager_dynamic_cache():
     assert all(sess.kv.seq_used[r] == n0 + steps for r in range(B))
 
 
-def test_bf16_logits_follow_fp32_attention():
-    model = _model(torch.bfloat16)
+@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 128), (16, 2, 64)])   # GQA 4 at head dim 128; GQA 8 at 64
+def test_bf16_logits_follow_fp32_attention(hq, hkv, d):
+    model = _model(torch.bfloat16, hq=hq, hkv=hkv, d=d)
     B, n0, steps = 2, 300, 8
     prompts, toks = _tokens(B, n0, steps, seed=4)
     want = _reference_run(model, "fp32_ref", prompts, toks)

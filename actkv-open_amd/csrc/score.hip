@@ -73,11 +73,17 @@ __device__ __forceinline__ float vmax(float x, float y) { return __builtin_eleme
 // W = 16 or 4).  Issued as assembly so the compiler's wait insertion does not track them:
 // it cannot tell which LDS array such a load writes, and waits for all of them (vmcnt(0))
 // before any later LDS access.  Every wait for these loads is explicit in the kernel.
+// M0 carries the LDS address; the compiler reserves M0 (a clobber of it is not honoured),
+// so the statement saves and restores it.
 __device__ __forceinline__ void load_lds16(const void *gptr, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(gptr), "s"(lds_addr) : "memory", "m0");
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved) : "v"(gptr), "s"(lds_addr) : "memory");
 }
 __device__ __forceinline__ void load_lds4(const void *gptr, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" :: "v"(gptr), "s"(lds_addr) : "memory", "m0");
+  uint32_t saved;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(saved) : "v"(gptr), "s"(lds_addr) : "memory");
 }
 __device__ __forceinline__ uint32_t lds_address(const void *p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;

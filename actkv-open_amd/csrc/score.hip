@@ -21,10 +21,13 @@
 // Groups of 8 and 16 heads run on the query-register kernel only: a query's rows
 // span both halves of a wave, and their max is taken across the halves.  Groups of
 // 3, 5-7 and 9-15 take that kernel too, laid out as 4, 8 and 16 rows per query
-// (padding rows load no query and start at -inf).  The generic kernel covers every
-// other shape/dtype (fp32 caches, head_dim not 128, groups above 16) and follows the
+// (padding rows load no query and start at -inf).  The generic kernels cover every
+// other shape/dtype (fp32 caches or queries, head dims other than 64 and 128, groups
+// above 16, blocks that are not a power of two from 16 up) in float32 and follow the
 // reference fold order exactly: for each query in turn,
-// out += (p - out) / (n_seen + n + 1).
+// out += (p - out) / (n_seen + n + 1).  score_generic_rows_kernel (head dims that are a
+// multiple of 4 up to 512) keeps a chunk of query rows' dot products in registers;
+// score_generic_kernel takes the rest one query at a time.
 #include "common.h"
 
 #include <algorithm>
@@ -156,6 +159,110 @@ __global__ void __launch_bounds__(256) score_generic_kernel(ScoreArgs a) {
         }
       }
       acc = acc + (p - acc) / (float)(n0 + n + 1);
+    }
+  }
+  if (valid) *optr = acc;
+}
+
+// ------------------------------------------------------------------ generic, query rows in chunks
+// The same computation and fold order as score_generic_kernel, for head dims that are a
+// multiple of 4 up to 512: grid (ceil(span/256), L*R*Hkv), 256 threads, one thread per
+// token slot.  The query rows (n, g) go through LDS ROWS at a time (qc whole queries of
+// gc group heads each: gc = min(G, ROWS), qc = ROWS / gc; a group wider than ROWS takes
+// one query per chunk and several chunks of heads, the running max carried between
+// them).  A thread walks its K row once per chunk, four dims per step, and keeps the
+// chunk's ROWS dot products in registers: K is read once per ROWS rows instead of once
+// per row, and the dot products are independent FMA chains.  Each dot product still
+// sums its dims in order, so the scores equal score_generic_kernel's.
+template <typename QT, typename KT, int ROWS>
+__global__ void __launch_bounds__(256) score_generic_rows_kernel(ScoreArgs a, int gc) {
+  extern __shared__ __attribute__((aligned(16))) float qrows[];  // [ROWS][D] fp32, [ROWS] lse, [ROWS] kv_len
+  const int pair = blockIdx.y;
+  const int h = pair % a.Hkv;
+  const int r = (pair / a.Hkv) % a.R;
+  const int l = pair / (a.Hkv * a.R);
+  const int S = seq_len_of(a, r);
+  if ((int64_t)blockIdx.x * 256 >= S) return;
+  const int nq_all = a.n_valid ? min(max(a.n_valid[r], 0), a.N) : a.N;
+  if (nq_all == 0) return;
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  const int G = a.G, D = a.D;
+  const int qc = ROWS / gc;
+  float *lse_s = qrows + ROWS * D;
+  int *kvl_s = (int *)(lse_s + ROWS);
+
+  bool valid = t < S;
+  const KT *krow = nullptr;
+  if (valid) {
+    const int64_t phys = a.bt[(int64_t)r * a.bt_sr + t / a.BS];
+    if (phys < 0 || phys >= a.num_blocks) {
+      valid = false;
+    } else {
+      krow = (const KT *)a.kv + (int64_t)l * a.kv_sl + phys * a.kv_sb +
+             (int64_t)(t % a.BS) * a.kv_ss + (int64_t)h * a.kv_sh;
+    }
+  }
+  float *optr = a.out + (int64_t)l * a.out_sl + (int64_t)r * a.out_sr + (int64_t)h * a.out_sh + t;
+  float acc = valid ? *optr : 0.f;
+  const int n0 = a.n_seen[r];
+  const QT *qbase = (const QT *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr;
+  const float *lbase = a.lse + (int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr;
+
+  float carry = -INFINITY;  // max over the earlier head chunks of a group wider than ROWS
+  for (int nc = 0; nc < nq_all; nc += qc) {
+    const int qn = min(qc, nq_all - nc);
+    for (int g0 = 0; g0 < G; g0 += gc) {
+      const int gn = min(gc, G - g0);
+      const bool last = g0 + gc >= G;
+      __syncthreads();
+      for (int i = threadIdx.x; i < ROWS * D; i += 256) {
+        const int row = i / D, d = i % D, j = row / gc, g = row % gc;
+        qrows[i] = j < qn && g < gn
+                       ? (float)qbase[(int64_t)(nc + j) * a.q_sn + (int64_t)(h * G + g0 + g) * a.q_sh + d]
+                       : 0.f;
+      }
+      if (threadIdx.x < ROWS) {
+        const int row = threadIdx.x, j = row / gc, g = row % gc;
+        lse_s[row] = j < qn && g < gn ? lbase[(int64_t)(nc + j) * a.lse_sn + h * G + g0 + g] : 0.f;
+        kvl_s[row] = row < qn && a.kv_len ? a.kv_len[(int64_t)r * a.N + nc + row] : 0x7fffffff;  // query row's limit
+      }
+      __syncthreads();
+      if (!valid) continue;
+      float dot[ROWS];
+#pragma unroll
+      for (int i = 0; i < ROWS; ++i) dot[i] = 0.f;
+      for (int d = 0; d < D; d += 4) {
+        const float k0 = (float)krow[d], k1 = (float)krow[d + 1], k2 = (float)krow[d + 2], k3 = (float)krow[d + 3];
+#pragma unroll
+        for (int i = 0; i < ROWS; ++i) {
+          const float4 qv = *(const float4 *)&qrows[i * D + d];
+          dot[i] = fmaf(k0, qv.x, dot[i]);
+          dot[i] = fmaf(k1, qv.y, dot[i]);
+          dot[i] = fmaf(k2, qv.z, dot[i]);
+          dot[i] = fmaf(k3, qv.w, dot[i]);
+        }
+      }
+      // rows in (query, head) order: the group max, then each whole query folds in turn
+      float cur = carry;
+      int k = 0, j = 0;
+#pragma unroll
+      for (int i = 0; i < ROWS; ++i) {
+        if (k < gn) cur = vmax(cur, dot[i] * a.scale - lse_s[i]);
+        if (++k == gc) {
+          if (j < qn) {
+            if (last) {
+              const float p = t < kvl_s[j] ? expf(cur) : 0.f;
+              acc = acc + (p - acc) / (float)(n0 + nc + j + 1);
+              carry = -INFINITY;
+            } else {
+              carry = cur;
+            }
+          }
+          k = 0;
+          cur = -INFINITY;
+          ++j;
+        }
+      }
     }
   }
   if (valid) *optr = acc;
@@ -1033,8 +1140,22 @@ static int launch_mfma_groups(const ScoreArgs &a, int G, int bs_shift, hipStream
                 : launch_mfma<T, V8, 1, DH>(a, bs_shift, st);
 }
 
+template <typename QT, typename KT, int ROWS>
+static int launch_generic_rows(const ScoreArgs &a, hipStream_t st) {
+  const int span = a.max_blocks * a.BS;
+  dim3 grid((span + 255) / 256, a.L * a.R * a.Hkv);
+  const size_t shm = (size_t)(ROWS * a.D + 2 * ROWS) * sizeof(float);
+  hipLaunchKernelGGL((score_generic_rows_kernel<QT, KT, ROWS>), grid, dim3(256), shm, st, a, std::min(a.G, ROWS));
+  return actkv_check_launch();
+}
+
 template <typename QT, typename KT>
 static int launch_generic(const ScoreArgs &a, hipStream_t st) {
+  // head dims that are a multiple of 4 up to 512: query rows in chunks (at most 32 KiB of LDS)
+  if (a.D % 4 == 0 && a.D <= 512)
+    return a.D <= 128 ? launch_generic_rows<QT, KT, 64>(a, st)
+         : a.D <= 256 ? launch_generic_rows<QT, KT, 32>(a, st)
+                      : launch_generic_rows<QT, KT, 16>(a, st);
   const int span = a.max_blocks * a.BS;
   dim3 grid((span + 255) / 256, a.L * a.R * a.Hkv);
   const size_t shm = (size_t)(a.G * a.D + a.G) * sizeof(float);

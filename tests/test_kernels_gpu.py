@@ -85,6 +85,43 @@ def test_action_scores_matches_oracle(lens, hq, hkv, d, bs, dtype):
     assert torch.equal(n_k.cpu(), n_o)
 
 
+@pytest.mark.parametrize("hq,hkv,d,bs,qdt,kdt,n_q", [
+    (6, 2, 24, 16, torch.float32, torch.float32, 50),      # G 3: 21 queries per chunk of 64 rows, 3 chunks
+    (96, 1, 32, 16, torch.bfloat16, torch.bfloat16, 3),     # G 96 > 64 rows: head chunks 64 + 32, max carried
+    (40, 1, 512, 16, torch.float16, torch.float16, 2),      # head dim 512: 16-row chunks, heads 16 + 16 + 8
+    (16, 8, 256, 16, torch.bfloat16, torch.bfloat16, 20),   # head dim 256, G 2 (Gemma shape): 32-row chunks
+    (32, 8, 128, 16, torch.float32, torch.bfloat16, 9),     # float32 queries on a bf16 cache
+    (10, 2, 36, 12, torch.float16, torch.float16, 13),      # G 5, head dim 36, block 12
+    (4, 2, 30, 16, torch.float32, torch.float32, 7),        # head dim 30 (not a multiple of 4): row-at-a-time kernel
+])
+def test_action_scores_generic_query_row_chunks(hq, hkv, d, bs, qdt, kdt, n_q):
+    """The float32 path for shapes off the matrix cores walks the query rows (n, g) through LDS
+    in chunks and keeps a chunk's dot products in registers: partial chunks, groups wider than
+    a chunk (the max carried across head chunks), causal limits and partial query counts, against
+    the oracle's folds."""
+    lens = [300, 77]
+    cache = _filled_cache(lens, bs=bs, hkv=hkv, d=d, dtype=kdt, seed=hq + d)
+    reqs = list(range(len(lens)))
+    bt, seq = cache.block_table(reqs), cache.seq_tensor(reqs)
+    width = bt.shape[1] * bs
+    kv0 = cache.kv[0].cpu()
+    tables = [cache.tables[r] for r in reqs]
+    g = torch.Generator().manual_seed(d + n_q)
+    q = (torch.randn(len(reqs), n_q, hq, d, generator=g) * 0.5).to(qdt)
+    lse = torch.stack([ref.decode_lse(q[:, n].float(), kv0, tables, lens) for n in range(n_q)], 1)
+    n_valid = torch.tensor([n_q, max(1, n_q - 2)], dtype=torch.int32)
+    kv_len = torch.stack([torch.randint(0, s + 3, (n_q,), generator=g) for s in lens]).to(torch.int32)
+    out0 = torch.rand(len(reqs), hkv, width, generator=g)
+    n0 = torch.tensor([2, 0], dtype=torch.int32)
+    out_k, n_k = out0.cuda(), n0.cuda()
+    action_scores(q.cuda(), cache.kv[0], bt, seq, lse.cuda(), out_k, n_k, n_valid=n_valid.cuda(), kv_len=kv_len.cuda())
+    out_o, n_o = out0.clone(), n0.clone()
+    ref.action_scores_nfold(q.float(), kv0, tables, lens, lse, out_o, n_o, n_valid=n_valid, kv_len=kv_len)
+    rtol = 1e-4 if kdt == torch.float32 and qdt == torch.float32 else 1e-3
+    torch.testing.assert_close(out_k.cpu(), out_o, rtol=rtol, atol=1e-6)
+    assert torch.equal(n_k.cpu(), n_o)
+
+
 @pytest.mark.parametrize("n_q,hq,hkv,dtype", [(37, 32, 8, torch.bfloat16), (129, 32, 8, torch.bfloat16),
                                               (40, 16, 8, torch.float16), (9, 6, 3, torch.float32),
                                               (300, 16, 8, torch.float16), (600, 8, 8, torch.bfloat16),

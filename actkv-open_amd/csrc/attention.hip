@@ -38,9 +38,10 @@
 // instruction then moves eight rows instead of four, the rows' eight 16-byte chunks are
 // swizzled with their own pattern (dswz), and two 32-dim output tiles replace four.
 //
-// Generic path (any other dtype / head_dim): one workgroup per query row,
-// float32 dot products, an online max/sum pass for lse and a second pass that
-// accumulates out through LDS-staged probabilities.
+// Generic path (any other dtype / head_dim up to 512 / block size): float32, up to 16
+// query rows of one KV head per workgroup (a decode step's GQA group reads K and V
+// once), one pass with an online max and sum, token chunks merged by the same combine
+// launch.  Described at attn_generic_kernel.
 #include "common.h"
 
 #include <algorithm>
@@ -148,6 +149,38 @@ __device__ __forceinline__ void attn_merge_row(const AttnArgs &a, int64_t id, in
   float *op = a.out + o_off;
   op[lane] = o0 * inv;
   if constexpr (DH == 128) op[64 + lane] = o1 * inv;
+  if (lane == 0) a.lse[lse_off] = Lsum > 0.f ? (M + __log2f(Lsum)) * 0.6931471805599453f : -INFINITY;
+}
+
+// The same merge for any head dim (the float32 path's chunks): the chunk weights are
+// recomputed for each 64-dim slice of the row.
+__device__ __forceinline__ void attn_merge_row_any(const AttnArgs &a, int64_t id, int nc, int64_t o_off,
+                                                   int64_t lse_off, int lane) {
+  const int D = a.D;
+  const float *ml = a.ws_ml + id * a.nchunk * 2;
+  const float *wo = a.ws_o + id * a.nchunk * D;
+  float M = -INFINITY;
+  for (int c = lane; c < nc; c += 64) M = fmaxf(M, ml[2 * c]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 64));
+  const float Ms = M == -INFINITY ? 0.f : M;
+  float Lsum = 0.f;
+  for (int c0 = 0; c0 < nc; c0 += 64) {
+    const int c = c0 + lane;
+    float lw = c < nc ? exp2f(ml[2 * c] - Ms) * ml[2 * c + 1] : 0.f;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) lw += __shfl_xor(lw, o, 64);
+    Lsum += lw;
+  }
+  const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
+  float *op = a.out + o_off;
+  for (int d0 = 0; d0 < D; d0 += 64) {
+    const int d = d0 + lane;
+    float o = 0.f;
+    if (d < D)
+      for (int c = 0; c < nc; ++c) o += exp2f(ml[2 * c] - Ms) * wo[(int64_t)c * D + d];
+    if (d < D) op[d] = o * inv;
+  }
   if (lane == 0) a.lse[lse_off] = Lsum > 0.f ? (M + __log2f(Lsum)) * 0.6931471805599453f : -INFINITY;
 }
 
@@ -835,8 +868,8 @@ attn_ring_kernel(AttnArgs a, int pairs, int ngroups, int bs_shift) {
 
 // ------------------------------------------------------------------ split combine
 // grid ceil(pairs*rows_pad/4), 256 threads: one wave per (pair, row) merging with
-// attn_merge_row.  The decode kernel (a.dyn) wrote a sequence of at most one chunk's tokens
-// itself: those rows are skipped.
+// attn_merge_row (DH = 0: attn_merge_row_any, the float32 path's head dims).  The decode
+// kernel (a.dyn) wrote a sequence of at most one chunk's tokens itself: those rows are skipped.
 template <int DH>
 __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int pairs) {
   const int64_t id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -852,91 +885,182 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int pairs
   const int S_all = attn_seq_len(a, r);
   const int nc = a.dyn ? attn_dec_chunks(a, S_all) : min(a.nchunk, (S_all + a.tpc - 1) / a.tpc);
   if (a.dyn && nc <= 1) return;
-  attn_merge_row<DH>(a, id, nc,
-                 (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * a.G + g) * a.o_sh,
-                 (int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * a.G + g, lane);
+  const int64_t o_off = (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * a.G + g) * a.o_sh;
+  const int64_t lse_off = (int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * a.G + g;
+  if constexpr (DH == 0)
+    attn_merge_row_any(a, id, nc, o_off, lse_off, lane);
+  else
+    attn_merge_row<DH>(a, id, nc, o_off, lse_off, lane);
 }
 
 // ------------------------------------------------------------------ generic path
-// grid L*R*N*Hq, 256 threads: one query row per workgroup.
+// Any dtype pairing, head dims up to 512, any block size.  grid pairs * ngroups * nchunk,
+// 256 threads: a workgroup takes up to AG_ROWS query rows (n, g) of one (layer, request, KV
+// head) pair -- a decode step's whole GQA group, so K and V are read once for all of its
+// rows -- over one token chunk, 256 tokens at a time:
+//   thread j: s_i = q_i . k_(t0+j) for each row i (the rows from LDS, the dot products in
+//   registers as independent FMA chains), the tile's max per row through wave reductions and
+//   LDS, p_i,j into LDS; then thread d: O_i[d] += sum_j p_i,j v_(t0+j)[d] (V rows read
+//   coalesced) and l_i += sum_j p_i,j, the same sum in every thread.
+// Online softmax in log2 units, as the matrix-core kernels; a split sequence's chunks go
+// through the same workspace layout ([pair][row][chunk][D] and (max, sum)) and the combine
+// launch.  Tokens in blocks the table marks invalid, and tokens a row does not see, get
+// probability 0 (the V rows of invalid blocks are not read).
+constexpr int AG_ROWS = 16;
 template <typename QT, typename KT>
-__global__ void __launch_bounds__(256) attn_generic_kernel(AttnArgs a) {
-  extern __shared__ float sm[];  // q [D], then p [256]
-  float *qs = sm, *ps = sm + a.D;
-  __shared__ float red_m[4], red_l[4];
-  const int64_t id = blockIdx.x;
-  const int hq = (int)(id % a.Hq);
-  const int n = (int)((id / a.Hq) % a.N);
-  const int r = (int)((id / ((int64_t)a.Hq * a.N)) % a.R);
-  const int l = (int)(id / ((int64_t)a.Hq * a.N * a.R));
-  if (n >= attn_nq(a, r)) return;
-  const int S = attn_seq_len(a, r);
-  const int lim = attn_lim(a, r, n, S);
-  const int h = hq / a.G, D = a.D, tid = threadIdx.x;
-  const QT *qp = (const QT *)a.q + (int64_t)l * a.q_sl + (int64_t)r * a.q_sr + (int64_t)n * a.q_sn + (int64_t)hq * a.q_sh;
-  for (int d = tid; d < D; d += 256) qs[d] = (float)qp[d];
+__global__ void __launch_bounds__(256) attn_generic_kernel(AttnArgs a, int pairs, int ngroups) {
+  extern __shared__ __attribute__((aligned(16))) float sm[];  // q rows [AG_ROWS][DP], then p [AG_ROWS][256]
+  __shared__ float red[AG_ROWS][4];
+  __shared__ int lims[AG_ROWS];
+  __shared__ int64_t offs[256];
+  const int D = a.D, DP = (D + 3) & ~3;
+  float *qs = sm, *ps = sm + AG_ROWS * DP;
+  const int bid = blockIdx.x;
+  const int chunk = bid % a.nchunk;
+  const int grp = (bid / a.nchunk) % ngroups;
+  const int p = bid / (a.nchunk * ngroups);
+  if (p >= pairs) return;
+  const int h = p % a.Hkv;
+  const int r = (p / a.Hkv) % a.R;
+  const int l = p / (a.Hkv * a.R);
+  const int G = a.G;
+  const int nq = attn_nq(a, r);
+  const int row0 = grp * AG_ROWS;
+  if (row0 >= nq * G) return;
+  const int nrows = min(AG_ROWS, nq * G - row0);
+  const int S_all = attn_seq_len(a, r);
+  if (a.nchunk > 1 && chunk * a.tpc >= S_all) return;   // the combine reads only chunks with tokens
+  const int c_begin = min(chunk * a.tpc, S_all);
+  const int c_end = a.nchunk > 1 ? min(S_all, c_begin + a.tpc) : S_all;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  for (int i = tid; i < AG_ROWS * DP; i += 256) {
+    const int ri = i / DP, d = i % DP, row = row0 + ri;
+    float v = 0.f;
+    if (ri < nrows && d < D)
+      v = (float)((const QT *)a.q)[(int64_t)l * a.q_sl + (int64_t)r * a.q_sr + (int64_t)(row / G) * a.q_sn +
+                                   (int64_t)(h * G + row % G) * a.q_sh + d];
+    qs[i] = v;
+  }
+  if (tid < AG_ROWS) lims[tid] = tid < nrows ? min(attn_lim(a, r, (row0 + tid) / G, S_all), c_end) : c_begin;
   __syncthreads();
+  int t_end = c_begin;  // the last token any row of the workgroup sees, plus one
+  for (int i = 0; i < nrows; ++i) t_end = max(t_end, lims[i]);
+
   const KT *kplane = (const KT *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh;
   const KT *vplane = kplane + a.kv_sv;
-  auto row_off = [&](int t) -> int64_t {
-    const int ph = attn_phys(a, r, t / a.BS);
-    return ph < 0 ? -1 : (int64_t)ph * a.kv_sb + (int64_t)(t % a.BS) * a.kv_ss;
-  };
-  auto logit = [&](int t) -> float {
-    const int64_t off = row_off(t);
-    if (off < 0) return -INFINITY;  // a token in a block the table marks invalid
-    float s = 0.f;
-    for (int d = 0; d < D; ++d) s = fmaf(qs[d], (float)kplane[off + d], s);
-    return s * a.scale;
-  };
-  // pass 1: online max / sum per thread, then over the workgroup
-  float m = -INFINITY, sum = 0.f;
-  for (int t = tid; t < lim; t += 256) {
-    const float x = logit(t);
-    if (x == -INFINITY) continue;
-    if (x > m) { sum = sum * expf(m - x) + 1.f; m = x; }
-    else sum += expf(x - m);
-  }
-  for (int o = 32; o > 0; o >>= 1) {
-    const float mo = __shfl_xor(m, o, 64), so = __shfl_xor(sum, o, 64);
-    const float mn = fmaxf(m, mo);
-    sum = (m == -INFINITY ? 0.f : sum * expf(m - mn)) + (mo == -INFINITY ? 0.f : so * expf(mo - mn));
-    m = mn;
-  }
-  if ((tid & 63) == 0) { red_m[tid >> 6] = m; red_l[tid >> 6] = sum; }
-  __syncthreads();
-  float M = -INFINITY;
-  for (int w = 0; w < 4; ++w) M = fmaxf(M, red_m[w]);
-  float Lsum = 0.f;
-  for (int w = 0; w < 4; ++w) Lsum += red_m[w] == -INFINITY ? 0.f : red_l[w] * expf(red_m[w] - M);
-  // pass 2: out = sum_t p_t v_t / Lsum, 256 tokens at a time through LDS
-  float acc0 = 0.f, acc1 = 0.f;  // dims tid and tid + 256 (D <= 512)
-  for (int t0 = 0; t0 < lim; t0 += 256) {
-    __syncthreads();
+  const float c2 = a.scale * 1.4426950408889634f;
+  float m2[AG_ROWS], lsum[AG_ROWS], acc0[AG_ROWS], acc1[AG_ROWS];
+#pragma unroll
+  for (int i = 0; i < AG_ROWS; ++i) { m2[i] = -INFINITY; lsum[i] = 0.f; acc0[i] = 0.f; acc1[i] = 0.f; }
+
+  for (int t0 = c_begin; t0 < t_end; t0 += 256) {
     const int t = t0 + tid;
-    float pt = 0.f;
-    if (t < lim) {
-      const float x = logit(t);
-      pt = x == -INFINITY ? 0.f : expf(x - M);
+    int64_t off = -1;
+    if (t < t_end) {
+      const int ph = attn_phys(a, r, t / a.BS);
+      if (ph >= 0) off = (int64_t)ph * a.kv_sb + (int64_t)(t % a.BS) * a.kv_ss;
     }
-    ps[tid] = pt;
+    offs[tid] = off;
+    float x[AG_ROWS];
+#pragma unroll
+    for (int i = 0; i < AG_ROWS; ++i) x[i] = 0.f;
+    if (off >= 0) {
+      const KT *kr = kplane + off;
+      int d = 0;
+      for (; d + 4 <= D; d += 4) {
+        const float k0 = (float)kr[d], k1 = (float)kr[d + 1], k2 = (float)kr[d + 2], k3 = (float)kr[d + 3];
+#pragma unroll
+        for (int i = 0; i < AG_ROWS; ++i) {
+          if (i < nrows) {
+            const float4 qv = *(const float4 *)&qs[i * DP + d];
+            x[i] = fmaf(k0, qv.x, x[i]);
+            x[i] = fmaf(k1, qv.y, x[i]);
+            x[i] = fmaf(k2, qv.z, x[i]);
+            x[i] = fmaf(k3, qv.w, x[i]);
+          }
+        }
+      }
+      for (; d < D; ++d) {
+        const float k0 = (float)kr[d];
+#pragma unroll
+        for (int i = 0; i < AG_ROWS; ++i)
+          if (i < nrows) x[i] = fmaf(k0, qs[i * DP + d], x[i]);
+      }
+    }
+    // scaled logits (log2 units), -inf where the row does not see the token; tile max per row
+#pragma unroll
+    for (int i = 0; i < AG_ROWS; ++i) {
+      if (i < nrows) {
+        x[i] = off >= 0 && t < lims[i] ? x[i] * c2 : -INFINITY;
+        float mx = x[i];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        if (lane == 0) red[i][wave] = mx;
+      }
+    }
     __syncthreads();
-    const int cnt = min(256, lim - t0);
+    float alpha[AG_ROWS];
+#pragma unroll
+    for (int i = 0; i < AG_ROWS; ++i) {
+      alpha[i] = 1.f;
+      if (i < nrows) {
+        const float tm = fmaxf(fmaxf(red[i][0], red[i][1]), fmaxf(red[i][2], red[i][3]));
+        const float m_new = fmaxf(m2[i], tm);
+        const float msafe = m_new == -INFINITY ? 0.f : m_new;
+        alpha[i] = exp2f(m2[i] - msafe);
+        m2[i] = m_new;
+        ps[i * 256 + tid] = x[i] == -INFINITY ? 0.f : exp2f(x[i] - msafe);
+      }
+    }
+    __syncthreads();
+    // O_i[d] += sum_j p_i,j v_j[d] for d = tid and tid + 256
+#pragma unroll
+    for (int i = 0; i < AG_ROWS; ++i) {
+      acc0[i] *= alpha[i];
+      acc1[i] *= alpha[i];
+      lsum[i] *= alpha[i];
+    }
+    const int cnt = min(256, t_end - t0);
+    const bool d0 = tid < D, d1 = tid + 256 < D;
     for (int j = 0; j < cnt; ++j) {
-      const float pj = ps[j];
-      if (pj == 0.f) continue;
-      const int64_t off = row_off(t0 + j);
-      if (tid < D) acc0 = fmaf(pj, (float)vplane[off + tid], acc0);
-      if (tid + 256 < D) acc1 = fmaf(pj, (float)vplane[off + tid + 256], acc1);
+      const int64_t oj = offs[j];
+      if (oj < 0) continue;  // uniform: no row sees a token of an invalid block
+      const float v0 = d0 ? (float)vplane[oj + tid] : 0.f;
+      const float v1 = d1 ? (float)vplane[oj + tid + 256] : 0.f;
+#pragma unroll
+      for (int i = 0; i < AG_ROWS; ++i) {
+        if (i < nrows) {
+          const float pj = ps[i * 256 + j];
+          acc0[i] = fmaf(pj, v0, acc0[i]);
+          acc1[i] = fmaf(pj, v1, acc1[i]);
+          lsum[i] += pj;
+        }
+      }
+    }
+    __syncthreads();  // ps, offs and red are rewritten by the next tile
+  }
+
+#pragma unroll
+  for (int i = 0; i < AG_ROWS; ++i) {
+    if (i >= nrows) continue;
+    const int row = row0 + i, n = row / G, g = row % G;
+    if (a.nchunk > 1) {
+      const int64_t pr = ((int64_t)p * a.rows_pad + row) * a.nchunk + chunk;
+      float *wo = a.ws_o + pr * D;
+      if (tid < D) wo[tid] = acc0[i];
+      if (tid + 256 < D) wo[tid + 256] = acc1[i];
+      if (tid == 0) { a.ws_ml[pr * 2] = m2[i]; a.ws_ml[pr * 2 + 1] = lsum[i]; }
+    } else {
+      float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * G + g) * a.o_sh;
+      const float inv = lsum[i] > 0.f ? 1.0f / lsum[i] : 0.f;
+      if (tid < D) op[tid] = acc0[i] * inv;
+      if (tid + 256 < D) op[tid + 256] = acc1[i] * inv;
+      if (tid == 0)
+        a.lse[(int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * G + g] =
+            lsum[i] > 0.f ? (m2[i] + __log2f(lsum[i])) * 0.6931471805599453f : -INFINITY;
     }
   }
-  float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)hq * a.o_sh;
-  const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
-  if (tid < D) op[tid] = acc0 * inv;
-  if (tid + 256 < D) op[tid + 256] = acc1 * inv;
-  if (tid == 0)
-    a.lse[(int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + hq] =
-        Lsum > 0.f ? M + logf(Lsum) : -INFINITY;
 }
 
 // Ring workgroup shape for a pair with rtiles 32-row tiles of query rows: waves and row
@@ -1056,21 +1180,54 @@ static int launch_attn_mfma(AttnArgs a, int bs_shift, void *ws, size_t ws_bytes,
   return actkv_check_launch();
 }
 
+// Token split of the float32 path: about four workgroups per CU over the (pair, row group)
+// items, chunks of a whole number of 256-token tiles.
+static AttnSplit attn_split_generic(int pairs, int N, int G, int span, int cus) {
+  AttnSplit sp;
+  sp.ngroups = (N * G + AG_ROWS - 1) / AG_ROWS;
+  sp.rows_pad = sp.ngroups * AG_ROWS;
+  const int64_t items = (int64_t)pairs * sp.ngroups;
+  const int64_t want = 4LL * cus;
+  int nchunk = (int)std::min<int64_t>(std::max<int64_t>(1, (want + items - 1) / items), std::max(1, span / 256));
+  int tpc = ((span + nchunk - 1) / nchunk + 255) / 256 * 256;
+  tpc = std::max(tpc, 256);
+  sp.nchunk = (span + tpc - 1) / tpc;
+  sp.tpc = tpc;
+  if (sp.nchunk <= 1) { sp.nchunk = 1; sp.tpc = std::max(span, 1); }
+  return sp;
+}
+
 template <typename QT, typename KT>
-static int launch_attn_generic(const AttnArgs &a, hipStream_t st) {
-  const int64_t rows = (int64_t)a.L * a.R * a.N * a.Hq;
-  if (rows > 0x7fffffffLL) return ACTKV_ERR_UNSUPPORTED;
-  const size_t shm = (size_t)(a.D + 256) * sizeof(float);
-  hipLaunchKernelGGL((attn_generic_kernel<QT, KT>), dim3((unsigned)rows), dim3(256), shm, st, a);
+static int launch_attn_generic(AttnArgs a, void *ws, size_t ws_bytes, hipStream_t st) {
+  const int64_t pairs64 = (int64_t)a.L * a.R * a.Hkv;
+  const int64_t groups = ((int64_t)a.N * a.G + AG_ROWS - 1) / AG_ROWS;
+  if (pairs64 * groups > 0x7fffffffLL) return ACTKV_ERR_UNSUPPORTED;
+  const int pairs = (int)pairs64;
+  AttnSplit sp = attn_split_generic(pairs, a.N, a.G, a.max_blocks * a.BS, device_cus());
+  const size_t need = attn_ws_bytes(pairs, sp, a.D);
+  if (sp.nchunk > 1 && (!ws || ws_bytes < need || (int64_t)pairs * sp.ngroups * sp.nchunk > 0x7fffffffLL)) {
+    sp.nchunk = 1;
+    sp.tpc = std::max(a.max_blocks * a.BS, 1);
+  }
+  a.nchunk = sp.nchunk; a.tpc = sp.tpc; a.rows_pad = sp.rows_pad; a.dyn = 0;
+  a.ws_o = sp.nchunk > 1 ? (float *)ws : nullptr;
+  a.ws_ml = sp.nchunk > 1 ? (float *)((char *)ws + (size_t)pairs * sp.rows_pad * sp.nchunk * a.D * sizeof(float)) : nullptr;
+  const size_t shm = (size_t)AG_ROWS * (((a.D + 3) & ~3) + 256) * sizeof(float);
+  const int64_t grid = (int64_t)pairs * sp.ngroups * sp.nchunk;
+  hipLaunchKernelGGL((attn_generic_kernel<QT, KT>), dim3((unsigned)grid), dim3(256), shm, st, a, pairs, sp.ngroups);
+  int rc = actkv_check_launch();
+  if (rc || sp.nchunk <= 1) return rc;
+  const int64_t waves = (int64_t)pairs * sp.rows_pad;
+  hipLaunchKernelGGL(attn_combine_kernel<0>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, a, pairs);
   return actkv_check_launch();
 }
 
 template <typename QT>
-static int dispatch_attn_generic(const AttnArgs &a, int kv_dtype, hipStream_t st) {
+static int dispatch_attn_generic(const AttnArgs &a, int kv_dtype, void *ws, size_t wb, hipStream_t st) {
   switch (kv_dtype) {
-    case ACTKV_F32: return launch_attn_generic<QT, float>(a, st);
-    case ACTKV_F16: return launch_attn_generic<QT, _Float16>(a, st);
-    case ACTKV_BF16: return launch_attn_generic<QT, __bf16>(a, st);
+    case ACTKV_F32: return launch_attn_generic<QT, float>(a, ws, wb, st);
+    case ACTKV_F16: return launch_attn_generic<QT, _Float16>(a, ws, wb, st);
+    case ACTKV_BF16: return launch_attn_generic<QT, __bf16>(a, ws, wb, st);
   }
   return ACTKV_ERR_INVALID_ARG;
 }
@@ -1130,9 +1287,9 @@ extern "C" int actkv_paged_attention(
                    : launch_attn_mfma<_Float16, f16x8, 128>(a, bs_shift, ws, wb, st);
   }
   switch (q_dtype) {
-    case ACTKV_F32: return dispatch_attn_generic<float>(a, kv_dtype, st);
-    case ACTKV_F16: return dispatch_attn_generic<_Float16>(a, kv_dtype, st);
-    default: return dispatch_attn_generic<__bf16>(a, kv_dtype, st);
+    case ACTKV_F32: return dispatch_attn_generic<float>(a, kv_dtype, workspace, workspace_bytes, st);
+    case ACTKV_F16: return dispatch_attn_generic<_Float16>(a, kv_dtype, workspace, workspace_bytes, st);
+    default: return dispatch_attn_generic<__bf16>(a, kv_dtype, workspace, workspace_bytes, st);
   }
 }
 
@@ -1140,8 +1297,11 @@ extern "C" size_t actkv_paged_attention_workspace_size(int L, int R, int N, int 
                                                        int max_blocks, int block_size) {
   if (L < 1 || R < 1 || N < 1 || Hkv < 1 || Hq % Hkv != 0 || max_blocks < 1 || block_size < 1) return 0;
   const int G = Hq / Hkv;
-  if ((D != 128 && D != 64) || G < 1) return 0;  // the float32 path does not split
+  if (G < 1 || D > 512) return 0;
   if ((int64_t)max_blocks * block_size > 0x7fffffffLL) return 0;
   const int pairs = L * R * Hkv;
-  return attn_ws_bytes(pairs, attn_split(pairs, N, G, max_blocks * block_size, device_cus()), D);
+  // head dims 128 and 64: the matrix-core split; others: the float32 path's split
+  if (D == 128 || D == 64)
+    return attn_ws_bytes(pairs, attn_split(pairs, N, G, max_blocks * block_size, device_cus()), D);
+  return attn_ws_bytes(pairs, attn_split_generic(pairs, N, G, max_blocks * block_size, device_cus()), D);
 }

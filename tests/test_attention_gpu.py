@@ -182,6 +182,40 @@ def test_float32_path_matches_the_oracle(d, hq, hkv, bs, dtype):
     torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-4)
 
 
+@pytest.mark.parametrize("lens,n_q,hq,hkv,d,bs,dtype,causal,split", [
+    ([4000, 2500], 1, 16, 8, 256, 16, torch.bfloat16, False, True),   # head dim 256 decode (Gemma shape), split
+    ([4000, 2500], 1, 16, 8, 256, 16, torch.bfloat16, False, False),  # the same in one pass
+    ([3000, 47], 3, 8, 2, 30, 12, torch.float16, True, True),         # head dim 30, block 12, causal
+    ([900], 9, 8, 2, 96, 16, torch.bfloat16, True, True),             # 36 rows: three row groups
+    ([2100, 0, 5], 1, 40, 1, 80, 8, torch.float32, False, True),      # G 40, an empty request, fp32
+    ([1300], 20, 32, 8, 128, 16, torch.float32, True, False),         # fp32 cache, 80 rows, one pass
+])
+def test_float32_path_row_groups_and_token_split(monkeypatch, lens, n_q, hq, hkv, d, bs, dtype, causal, split):
+    """The float32 path takes up to 16 query rows of one KV head per workgroup over a token
+    chunk (the chunks merged by the combine launch when a workspace is given): head dims off
+    the matrix cores, blocks that are not a power of two, GQA groups wider than a row group,
+    empty requests, causal limits, with and without the split, against the oracle."""
+    from actkv import _hip
+    cache = _cache(lens, hkv=hkv, d=d, bs=bs, dtype=dtype, seed=d + n_q + bs)
+    reqs = list(range(len(lens)))
+    g = torch.Generator().manual_seed(d + hq)
+    q = torch.randn(len(lens), n_q, hq, d, generator=g).to(dtype)
+    kv_len = None
+    if causal:
+        kv_len = torch.stack([torch.randint(0, S + 8, (n_q,), generator=g) for S in lens]).to(torch.int32)
+        kv_len[0, 0] = 0
+    lib = _hip.lib()
+    mb = max(len(t) for t in cache.tables.values())
+    if split:
+        assert lib.actkv_paged_attention_workspace_size(1, len(lens), n_q, hq, hkv, d, mb, bs) > 0
+    else:
+        monkeypatch.setattr(lib, "actkv_paged_attention_workspace_size", lambda *a: 0)
+    out, lse = cache.decode_attention(reqs, q.cuda(), kv_len=None if kv_len is None else kv_len.cuda())
+    want_out, want_lse = _oracle(cache, reqs, q, 0, kv_len=None if kv_len is None else kv_len.tolist())
+    torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
+    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-4)
+
+
 def test_device_lse_drives_action_scoring():
     """Algorithm 3 end to end on the device: the attention kernel's lse, fed to cal_attn, gives
     the oracle's scores computed with the oracle's lse (within the scoring tolerance)."""

@@ -144,3 +144,45 @@ def test_random_shapes_at_head_dim_64_match_the_oracle(seed):
         kv_len=None if kv_len is None else kv_len.tolist(), n_valid=None if n_valid is None else n_valid.tolist())
     torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
     torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=2e-4)   # P as hi + lo terms
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_shapes_on_the_float32_path_match_the_oracle(seed):
+    """Shapes off the matrix cores (head dims other than 64 and 128, float32 caches, blocks
+    that are not a power of two from 16 up, groups up to 40): the float32 kernel's row groups
+    and token split, against the oracle; out and lse within 1e-4."""
+    rnd = random.Random(15000 + seed)
+    n_req = rnd.randint(1, 4)
+    lens = [rnd.choice([0, rnd.randint(1, 200), rnd.randint(200, 4000)]) for _ in range(n_req)]
+    if max(lens) == 0:
+        lens[0] = rnd.randint(1, 3000)
+    d = rnd.choice([8, 30, 36, 80, 96, 256, 512])
+    hkv = rnd.choice([1, 2, 4])
+    hq = hkv * rnd.choice([1, 2, 3, 4, 8, rnd.randint(9, 40)])
+    n_q = rnd.choice([1, rnd.randint(2, 4), rnd.randint(5, 24)])
+    dtype, bs = rnd.choice([torch.bfloat16, torch.float16, torch.float32]), rnd.choice([8, 12, 16, 32])
+    causal, partial = rnd.random() < 0.5, rnd.random() < 0.3
+    print(f"case {seed}: lens {lens} d {d} hq {hq} hkv {hkv} n_q {n_q} {dtype} bs {bs} causal {causal} "
+          f"partial {partial}", flush=True)
+    g = torch.Generator().manual_seed(17000 + seed)
+    nb = sum(math.ceil(n / bs) for n in lens) + 3
+    cache = PagedKVCache(nb, bs, hkv, d, n_layers=1, dtype=dtype, device="cuda")
+    cache.free = torch.randperm(nb, generator=g).tolist()
+    for r, n in enumerate(lens):
+        cache.append(r, torch.randn(1, n, hkv, d, generator=g).to(dtype).cuda(),
+                     torch.randn(1, n, hkv, d, generator=g).to(dtype).cuda())
+    reqs = list(range(len(lens)))
+    seq, bt = cache._device_tables(reqs)
+    q = torch.randn(len(lens), n_q, hq, d, generator=g).to(dtype)
+    kv_len = (torch.stack([torch.randint(0, S + 4, (n_q,), generator=g) for S in lens]).to(torch.int32)
+              if causal else None)
+    n_valid = (torch.tensor([random.Random(seed + r).randint(0, n_q) for r in reqs], dtype=torch.int32)
+               if partial else None)
+    out, lse = paged_decode_attention(q.cuda(), cache.kv[0], bt, seq,
+                                      kv_len=None if kv_len is None else kv_len.cuda(),
+                                      n_valid=None if n_valid is None else n_valid.cuda())
+    want_out, want_lse = ref.paged_attention(
+        q.float(), cache.kv[0].cpu().float(), [cache.tables[r] for r in reqs], [cache.seq_used[r] for r in reqs],
+        kv_len=None if kv_len is None else kv_len.tolist(), n_valid=None if n_valid is None else n_valid.tolist())
+    torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-4)
+    torch.testing.assert_close(out.cpu(), want_out, rtol=0, atol=1e-4)

@@ -38,10 +38,10 @@
 // instruction then moves eight rows instead of four, the rows' eight 16-byte chunks are
 // swizzled with their own pattern (dswz), and two 32-dim output tiles replace four.
 //
-// Generic path (any other dtype / head_dim up to 512 / block size): float32, up to 16
-// query rows of one KV head per workgroup (a decode step's GQA group reads K and V
-// once), one pass with an online max and sum, token chunks merged by the same combine
-// launch.  Described at attn_generic_kernel.
+// Generic path (any other dtype / head_dim up to 512 / block size): float32, up to 8
+// query rows of one KV head per workgroup (a decode step's GQA group of up to 8 heads
+// reads K and V once), one pass with an online max and sum, token chunks merged by the
+// same combine launch.  Described at attn_generic_kernel.
 #include "common.h"
 
 #include <algorithm>
@@ -895,9 +895,9 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int pairs
 
 // ------------------------------------------------------------------ generic path
 // Any dtype pairing, head dims up to 512, any block size.  grid pairs * ngroups * nchunk,
-// 256 threads: a workgroup takes up to AG_ROWS query rows (n, g) of one (layer, request, KV
-// head) pair -- a decode step's whole GQA group, so K and V are read once for all of its
-// rows -- over one token chunk, 256 tokens at a time:
+// 256 threads: a workgroup takes up to NR query rows (n, g) of one (layer, request, KV
+// head) pair -- a decode step's whole GQA group of up to 8 heads, so K and V are read once
+// for all of its rows -- over one token chunk, 256 tokens at a time:
 //   thread j: s_i = q_i . k_(t0+j) for each row i (the rows from LDS, the dot products in
 //   registers as independent FMA chains), the tile's max per row through wave reductions and
 //   LDS, p_i,j into LDS; then thread d: O_i[d] += sum_j p_i,j v_(t0+j)[d] (V rows read
@@ -906,15 +906,20 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int pairs
 // through the same workspace layout ([pair][row][chunk][D] and (max, sum)) and the combine
 // launch.  Tokens in blocks the table marks invalid, and tokens a row does not see, get
 // probability 0 (the V rows of invalid blocks are not read).
-constexpr int AG_ROWS = 16;
-template <typename QT, typename KT>
+// NR rows per workgroup (a power of two up to AG_ROWS, the fewest that hold a pair's rows):
+// the row loops are unrolled over NR, and rows past the pair's last are padding that sees
+// no token.  With the row loops bounded at run time instead, the compiler walked the rows
+// one at a time and re-read K and V per row; a cap of 16 rows cost a wave per SIMD (133
+// registers) and measured slower than 8 on 32 and 512 rows per pair.
+constexpr int AG_ROWS = 8;
+template <typename QT, typename KT, int NR>
 __global__ void __launch_bounds__(256) attn_generic_kernel(AttnArgs a, int pairs, int ngroups) {
-  extern __shared__ __attribute__((aligned(16))) float sm[];  // q rows [AG_ROWS][DP], then p [AG_ROWS][256]
-  __shared__ float red[AG_ROWS][4];
-  __shared__ int lims[AG_ROWS];
+  extern __shared__ __attribute__((aligned(16))) float sm[];  // q rows [NR][DP], then p [NR][256]
+  __shared__ float red[NR][4];
+  __shared__ int lims[NR];
   __shared__ int64_t offs[256];
   const int D = a.D, DP = (D + 3) & ~3;
-  float *qs = sm, *ps = sm + AG_ROWS * DP;
+  float *qs = sm, *ps = sm + NR * DP;
   const int bid = blockIdx.x;
   const int chunk = bid % a.nchunk;
   const int grp = (bid / a.nchunk) % ngroups;
@@ -925,16 +930,16 @@ __global__ void __launch_bounds__(256) attn_generic_kernel(AttnArgs a, int pairs
   const int l = p / (a.Hkv * a.R);
   const int G = a.G;
   const int nq = attn_nq(a, r);
-  const int row0 = grp * AG_ROWS;
+  const int row0 = grp * NR;
   if (row0 >= nq * G) return;
-  const int nrows = min(AG_ROWS, nq * G - row0);
+  const int nrows = min(NR, nq * G - row0);
   const int S_all = attn_seq_len(a, r);
   if (a.nchunk > 1 && chunk * a.tpc >= S_all) return;   // the combine reads only chunks with tokens
   const int c_begin = min(chunk * a.tpc, S_all);
   const int c_end = a.nchunk > 1 ? min(S_all, c_begin + a.tpc) : S_all;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-  for (int i = tid; i < AG_ROWS * DP; i += 256) {
+  for (int i = tid; i < NR * DP; i += 256) {
     const int ri = i / DP, d = i % DP, row = row0 + ri;
     float v = 0.f;
     if (ri < nrows && d < D)
@@ -942,7 +947,7 @@ __global__ void __launch_bounds__(256) attn_generic_kernel(AttnArgs a, int pairs
                                    (int64_t)(h * G + row % G) * a.q_sh + d];
     qs[i] = v;
   }
-  if (tid < AG_ROWS) lims[tid] = tid < nrows ? min(attn_lim(a, r, (row0 + tid) / G, S_all), c_end) : c_begin;
+  if (tid < NR) lims[tid] = tid < nrows ? min(attn_lim(a, r, (row0 + tid) / G, S_all), c_end) : c_begin;
   __syncthreads();
   int t_end = c_begin;  // the last token any row of the workgroup sees, plus one
   for (int i = 0; i < nrows; ++i) t_end = max(t_end, lims[i]);
@@ -950,9 +955,9 @@ __global__ void __launch_bounds__(256) attn_generic_kernel(AttnArgs a, int pairs
   const KT *kplane = (const KT *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh;
   const KT *vplane = kplane + a.kv_sv;
   const float c2 = a.scale * 1.4426950408889634f;
-  float m2[AG_ROWS], lsum[AG_ROWS], acc0[AG_ROWS], acc1[AG_ROWS];
+  float m2[NR], lsum[NR], acc0[NR], acc1[NR];
 #pragma unroll
-  for (int i = 0; i < AG_ROWS; ++i) { m2[i] = -INFINITY; lsum[i] = 0.f; acc0[i] = 0.f; acc1[i] = 0.f; }
+  for (int i = 0; i < NR; ++i) { m2[i] = -INFINITY; lsum[i] = 0.f; acc0[i] = 0.f; acc1[i] = 0.f; }
 
   for (int t0 = c_begin; t0 < t_end; t0 += 256) {
     const int t = t0 + tid;
@@ -962,61 +967,53 @@ __global__ void __launch_bounds__(256) attn_generic_kernel(AttnArgs a, int pairs
       if (ph >= 0) off = (int64_t)ph * a.kv_sb + (int64_t)(t % a.BS) * a.kv_ss;
     }
     offs[tid] = off;
-    float x[AG_ROWS];
+    float x[NR];
 #pragma unroll
-    for (int i = 0; i < AG_ROWS; ++i) x[i] = 0.f;
+    for (int i = 0; i < NR; ++i) x[i] = 0.f;
     if (off >= 0) {
       const KT *kr = kplane + off;
       int d = 0;
       for (; d + 4 <= D; d += 4) {
         const float k0 = (float)kr[d], k1 = (float)kr[d + 1], k2 = (float)kr[d + 2], k3 = (float)kr[d + 3];
 #pragma unroll
-        for (int i = 0; i < AG_ROWS; ++i) {
-          if (i < nrows) {
-            const float4 qv = *(const float4 *)&qs[i * DP + d];
-            x[i] = fmaf(k0, qv.x, x[i]);
-            x[i] = fmaf(k1, qv.y, x[i]);
-            x[i] = fmaf(k2, qv.z, x[i]);
-            x[i] = fmaf(k3, qv.w, x[i]);
-          }
+        for (int i = 0; i < NR; ++i) {
+          const float4 qv = *(const float4 *)&qs[i * DP + d];
+          x[i] = fmaf(k0, qv.x, x[i]);
+          x[i] = fmaf(k1, qv.y, x[i]);
+          x[i] = fmaf(k2, qv.z, x[i]);
+          x[i] = fmaf(k3, qv.w, x[i]);
         }
       }
       for (; d < D; ++d) {
         const float k0 = (float)kr[d];
 #pragma unroll
-        for (int i = 0; i < AG_ROWS; ++i)
-          if (i < nrows) x[i] = fmaf(k0, qs[i * DP + d], x[i]);
+        for (int i = 0; i < NR; ++i) x[i] = fmaf(k0, qs[i * DP + d], x[i]);
       }
     }
     // scaled logits (log2 units), -inf where the row does not see the token; tile max per row
 #pragma unroll
-    for (int i = 0; i < AG_ROWS; ++i) {
-      if (i < nrows) {
-        x[i] = off >= 0 && t < lims[i] ? x[i] * c2 : -INFINITY;
-        float mx = x[i];
+    for (int i = 0; i < NR; ++i) {
+      x[i] = off >= 0 && t < lims[i] ? x[i] * c2 : -INFINITY;   // padding rows see no token
+      float mx = x[i];
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-        if (lane == 0) red[i][wave] = mx;
-      }
+      for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+      if (lane == 0) red[i][wave] = mx;
     }
     __syncthreads();
-    float alpha[AG_ROWS];
+    float alpha[NR];
 #pragma unroll
-    for (int i = 0; i < AG_ROWS; ++i) {
-      alpha[i] = 1.f;
-      if (i < nrows) {
-        const float tm = fmaxf(fmaxf(red[i][0], red[i][1]), fmaxf(red[i][2], red[i][3]));
-        const float m_new = fmaxf(m2[i], tm);
-        const float msafe = m_new == -INFINITY ? 0.f : m_new;
-        alpha[i] = exp2f(m2[i] - msafe);
-        m2[i] = m_new;
-        ps[i * 256 + tid] = x[i] == -INFINITY ? 0.f : exp2f(x[i] - msafe);
-      }
+    for (int i = 0; i < NR; ++i) {
+      const float tm = fmaxf(fmaxf(red[i][0], red[i][1]), fmaxf(red[i][2], red[i][3]));
+      const float m_new = fmaxf(m2[i], tm);
+      const float msafe = m_new == -INFINITY ? 0.f : m_new;
+      alpha[i] = exp2f(m2[i] - msafe);
+      m2[i] = m_new;
+      ps[i * 256 + tid] = x[i] == -INFINITY ? 0.f : exp2f(x[i] - msafe);
     }
     __syncthreads();
     // O_i[d] += sum_j p_i,j v_j[d] for d = tid and tid + 256
 #pragma unroll
-    for (int i = 0; i < AG_ROWS; ++i) {
+    for (int i = 0; i < NR; ++i) {
       acc0[i] *= alpha[i];
       acc1[i] *= alpha[i];
       lsum[i] *= alpha[i];
@@ -1029,20 +1026,18 @@ __global__ void __launch_bounds__(256) attn_generic_kernel(AttnArgs a, int pairs
       const float v0 = d0 ? (float)vplane[oj + tid] : 0.f;
       const float v1 = d1 ? (float)vplane[oj + tid + 256] : 0.f;
 #pragma unroll
-      for (int i = 0; i < AG_ROWS; ++i) {
-        if (i < nrows) {
-          const float pj = ps[i * 256 + j];
-          acc0[i] = fmaf(pj, v0, acc0[i]);
-          acc1[i] = fmaf(pj, v1, acc1[i]);
-          lsum[i] += pj;
-        }
+      for (int i = 0; i < NR; ++i) {
+        const float pj = ps[i * 256 + j];
+        acc0[i] = fmaf(pj, v0, acc0[i]);
+        acc1[i] = fmaf(pj, v1, acc1[i]);
+        lsum[i] += pj;
       }
     }
     __syncthreads();  // ps, offs and red are rewritten by the next tile
   }
 
 #pragma unroll
-  for (int i = 0; i < AG_ROWS; ++i) {
+  for (int i = 0; i < NR; ++i) {
     if (i >= nrows) continue;
     const int row = row0 + i, n = row / G, g = row % G;
     if (a.nchunk > 1) {
@@ -1182,10 +1177,20 @@ static int launch_attn_mfma(AttnArgs a, int bs_shift, void *ws, size_t ws_bytes,
 
 // Token split of the float32 path: about four workgroups per CU over the (pair, row group)
 // items, chunks of a whole number of 256-token tiles.
+// rows per workgroup of the float32 path: the fewest (a power of two, at most AG_ROWS) that
+// hold a pair's N * G rows
+static int attn_generic_rows(int N, int G) {
+  const int64_t rows = (int64_t)N * G;
+  int nr = 1;
+  while (nr < AG_ROWS && nr < rows) nr *= 2;
+  return nr;
+}
+
 static AttnSplit attn_split_generic(int pairs, int N, int G, int span, int cus) {
   AttnSplit sp;
-  sp.ngroups = (N * G + AG_ROWS - 1) / AG_ROWS;
-  sp.rows_pad = sp.ngroups * AG_ROWS;
+  const int nr = attn_generic_rows(N, G);
+  sp.ngroups = (int)(((int64_t)N * G + nr - 1) / nr);
+  sp.rows_pad = sp.ngroups * nr;
   const int64_t items = (int64_t)pairs * sp.ngroups;
   const int64_t want = 4LL * cus;
   int nchunk = (int)std::min<int64_t>(std::max<int64_t>(1, (want + items - 1) / items), std::max(1, span / 256));
@@ -1200,7 +1205,8 @@ static AttnSplit attn_split_generic(int pairs, int N, int G, int span, int cus) 
 template <typename QT, typename KT>
 static int launch_attn_generic(AttnArgs a, void *ws, size_t ws_bytes, hipStream_t st) {
   const int64_t pairs64 = (int64_t)a.L * a.R * a.Hkv;
-  const int64_t groups = ((int64_t)a.N * a.G + AG_ROWS - 1) / AG_ROWS;
+  const int nr = attn_generic_rows(a.N, a.G);
+  const int64_t groups = ((int64_t)a.N * a.G + nr - 1) / nr;
   if (pairs64 * groups > 0x7fffffffLL) return ACTKV_ERR_UNSUPPORTED;
   const int pairs = (int)pairs64;
   AttnSplit sp = attn_split_generic(pairs, a.N, a.G, a.max_blocks * a.BS, device_cus());
@@ -1212,9 +1218,17 @@ static int launch_attn_generic(AttnArgs a, void *ws, size_t ws_bytes, hipStream_
   a.nchunk = sp.nchunk; a.tpc = sp.tpc; a.rows_pad = sp.rows_pad; a.dyn = 0;
   a.ws_o = sp.nchunk > 1 ? (float *)ws : nullptr;
   a.ws_ml = sp.nchunk > 1 ? (float *)((char *)ws + (size_t)pairs * sp.rows_pad * sp.nchunk * a.D * sizeof(float)) : nullptr;
-  const size_t shm = (size_t)AG_ROWS * (((a.D + 3) & ~3) + 256) * sizeof(float);
-  const int64_t grid = (int64_t)pairs * sp.ngroups * sp.nchunk;
-  hipLaunchKernelGGL((attn_generic_kernel<QT, KT>), dim3((unsigned)grid), dim3(256), shm, st, a, pairs, sp.ngroups);
+  const size_t shm = (size_t)nr * (((a.D + 3) & ~3) + 256) * sizeof(float);
+  const dim3 grid((unsigned)((int64_t)pairs * sp.ngroups * sp.nchunk));
+#define ACTKV_AG(NRV) hipLaunchKernelGGL((attn_generic_kernel<QT, KT, NRV>), grid, dim3(256), shm, st, a, pairs, sp.ngroups)
+  switch (nr) {
+    case 1: ACTKV_AG(1); break;
+    case 2: ACTKV_AG(2); break;
+    case 4: ACTKV_AG(4); break;
+    case 8: ACTKV_AG(8); break;
+    default: ACTKV_AG(16); break;
+  }
+#undef ACTKV_AG
   int rc = actkv_check_launch();
   if (rc || sp.nchunk <= 1) return rc;
   const int64_t waves = (int64_t)pairs * sp.rows_pad;

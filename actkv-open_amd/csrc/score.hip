@@ -167,10 +167,10 @@ __global__ void __launch_bounds__(256) score_generic_kernel(ScoreArgs a) {
 // ------------------------------------------------------------------ generic, query rows in chunks
 // The same computation and fold order as score_generic_kernel, for head dims that are a
 // multiple of 4 up to 512: grid (ceil(span/256), L*R*Hkv), 256 threads, one thread per
-// token slot.  The query rows (n, g) go through LDS ROWS at a time (qc whole queries of
-// gc group heads each: gc = min(G, ROWS), qc = ROWS / gc; a group wider than ROWS takes
-// one query per chunk and several chunks of heads, the running max carried between
-// them).  A thread walks its K row once per chunk, four dims per step, and keeps the
+// token slot.  The query rows (n, g) go through LDS ROWS at a time (a power of two; qc
+// whole queries of gc group heads each: gc = min(G, ROWS), qc = ROWS / gc; a group wider
+// than ROWS takes one query per chunk and several chunks of heads, the running max carried
+// between them).  A thread walks its K row once per chunk, four dims per step, and keeps the
 // chunk's ROWS dot products in registers: K is read once per ROWS rows instead of once
 // per row, and the dot products are independent FMA chains.  Each dot product still
 // sums its dims in order, so the scores equal score_generic_kernel's.
@@ -1151,11 +1151,25 @@ static int launch_generic_rows(const ScoreArgs &a, hipStream_t st) {
 
 template <typename QT, typename KT>
 static int launch_generic(const ScoreArgs &a, hipStream_t st) {
-  // head dims that are a multiple of 4 up to 512: query rows in chunks (at most 32 KiB of LDS)
-  if (a.D % 4 == 0 && a.D <= 512)
-    return a.D <= 128 ? launch_generic_rows<QT, KT, 64>(a, st)
-         : a.D <= 256 ? launch_generic_rows<QT, KT, 32>(a, st)
-                      : launch_generic_rows<QT, KT, 16>(a, st);
+  // head dims that are a multiple of 4 up to 512: query rows in chunks of at most 64, 32 or 16
+  // rows (head dim up to 128, 256, 512: at most 32 KiB of LDS), and no more than the call's
+  // N * G rows rounded up to a power of two (one action query of a small group, the
+  // reference's per-token fold, computes no padding rows)
+  if (a.D % 4 == 0 && a.D <= 512) {
+    const int rmax = a.D <= 128 ? 64 : a.D <= 256 ? 32 : 16;
+    const int64_t need = (int64_t)a.N * a.G;
+    int rows = 1;
+    while (rows < rmax && rows < need) rows *= 2;
+    switch (rows) {
+      case 1: return launch_generic_rows<QT, KT, 1>(a, st);
+      case 2: return launch_generic_rows<QT, KT, 2>(a, st);
+      case 4: return launch_generic_rows<QT, KT, 4>(a, st);
+      case 8: return launch_generic_rows<QT, KT, 8>(a, st);
+      case 16: return launch_generic_rows<QT, KT, 16>(a, st);
+      case 32: return launch_generic_rows<QT, KT, 32>(a, st);
+      default: return launch_generic_rows<QT, KT, 64>(a, st);
+    }
+  }
   const int span = a.max_blocks * a.BS;
   dim3 grid((span + 255) / 256, a.L * a.R * a.Hkv);
   const size_t shm = (size_t)(a.G * a.D + a.G) * sizeof(float);

@@ -98,7 +98,7 @@ def test_fp32_logits_equal_eager_dynamic_cache():
     assert all(sess.kv.seq_used[r] == n0 + steps for r in range(B))
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 128), (16, 2, 64)])   # GQA 4 at head dim 128; GQA 8 at 64
+@pytest.mark.parametrize("hq,hkv,d", [(8, 2, 128), (16, 2, 64), (4, 2, 256)])   # GQA 4 at head dim 128; GQA 8 at 64; the float32 path at 256
 def test_bf16_logits_follow_fp32_attention(hq, hkv, d):
     model = _model(torch.bfloat16, hq=hq, hkv=hkv, d=d)
     B, n0, steps = 2, 300, 8

@@ -911,13 +911,14 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int pairs
 // no token.  With the row loops bounded at run time instead, the compiler walked the rows
 // one at a time and re-read K and V per row; a cap of 16 rows cost a wave per SIMD (133
 // registers) and measured slower than 8 on 32 and 512 rows per pair.
-constexpr int AG_ROWS = 8;
+constexpr int AG_ROWS = 8;  // the launch switch instantiates 1, 2, 4 and 8
 template <typename QT, typename KT, int NR>
 __global__ void __launch_bounds__(256) attn_generic_kernel(AttnArgs a, int pairs, int ngroups) {
   extern __shared__ __attribute__((aligned(16))) float sm[];  // q rows [NR][DP], then p [NR][256]
-  __shared__ float red[NR][4];
+  __shared__ float red[NR][4], redsum[NR][4];
   __shared__ int lims[NR];
   __shared__ int64_t offs[256];
+  __shared__ float vred[2048];  // the token groups' partial O of one row: tp * D <= 2048
   const int D = a.D, DP = (D + 3) & ~3;
   float *qs = sm, *ps = sm + NR * DP;
   const int bid = blockIdx.x;
@@ -955,9 +956,20 @@ __global__ void __launch_bounds__(256) attn_generic_kernel(AttnArgs a, int pairs
   const KT *kplane = (const KT *)a.kv + (int64_t)l * a.kv_sl + (int64_t)h * a.kv_sh;
   const KT *vplane = kplane + a.kv_sv;
   const float c2 = a.scale * 1.4426950408889634f;
-  float m2[NR], lsum[NR], acc0[NR], acc1[NR];
+  // P.V mapping: tpt threads per token, each with DPT consecutive dims of its V row; tp tokens
+  // in flight at a time, token j of a tile on thread group j mod tp
+  constexpr int DPT = 8;
+  const int tpt = (D + DPT - 1) / DPT, tp = 256 / tpt;
+  const int vgrp = tid / tpt, dbase = (tid - vgrp * tpt) * DPT;
+  const bool vact = vgrp < tp;
+  float m2[NR], lsum[NR], acc[NR][DPT];
 #pragma unroll
-  for (int i = 0; i < NR; ++i) { m2[i] = -INFINITY; lsum[i] = 0.f; acc0[i] = 0.f; acc1[i] = 0.f; }
+  for (int i = 0; i < NR; ++i) {
+    m2[i] = -INFINITY;
+    lsum[i] = 0.f;
+#pragma unroll
+    for (int e = 0; e < DPT; ++e) acc[i][e] = 0.f;
+  }
 
   for (int t0 = c_begin; t0 < t_end; t0 += 256) {
     const int t = t0 + tid;
@@ -1008,49 +1020,71 @@ __global__ void __launch_bounds__(256) attn_generic_kernel(AttnArgs a, int pairs
       const float msafe = m_new == -INFINITY ? 0.f : m_new;
       alpha[i] = exp2f(m2[i] - msafe);
       m2[i] = m_new;
-      ps[i * 256 + tid] = x[i] == -INFINITY ? 0.f : exp2f(x[i] - msafe);
+      const float pv = x[i] == -INFINITY ? 0.f : exp2f(x[i] - msafe);
+      ps[i * 256 + tid] = pv;
+      float sum = pv;
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 64);
+      if (lane == 0) redsum[i][wave] = sum;
     }
     __syncthreads();
-    // O_i[d] += sum_j p_i,j v_j[d] for d = tid and tid + 256
+    // l_i += the tile's sum of p (the same four wave sums, in order, in every thread);
+    // O_i[d] += sum_j p_i,j v_j[d] over the thread's tokens j = vgrp, vgrp + tp, ...
 #pragma unroll
     for (int i = 0; i < NR; ++i) {
-      acc0[i] *= alpha[i];
-      acc1[i] *= alpha[i];
-      lsum[i] *= alpha[i];
+      lsum[i] = lsum[i] * alpha[i] + ((redsum[i][0] + redsum[i][1]) + (redsum[i][2] + redsum[i][3]));
+#pragma unroll
+      for (int e = 0; e < DPT; ++e) acc[i][e] *= alpha[i];
     }
     const int cnt = min(256, t_end - t0);
-    const bool d0 = tid < D, d1 = tid + 256 < D;
-    for (int j = 0; j < cnt; ++j) {
-      const int64_t oj = offs[j];
-      if (oj < 0) continue;  // uniform: no row sees a token of an invalid block
-      const float v0 = d0 ? (float)vplane[oj + tid] : 0.f;
-      const float v1 = d1 ? (float)vplane[oj + tid + 256] : 0.f;
+    if (vact) {
+      for (int j = vgrp; j < cnt; j += tp) {
+        const int64_t oj = offs[j];
+        if (oj < 0) continue;  // a token of an invalid block: p = 0 in every row
+        const KT *vr = vplane + oj + dbase;
+        float v[DPT];
 #pragma unroll
-      for (int i = 0; i < NR; ++i) {
-        const float pj = ps[i * 256 + j];
-        acc0[i] = fmaf(pj, v0, acc0[i]);
-        acc1[i] = fmaf(pj, v1, acc1[i]);
-        lsum[i] += pj;
+        for (int e = 0; e < DPT; ++e) v[e] = dbase + e < D ? (float)vr[e] : 0.f;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+          const float pj = ps[i * 256 + j];
+#pragma unroll
+          for (int e = 0; e < DPT; ++e) acc[i][e] = fmaf(pj, v[e], acc[i][e]);
+        }
       }
     }
     __syncthreads();  // ps, offs and red are rewritten by the next tile
   }
 
+  // each row: the token groups' partial O summed in group order through LDS, then written
 #pragma unroll
   for (int i = 0; i < NR; ++i) {
-    if (i >= nrows) continue;
+    if (i >= nrows) break;  // uniform
+    __syncthreads();
+    if (vact) {
+#pragma unroll
+      for (int e = 0; e < DPT; ++e)
+        if (dbase + e < D) vred[vgrp * D + dbase + e] = acc[i][e];
+    }
+    __syncthreads();
     const int row = row0 + i, n = row / G, g = row % G;
     if (a.nchunk > 1) {
       const int64_t pr = ((int64_t)p * a.rows_pad + row) * a.nchunk + chunk;
       float *wo = a.ws_o + pr * D;
-      if (tid < D) wo[tid] = acc0[i];
-      if (tid + 256 < D) wo[tid + 256] = acc1[i];
+      for (int d = tid; d < D; d += 256) {
+        float o = 0.f;
+        for (int gi = 0; gi < tp; ++gi) o += vred[gi * D + d];
+        wo[d] = o;
+      }
       if (tid == 0) { a.ws_ml[pr * 2] = m2[i]; a.ws_ml[pr * 2 + 1] = lsum[i]; }
     } else {
       float *op = a.out + (int64_t)l * a.o_sl + (int64_t)r * a.o_sr + (int64_t)n * a.o_sn + (int64_t)(h * G + g) * a.o_sh;
       const float inv = lsum[i] > 0.f ? 1.0f / lsum[i] : 0.f;
-      if (tid < D) op[tid] = acc0[i] * inv;
-      if (tid + 256 < D) op[tid + 256] = acc1[i] * inv;
+      for (int d = tid; d < D; d += 256) {
+        float o = 0.f;
+        for (int gi = 0; gi < tp; ++gi) o += vred[gi * D + d];
+        op[d] = o * inv;
+      }
       if (tid == 0)
         a.lse[(int64_t)l * a.lse_sl + (int64_t)r * a.lse_sr + (int64_t)n * a.lse_sn + h * G + g] =
             lsum[i] > 0.f ? (m2[i] + __log2f(lsum[i])) * 0.6931471805599453f : -INFINITY;
@@ -1225,8 +1259,7 @@ static int launch_attn_generic(AttnArgs a, void *ws, size_t ws_bytes, hipStream_
     case 1: ACTKV_AG(1); break;
     case 2: ACTKV_AG(2); break;
     case 4: ACTKV_AG(4); break;
-    case 8: ACTKV_AG(8); break;
-    default: ACTKV_AG(16); break;
+    default: ACTKV_AG(8); break;   // AG_ROWS
   }
 #undef ACTKV_AG
   int rc = actkv_check_launch();

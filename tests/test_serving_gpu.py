@@ -111,8 +111,13 @@ def test_bf16_logits_follow_fp32_attention(hq, hkv, d):
     got = torch.stack(got, 1).float()
     for b in range(B):
         w = want[b].float()
-        assert (got[b] - w).abs().max().item() < 3e-2 * max(1.0, w.abs().max().item())
-        assert torch.equal(got[b].argmax(-1), w.argmax(-1))
+        tol = 3e-2 * max(1.0, w.abs().max().item())
+        assert (got[b] - w).abs().max().item() < tol
+        # the greedy token: the same as the reference's, or one whose reference logit is within the
+        # tolerance of the reference's best (bf16 rounding of the attention output can flip a near-tie)
+        pick = got[b].argmax(-1, keepdim=True)
+        gap = w.max(-1).values - w.gather(-1, pick).squeeze(-1)
+        assert bool((gap <= tol).all()), gap
 
 
 def test_round_scores_equal_eager_attention_probabilities():

@@ -53,6 +53,23 @@ def test_workspace_size():
     assert ws(_hip.WS_KEEP_MASK, 0, 10) == 0 and ws(7, 1, 10) == 0
 
 
+def test_paged_attention_workspace_size():
+    """The split workspace: [pairs][rows][chunks][D] partial outputs plus (max, sum), for the
+    matrix-core kernels (head dims 64 and 128) and the float32 path (other head dims up to 512).
+    The float32 path's rows per workgroup are the fewest power of two (up to 8) holding a pair's
+    N * G rows; its chunks aim at four workgroups per CU (256 CUs off a GPU) in 256-token tiles."""
+    ws = _hip.lib().actkv_paged_attention_workspace_size
+    # head dim 256, 8 requests x 8192 tokens, one decode query of 16/8 heads: 64 pairs x 2 rows,
+    # 16 chunks of 512 tokens
+    assert ws(1, 8, 1, 16, 8, 256, 512, 16) == 64 * 2 * 16 * (256 + 2) * 4
+    assert ws(1, 8, 1, 16, 8, 96, 512, 16) == 64 * 2 * 16 * (96 + 2) * 4
+    assert ws(1, 8, 1, 16, 8, 513, 512, 16) == 0            # past the largest head dim
+    assert ws(1, 1, 1, 32, 8, 128, 2048, 16) > 0            # matrix-core decode split
+    assert ws(1, 1, 1, 32, 8, 64, 2048, 16) > 0
+    assert ws(1, 8, 1, 16, 7, 256, 512, 16) == 0            # Hq not a multiple of Hkv
+    assert ws(1, 1, 1, 16, 8, 256, 1, 16) == 0              # one block: nothing to split
+
+
 @pytest.mark.skipif(_hip.torch.cuda.is_available(),
                     reason="passes unmapped pointers that validation must reject; kept off GPU machines")
 def test_invalid_arguments_are_rejected_before_any_launch():

@@ -174,9 +174,22 @@ __global__ void __launch_bounds__(256) score_generic_kernel(ScoreArgs a) {
 // chunk's ROWS dot products in registers: K is read once per ROWS rows instead of once
 // per row, and the dot products are independent FMA chains.  Each dot product still
 // sums its dims in order, so the scores equal score_generic_kernel's.
+// Packed two-element dot products (v_dot2c_f32_bf16 / _f16: a.x * b.x + a.y * b.y + c in
+// float32) when q and K share a 16-bit dtype: the query rows sit in LDS as dim pairs.
+__device__ __forceinline__ float dot2_acc(uint32_t k, uint32_t q, float c, __bf16) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, k), __builtin_bit_cast(bf2, q), c, false);
+}
+__device__ __forceinline__ float dot2_acc(uint32_t k, uint32_t q, float c, _Float16) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, k), __builtin_bit_cast(h2, q), c, false);
+}
+
 template <typename QT, typename KT, int ROWS>
 __global__ void __launch_bounds__(256) score_generic_rows_kernel(ScoreArgs a, int gc) {
-  extern __shared__ __attribute__((aligned(16))) float qrows[];  // [ROWS][D] fp32, [ROWS] lse, [ROWS] kv_len
+  // [ROWS][D] fp32 query rows (packed: [ROWS][D/2] dim pairs), then [ROWS] lse, [ROWS] kv_len
+  extern __shared__ __attribute__((aligned(16))) float qrows[];
+  constexpr bool PACK = __is_same(QT, KT) && (__is_same(KT, __bf16) || __is_same(KT, _Float16));
   const int pair = blockIdx.y;
   const int h = pair % a.Hkv;
   const int r = (pair / a.Hkv) % a.R;
@@ -215,11 +228,25 @@ __global__ void __launch_bounds__(256) score_generic_rows_kernel(ScoreArgs a, in
       const int gn = min(gc, G - g0);
       const bool last = g0 + gc >= G;
       __syncthreads();
-      for (int i = threadIdx.x; i < ROWS * D; i += 256) {
-        const int row = i / D, d = i % D, j = row / gc, g = row % gc;
-        qrows[i] = j < qn && g < gn
-                       ? (float)qbase[(int64_t)(nc + j) * a.q_sn + (int64_t)(h * G + g0 + g) * a.q_sh + d]
-                       : 0.f;
+      if constexpr (PACK) {
+        uint32_t *qp = (uint32_t *)qrows;
+        const int D2 = D / 2;
+        for (int i = threadIdx.x; i < ROWS * D2; i += 256) {
+          const int row = i / D2, d = 2 * (i % D2), j = row / gc, g = row % gc;
+          uint32_t v = 0;
+          if (j < qn && g < gn) {
+            const QT *src = qbase + (int64_t)(nc + j) * a.q_sn + (int64_t)(h * G + g0 + g) * a.q_sh + d;
+            v = (uint32_t)__builtin_bit_cast(uint16_t, src[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, src[1]) << 16);
+          }
+          qp[i] = v;
+        }
+      } else {
+        for (int i = threadIdx.x; i < ROWS * D; i += 256) {
+          const int row = i / D, d = i % D, j = row / gc, g = row % gc;
+          qrows[i] = j < qn && g < gn
+                         ? (float)qbase[(int64_t)(nc + j) * a.q_sn + (int64_t)(h * G + g0 + g) * a.q_sh + d]
+                         : 0.f;
+        }
       }
       if (threadIdx.x < ROWS) {
         const int row = threadIdx.x, j = row / gc, g = row % gc;
@@ -231,15 +258,32 @@ __global__ void __launch_bounds__(256) score_generic_rows_kernel(ScoreArgs a, in
       float dot[ROWS];
 #pragma unroll
       for (int i = 0; i < ROWS; ++i) dot[i] = 0.f;
-      for (int d = 0; d < D; d += 4) {
-        const float k0 = (float)krow[d], k1 = (float)krow[d + 1], k2 = (float)krow[d + 2], k3 = (float)krow[d + 3];
+      if constexpr (PACK) {
+        const uint32_t *qp = (const uint32_t *)qrows;
+        const int D2 = D / 2;
+        for (int d = 0; d < D; d += 4) {
+          const uint32_t k01 = (uint32_t)__builtin_bit_cast(uint16_t, krow[d]) |
+                               ((uint32_t)__builtin_bit_cast(uint16_t, krow[d + 1]) << 16);
+          const uint32_t k23 = (uint32_t)__builtin_bit_cast(uint16_t, krow[d + 2]) |
+                               ((uint32_t)__builtin_bit_cast(uint16_t, krow[d + 3]) << 16);
 #pragma unroll
-        for (int i = 0; i < ROWS; ++i) {
-          const float4 qv = *(const float4 *)&qrows[i * D + d];
-          dot[i] = fmaf(k0, qv.x, dot[i]);
-          dot[i] = fmaf(k1, qv.y, dot[i]);
-          dot[i] = fmaf(k2, qv.z, dot[i]);
-          dot[i] = fmaf(k3, qv.w, dot[i]);
+          for (int i = 0; i < ROWS; ++i) {
+            const uint2 qv = *(const uint2 *)&qp[i * D2 + d / 2];
+            dot[i] = dot2_acc(k01, qv.x, dot[i], KT{});
+            dot[i] = dot2_acc(k23, qv.y, dot[i], KT{});
+          }
+        }
+      } else {
+        for (int d = 0; d < D; d += 4) {
+          const float k0 = (float)krow[d], k1 = (float)krow[d + 1], k2 = (float)krow[d + 2], k3 = (float)krow[d + 3];
+#pragma unroll
+          for (int i = 0; i < ROWS; ++i) {
+            const float4 qv = *(const float4 *)&qrows[i * D + d];
+            dot[i] = fmaf(k0, qv.x, dot[i]);
+            dot[i] = fmaf(k1, qv.y, dot[i]);
+            dot[i] = fmaf(k2, qv.z, dot[i]);
+            dot[i] = fmaf(k3, qv.w, dot[i]);
+          }
         }
       }
       // rows in (query, head) order: the group max, then each whole query folds in turn

@@ -899,9 +899,10 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a, int pairs
 // head) pair -- a decode step's whole GQA group of up to 8 heads, so K and V are read once
 // for all of its rows -- over one token chunk, 256 tokens at a time:
 //   thread j: s_i = q_i . k_(t0+j) for each row i (the rows from LDS, the dot products in
-//   registers as independent FMA chains), the tile's max per row through wave reductions and
-//   LDS, p_i,j into LDS; then thread d: O_i[d] += sum_j p_i,j v_(t0+j)[d] (V rows read
-//   coalesced) and l_i += sum_j p_i,j, the same sum in every thread.
+//   registers as independent FMA chains), the tile's max and sum of p per row through wave
+//   reductions and LDS, p_i,j into LDS; then O_i += sum_j p_i,j v_(t0+j) by token groups
+//   (ceil(D/8) threads per token, 8 dims each; the groups' partial O summed in order at the
+//   chunk's end).
 // Online softmax in log2 units, as the matrix-core kernels; a split sequence's chunks go
 // through the same workspace layout ([pair][row][chunk][D] and (max, sum)) and the combine
 // launch.  Tokens in blocks the table marks invalid, and tokens a row does not see, get

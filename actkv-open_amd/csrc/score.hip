@@ -172,10 +172,11 @@ __global__ void __launch_bounds__(256) score_generic_kernel(ScoreArgs a) {
 // than ROWS takes one query per chunk and several chunks of heads, the running max carried
 // between them).  A thread walks its K row once per chunk, four dims per step, and keeps the
 // chunk's ROWS dot products in registers: K is read once per ROWS rows instead of once
-// per row, and the dot products are independent FMA chains.  Each dot product still
-// sums its dims in order, so the scores equal score_generic_kernel's.
-// Packed two-element dot products (v_dot2c_f32_bf16 / _f16: a.x * b.x + a.y * b.y + c in
-// float32) when q and K share a 16-bit dtype: the query rows sit in LDS as dim pairs.
+// per row, and the dot products are independent FMA chains.  With a float32 cache or
+// queries each dot product still sums its dims in order, so the scores equal
+// score_generic_kernel's.  When q and K share a 16-bit dtype the query rows sit in LDS as
+// dim pairs and the products are packed two-element dots (v_dot2c_f32_bf16 / _f16:
+// a.x * b.x + a.y * b.y + c in float32), within 1e-6 relative of the in-order sums.
 __device__ __forceinline__ float dot2_acc(uint32_t k, uint32_t q, float c, __bf16) {
   typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, k), __builtin_bit_cast(bf2, q), c, false);

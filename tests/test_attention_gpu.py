@@ -96,6 +96,8 @@ def test_matrix_core_path_matches_the_oracle(lens, hq, hkv, n_q, dtype, causal):
     ([5000, 700], 8, 2, 48, torch.bfloat16, True, 256, True),    # chunk starts inside blocks
     ([4400, 1], 56, 8, 1, torch.bfloat16, False, 64, True),      # GQA 7 decode, a one-token request
     ([1800, 333], 24, 8, 30, torch.bfloat16, True, 16, True),    # GQA 3, 90 rows
+    ([1500, 300], 32, 2, 3, torch.bfloat16, True, 16, True),     # GQA 16, 48 rows: 2-wave ring
+    ([2000, 900], 64, 2, 1, torch.float16, False, 32, True),     # GQA 32 decode: one full tile
 ])
 def test_matrix_core_path_head_dim_64(monkeypatch, lens, hq, hkv, n_q, dtype, causal, bs, split):
     """Head dim 64 on the matrix-core kernels (128-byte token rows: eight rows per 16-byte
